@@ -1,0 +1,87 @@
+"""ctypes binding of ``libdropkv_amd.so`` (the C ABI in ``include/dropkv_amd.h``).
+
+The library is loaded from this package directory.  There is no fallback:
+if it is missing, every op raises ``RuntimeError`` telling how to build it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libdropkv_amd.so")
+
+DROPKV_BF16 = 1
+DROPKV_FP16 = 2
+
+_c_i64 = ctypes.c_int64
+_c_vp = ctypes.c_void_p
+_c_int = ctypes.c_int
+_c_size = ctypes.c_size_t
+_c_float = ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/dropkv_amd.h
+_SIGNATURES = {
+    "dropkv_version": (_c_int, []),
+    "dropkv_last_error": (ctypes.c_char_p, []),
+    "dropkv_supported_head_dims": (_c_int, [ctypes.POINTER(_c_i64), _c_int]),
+    "dropkv_scores_workspace_bytes": (_c_size, [_c_i64] * 7),
+    "dropkv_scores": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_int,
+                               _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                               _c_float, _c_int, _c_int, _c_i64, _c_vp, _c_vp, _c_size, _c_vp]),
+    "dropkv_scores_debug_state": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                           _c_vp, _c_vp, _c_vp]),
+    "dropkv_select_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
+    "dropkv_select": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_size,
+                               _c_vp]),
+    "dropkv_compact": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                _c_vp, _c_i64, _c_vp, _c_vp, _c_vp]),
+    "dropkv_compact2": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
+                                 _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
+                                 _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_vp]),
+    "dropkv_evict_workspace_bytes": (_c_size, [_c_i64] * 7),
+    "dropkv_evict": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_int,
+                              _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                              _c_float, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
+                              _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
+    "dropkv_selftest_mfma": (_c_int, [_c_vp, _c_vp]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load():
+    """Load and return the ctypes handle (raises RuntimeError if absent)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"DropKV HIP library not found at {LIB_PATH}; build it with "
+                    "`python -m dropkv_amd._build` (hipcc, gfx950)")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().dropkv_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def supported_head_dims() -> tuple[int, ...]:
+    buf = (_c_i64 * 16)()
+    n = load().dropkv_supported_head_dims(buf, 16)
+    return tuple(int(buf[i]) for i in range(min(n, 16)))

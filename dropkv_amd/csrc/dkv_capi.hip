@@ -1,0 +1,214 @@
+// extern "C" entry points of libdropkv_amd.so (declared in include/dropkv_amd.h).
+// Argument validation happens here, before anything is enqueued.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/dropkv_amd.h"
+#include "dkv_internal.h"
+
+
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return DROPKV_OK;
+  return fail(DROPKV_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int64_t kHeadDims[] = {64, 128};
+constexpr int64_t kMaxLk = (int64_t)1 << 30;
+
+bool head_dim_supported(int64_t D) {
+  for (int64_t d : kHeadDims)
+    if (d == D) return true;
+  return false;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_score_args(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                     int64_t Lq, int64_t Lk, int64_t D, int64_t W) {
+  if (!q || !k || !v) return fail(DROPKV_E_ARG, "null q/k/v pointer");
+  if (dtype != DROPKV_BF16 && dtype != DROPKV_FP16) return fail(DROPKV_E_ARG, "dtype must be bf16 or fp16");
+  if (B < 1 || Hq < 1 || Hkv < 1) return fail(DROPKV_E_ARG, "B, Hq, Hkv must be positive");
+  if (Hq % Hkv != 0) return fail(DROPKV_E_ARG, "Hq (%lld) must be divisible by Hkv (%lld)", (long long)Hq,
+                                 (long long)Hkv);
+  if (W < 1) return fail(DROPKV_E_ARG, "window must be positive");
+  if (Lq < W) return fail(DROPKV_E_ARG, "Lq (%lld) must be >= window_size (%lld)", (long long)Lq, (long long)W);
+  if (Lk < W) return fail(DROPKV_E_ARG, "Lk (%lld) must be >= window_size (%lld)", (long long)Lk, (long long)W);
+  if (Lq > Lk) return fail(DROPKV_E_ARG, "Lq (%lld) must be <= Lk (%lld)", (long long)Lq, (long long)Lk);
+  if (Lk > kMaxLk) return fail(DROPKV_E_UNSUPPORTED, "Lk (%lld) too large", (long long)Lk);
+  if (!head_dim_supported(D)) return fail(DROPKV_E_UNSUPPORTED, "head dim %lld not supported", (long long)D);
+  if (!aligned16(k) || !aligned16(v)) return fail(DROPKV_E_ARG, "k and v must be 16-byte aligned");
+  if ((int64_t)(Hq / Hkv) * W > 4096) return fail(DROPKV_E_UNSUPPORTED, "g*window above 4096");
+  return DROPKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dropkv_version(void) { return 100; }
+
+const char* dropkv_last_error(void) { return g_err.c_str(); }
+
+int dropkv_supported_head_dims(int64_t* out, int cap) {
+  const int n = (int)(sizeof(kHeadDims) / sizeof(kHeadDims[0]));
+  for (int i = 0; i < n && i < cap; ++i) out[i] = kHeadDims[i];
+  return n;
+}
+
+size_t dropkv_scores_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W,
+                                     int64_t splits) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || W < 1 || Lk < 1 || D < 1) return 0;
+  return dkv::make_score_plan(B, Hq, Hkv, Lk, D, W, splits).total;
+}
+
+int dropkv_scores(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const void* k,
+                  const void* v, int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D,
+                  int64_t W, float eps, int p_round, int y_round, int64_t splits, float* scores, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  int rc = check_score_args(q, k, v, dtype, B, Hq, Hkv, Lq, Lk, D, W);
+  if (rc) return rc;
+  if (!scores) return fail(DROPKV_E_ARG, "null scores pointer");
+  const dkv::ScorePlan p = dkv::make_score_plan(B, Hq, Hkv, Lk, D, W, splits);
+  if (!workspace || workspace_bytes < p.total)
+    return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", p.total, workspace_bytes);
+  return hip_status(dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Hkv,
+                                       (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, scores,
+                                       static_cast<char*>(workspace), static_cast<hipStream_t>(stream)),
+                    "dropkv_scores launch");
+}
+
+int dropkv_scores_debug_state(const void* workspace, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D,
+                              int64_t W, int64_t splits, float* lse_out, float* y_out, void* stream) {
+  if (!workspace || !lse_out || !y_out) return fail(DROPKV_E_ARG, "null pointer");
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || W < 1 || Lk < W || !head_dim_supported(D))
+    return fail(DROPKV_E_ARG, "invalid shape");
+  const dkv::ScorePlan p = dkv::make_score_plan(B, Hq, Hkv, Lk, D, W, splits);
+  return hip_status(dkv::launch_debug_state(p, static_cast<const char*>(workspace), (int)D, lse_out, y_out,
+                                            static_cast<hipStream_t>(stream)),
+                    "dropkv_scores_debug_state launch");
+}
+
+size_t dropkv_select_workspace_bytes(int64_t rows, int64_t Lk) {
+  if (rows < 1 || Lk < 1) return 0;
+  return dkv::select_workspace_bytes(rows, Lk);
+}
+
+static int check_select_args(const float* scores, int64_t rows, int64_t Lk, int64_t ks, int64_t window,
+                             int64_t keep, const int64_t* keep_idx) {
+  if (!scores || !keep_idx) return fail(DROPKV_E_ARG, "null scores/keep_idx pointer");
+  if (rows < 1 || Lk < 1) return fail(DROPKV_E_ARG, "rows and Lk must be positive");
+  if (rows > 65535 * 64) return fail(DROPKV_E_UNSUPPORTED, "too many rows");
+  if (Lk > kMaxLk) return fail(DROPKV_E_UNSUPPORTED, "Lk (%lld) too large", (long long)Lk);
+  if (ks < 1 || ks % 2 == 0) return fail(DROPKV_E_ARG, "kernel_size must be a positive odd integer");
+  if (window < 0 || window > Lk) return fail(DROPKV_E_ARG, "window must be in [0, Lk]");
+  if (keep < 1 || keep > Lk) return fail(DROPKV_E_ARG, "keep (%lld) must be in [1, Lk=%lld]", (long long)keep,
+                                         (long long)Lk);
+  return DROPKV_OK;
+}
+
+int dropkv_select(const float* scores, int64_t rows, int64_t Lk, int64_t kernel_size, int64_t window, int64_t keep,
+                  int64_t* keep_idx, float* pooled, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_select_args(scores, rows, Lk, kernel_size, window, keep, keep_idx);
+  if (rc) return rc;
+  const size_t need = dkv::select_workspace_bytes(rows, Lk);
+  if (!workspace || workspace_bytes < need)
+    return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+  return hip_status(dkv::launch_select(scores, (int)rows, (int)Lk, (int)kernel_size, (int)window, (int)keep, keep_idx,
+                                       pooled, static_cast<char*>(workspace), static_cast<hipStream_t>(stream)),
+                    "dropkv_select launch");
+}
+
+static int check_compact_common(const int64_t* idx, int64_t eb, int64_t B, int64_t H, int64_t D, int64_t keep,
+                                const void* ko, const void* vo) {
+  if (!idx || !ko || !vo) return fail(DROPKV_E_ARG, "null idx/output pointer");
+  if (eb != 1 && eb != 2 && eb != 4 && eb != 8) return fail(DROPKV_E_ARG, "elem_bytes must be 1, 2, 4 or 8");
+  if (B < 0 || H < 0 || D < 1 || keep < 0) return fail(DROPKV_E_ARG, "invalid shape");
+  if (keep > kMaxLk) return fail(DROPKV_E_UNSUPPORTED, "keep too large");
+  return DROPKV_OK;
+}
+
+int dropkv_compact(const void* k, const void* v, int64_t s_b, int64_t s_h, int64_t s_l, int64_t elem_bytes,
+                   int64_t B, int64_t H, int64_t L, int64_t D, const int64_t* idx, int64_t keep, void* k_out,
+                   void* v_out, void* stream) {
+  int rc = check_compact_common(idx, elem_bytes, B, H, D, keep, k_out, v_out);
+  if (rc) return rc;
+  if (!k || !v) return fail(DROPKV_E_ARG, "null k/v pointer");
+  return hip_status(dkv::launch_compact(k, v, s_b, s_h, s_l, L, nullptr, nullptr, 0, 0, 0, 0, elem_bytes, B, H, D,
+                                        idx, keep, k_out, v_out, static_cast<hipStream_t>(stream)),
+                    "dropkv_compact launch");
+}
+
+int dropkv_compact2(const void* k0, const void* v0, int64_t s0_b, int64_t s0_h, int64_t s0_l, int64_t L0,
+                    const void* k1, const void* v1, int64_t s1_b, int64_t s1_h, int64_t s1_l, int64_t L1,
+                    int64_t elem_bytes, int64_t B, int64_t H, int64_t D, const int64_t* idx, int64_t keep,
+                    void* k_out, void* v_out, void* stream) {
+  int rc = check_compact_common(idx, elem_bytes, B, H, D, keep, k_out, v_out);
+  if (rc) return rc;
+  if ((L0 > 0 && (!k0 || !v0)) || (L1 > 0 && (!k1 || !v1))) return fail(DROPKV_E_ARG, "null segment pointer");
+  if (L0 < 0 || L1 < 0) return fail(DROPKV_E_ARG, "segment lengths must be >= 0");
+  return hip_status(dkv::launch_compact(k0, v0, s0_b, s0_h, s0_l, L0, k1, v1, s1_b, s1_h, s1_l, L1, elem_bytes, B, H,
+                                        D, idx, keep, k_out, v_out, static_cast<hipStream_t>(stream)),
+                    "dropkv_compact2 launch");
+}
+
+size_t dropkv_evict_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W,
+                                    int64_t splits) {
+  const size_t a = dropkv_scores_workspace_bytes(B, Hq, Hkv, Lk, D, W, splits);
+  if (!a) return 0;
+  const size_t s = ((size_t)B * Hkv * Lk * 4 + 255) & ~size_t(255);
+  return a + s + dkv::select_workspace_bytes(B * Hkv, Lk);
+}
+
+int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const void* k, const void* v,
+                 int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D, int64_t W,
+                 float eps, int p_round, int y_round, int64_t splits, int64_t kernel_size, int64_t protect_window,
+                 int64_t keep, float* scores, int64_t* keep_idx, void* k_out, void* v_out, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  int rc = check_score_args(q, k, v, dtype, B, Hq, Hkv, Lq, Lk, D, W);
+  if (rc) return rc;
+  rc = check_select_args(reinterpret_cast<const float*>(1), B * Hkv, Lk, kernel_size, protect_window, keep, keep_idx);
+  if (rc) return rc;
+  if (!k_out || !v_out) return fail(DROPKV_E_ARG, "null k_out/v_out pointer");
+  const dkv::ScorePlan p = dkv::make_score_plan(B, Hq, Hkv, Lk, D, W, splits);
+  const size_t s_bytes = ((size_t)B * Hkv * Lk * 4 + 255) & ~size_t(255);
+  const size_t need = p.total + s_bytes + dkv::select_workspace_bytes(B * Hkv, Lk);
+  if (!workspace || workspace_bytes < need)
+    return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+  char* ws = static_cast<char*>(workspace);
+  float* sc = scores ? scores : reinterpret_cast<float*>(ws + p.total);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Hkv,
+                                    (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws, st);
+  if (e != hipSuccess) return hip_status(e, "dropkv_evict scores");
+  e = dkv::launch_select(sc, (int)(B * Hkv), (int)Lk, (int)kernel_size, (int)protect_window, (int)keep, keep_idx,
+                         nullptr, ws + p.total + s_bytes, st);
+  if (e != hipSuccess) return hip_status(e, "dropkv_evict select");
+  e = dkv::launch_compact(k, v, Hkv * Lk * D, Lk * D, D, Lk, nullptr, nullptr, 0, 0, 0, 0, 2, B, Hkv, D, keep_idx,
+                          keep, k_out, v_out, st);
+  return hip_status(e, "dropkv_evict compact");
+}
+
+int dropkv_selftest_mfma(float* out, void* stream) {
+  if (!out) return fail(DROPKV_E_ARG, "null out");
+  return hip_status(dkv::launch_mfma_selftest(out, static_cast<hipStream_t>(stream)), "selftest launch");
+}
+
+}  // extern "C"

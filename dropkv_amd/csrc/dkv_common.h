@@ -1,0 +1,80 @@
+// Shared device-side definitions for the DropKV gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dkv {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Element traits: the bf16 / fp16 operand vector (8 elements = 16 bytes =
+// one lane's share of a 16x16x32 MFMA operand) and the matching MFMA.
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<__bf16> {
+  typedef __bf16 v8 __attribute__((__vector_size__(16)));
+  static __device__ __forceinline__ f32x4 mfma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Elem<_Float16> {
+  typedef _Float16 v8 __attribute__((__vector_size__(16)));
+  static __device__ __forceinline__ f32x4 mfma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Round-to-nearest-even through the element type and back.
+template <typename T>
+__device__ __forceinline__ float round_through(float x) {
+  return static_cast<float>(static_cast<T>(x));
+}
+
+template <typename V>
+__device__ __forceinline__ V bitcast_u4(u32x4 x) {
+  return __builtin_bit_cast(V, x);
+}
+
+// Order-preserving map float -> uint32 (larger float => larger key).
+// -0.0 is folded onto +0.0 so that the two compare equal, as in torch.
+__device__ __forceinline__ uint32_t float_key(float f) {
+  uint32_t b = __float_as_uint(f);
+  if (b == 0x80000000u) b = 0u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_float(uint32_t k) {
+  uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(b);
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8).
+// Remap so that consecutive logical ids land on the same XCD (and so share
+// its L2) while keeping the dispatch order.  Bijective on [0, n).
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  const int q = n >> 3, r = n & 7;
+  const int xcd = bid & 7, slot = bid >> 3;
+  const int base = xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q;
+  return base + slot;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+}  // namespace dkv

@@ -1,0 +1,88 @@
+// Gather-compaction of the retained keys/values (DropKVCache._gather_compressed,
+// dropkv_cache.py:479-491) and its two-segment form for the chunked-prefill
+// continuation (dropkv_cache.py:581-607).  Bit copies in 16-byte pieces when
+// the row allows it, element copies otherwise.  Indices outside [0, L) are
+// not dereferenced; their output rows are zero-filled.
+#include "dkv_common.h"
+#include "dkv_internal.h"
+
+namespace dkv {
+
+constexpr int kCopyThreads = 256;
+constexpr int kRowsPerBlock = 64;
+
+struct Seg {
+  const uint8_t* k;
+  const uint8_t* v;
+  int64_t sb, sh, sl;  // byte strides
+  int64_t len;
+};
+
+template <typename U>
+__global__ void __launch_bounds__(kCopyThreads)
+compact_kernel(Seg s0, Seg s1, int H, int units_per_row, const int64_t* __restrict__ idx, int keep,
+               int blocks_per_head, uint8_t* __restrict__ ko, uint8_t* __restrict__ vo) {
+  const int bh = blockIdx.x / blocks_per_head;
+  const int r0 = (blockIdx.x % blocks_per_head) * kRowsPerBlock;
+  const int b = bh / H, h = bh % H;
+  const int64_t out_row_bytes = (int64_t)units_per_row * sizeof(U);
+  const int total = kRowsPerBlock * units_per_row;
+  for (int t = threadIdx.x; t < total; t += kCopyThreads) {
+    const int r = r0 + t / units_per_row;
+    const int u = t % units_per_row;
+    if (r >= keep) break;
+    const int64_t src = idx[(int64_t)bh * keep + r];
+    U kval, vval;
+    if (src >= 0 && src < s0.len) {
+      const int64_t off = b * s0.sb + h * s0.sh + src * s0.sl;
+      kval = reinterpret_cast<const U*>(s0.k + off)[u];
+      vval = reinterpret_cast<const U*>(s0.v + off)[u];
+    } else if (src >= s0.len && src < s0.len + s1.len) {
+      const int64_t off = b * s1.sb + h * s1.sh + (src - s0.len) * s1.sl;
+      kval = reinterpret_cast<const U*>(s1.k + off)[u];
+      vval = reinterpret_cast<const U*>(s1.v + off)[u];
+    } else {
+      kval = U{};
+      vval = U{};
+    }
+    const int64_t o = ((int64_t)bh * keep + r) * out_row_bytes;
+    reinterpret_cast<U*>(ko + o)[u] = kval;
+    reinterpret_cast<U*>(vo + o)[u] = vval;
+  }
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+hipError_t launch_compact(const void* k0, const void* v0, int64_t s0b, int64_t s0h, int64_t s0l, int64_t L0,
+                          const void* k1, const void* v1, int64_t s1b, int64_t s1h, int64_t s1l, int64_t L1,
+                          int64_t eb, int64_t B, int64_t H, int64_t D, const int64_t* idx, int64_t keep, void* ko,
+                          void* vo, hipStream_t st) {
+  if (keep <= 0 || B * H == 0) return hipSuccess;
+  Seg a{static_cast<const uint8_t*>(k0), static_cast<const uint8_t*>(v0), s0b * eb, s0h * eb, s0l * eb, L0};
+  Seg c{static_cast<const uint8_t*>(k1), static_cast<const uint8_t*>(v1), s1b * eb, s1h * eb, s1l * eb, L1};
+  const int64_t row_bytes = D * eb;
+  bool vec = (row_bytes % 16) == 0 && aligned16(ko) && aligned16(vo);
+  auto seg_ok = [&](const Seg& s, const void* kp, const void* vp) {
+    if (s.len == 0) return true;
+    return aligned16(kp) && aligned16(vp) && (s.sb % 16) == 0 && (s.sh % 16) == 0 && (s.sl % 16) == 0;
+  };
+  vec = vec && seg_ok(a, k0, v0) && seg_ok(c, k1, v1);
+  const int bph = (int)((keep + kRowsPerBlock - 1) / kRowsPerBlock);
+  const dim3 grid((unsigned)(B * H * bph));
+  if (vec) {
+    hipLaunchKernelGGL(compact_kernel<uint4>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)(row_bytes / 16),
+                       idx, (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
+  } else if (eb == 2) {
+    hipLaunchKernelGGL(compact_kernel<uint16_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)D, idx,
+                       (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
+  } else if (eb == 4) {
+    hipLaunchKernelGGL(compact_kernel<uint32_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)D, idx,
+                       (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
+  } else {
+    hipLaunchKernelGGL(compact_kernel<uint8_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)row_bytes, idx,
+                       (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
+  }
+  return hipGetLastError();
+}
+
+}  // namespace dkv

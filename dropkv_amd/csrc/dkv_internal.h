@@ -1,0 +1,35 @@
+// Host-side interfaces between the kernel translation units and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace dkv {
+
+// Launch geometry and workspace layout of one scoring call.
+struct ScorePlan {
+  int heads, g, M, n_mc, mpad;
+  int s1, kps1;  // pass 1: splits per (head, row-chunk), keys per split
+  int s2, kps2;  // pass 2: splits per head, keys per split
+  size_t off_ml, off_y, off_yhl, off_stat, off_yf, total;
+};
+
+ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W, int64_t splits);
+hipError_t launch_scores(const ScorePlan& p, int dtype_bf16, int D, const void* q, int64_t q_sb, int64_t q_sh,
+                         int64_t q_ss, int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk, int W,
+                         float eps, int p_round, int y_round, float* scores, char* ws, hipStream_t st);
+hipError_t launch_debug_state(const ScorePlan& p, const char* ws, int D, float* lse_out, float* y_out,
+                              hipStream_t st);
+hipError_t launch_mfma_selftest(float* out, hipStream_t st);
+
+size_t select_workspace_bytes(int64_t rows, int64_t Lk);
+hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int window, int keep, int64_t* out_idx,
+                         float* pooled_out, char* ws, hipStream_t st);
+
+hipError_t launch_compact(const void* k0, const void* v0, int64_t s0b, int64_t s0h, int64_t s0l, int64_t L0,
+                          const void* k1, const void* v1, int64_t s1b, int64_t s1h, int64_t s1l, int64_t L1,
+                          int64_t eb, int64_t B, int64_t H, int64_t D, const int64_t* idx, int64_t keep, void* ko,
+                          void* vo, hipStream_t st);
+
+}  // namespace dkv

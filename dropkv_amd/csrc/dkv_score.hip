@@ -1,0 +1,635 @@
+// DropKV scoring on gfx950: split-K flash partials, cross-split merge and the
+// per-key residual-output perturbation score.
+//
+// Math (one KV head; g = Hq/Hkv query heads, W window rows each, M = g*W):
+//   row m = gi*W + w is query head hkv*g+gi at position Lq-W+w, aligned to key
+//   position Lk-W+w (dropkv_triton.py:225-231);  l[m,j] = q_m.k_j/sqrt(D) for
+//   j <= Lk-W+w;  p = softmax_j(l);  y_m = sum_j p[m,j] v_j;
+//   w = (p/(1-p+eps))^2;  score_j = (1/g) sum_m w[m,j] * max(|v_j|^2 - 2<y_m,v_j> + |y_m|^2, 0)
+//   (dropkv_triton.py:29-109 and :574-606).
+//
+// Matrix-core mapping (v_mfma_f32_16x16x32_{bf16,f16}, wave64):
+//   operand A[i][k] lives in lane i + 16*g, element e, where (g, e) names the
+//   contraction slot; operand B[k][j] likewise in lane j + 16*g; the result
+//   C[i][j] lives in lane j + 16*(i/4), element i%4.  Any bijection between
+//   contraction slots and the real contraction index works as long as A and B
+//   use the same one, which the kernels exploit to keep P in registers.
+//   * logits are computed transposed, S^T = K Q^T: a lane then holds one query
+//     row m = lane%16 for keys 4*(lane/16)+r, so row max / row sum are mostly
+//     lane-local;
+//   * Y^T = V^T P^T: B = P^T comes straight from the S^T registers; A = V^T
+//     comes from a per-wave LDS tile written transposed (V rows are contiguous
+//     along D in HBM, but the contraction here runs along keys).
+#include "dkv_common.h"
+#include "dkv_internal.h"
+
+namespace dkv {
+
+constexpr int kWaves = 4;           // waves per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTile = 32;           // keys per wave tile
+constexpr int kRows = 32;           // query rows per row-chunk (2 MFMA row blocks)
+constexpr int kMB = kRows / 16;
+constexpr int kPitch = 18;          // dwords per row of the transposed V tile
+
+
+__device__ __forceinline__ int row_bound(int m, int M, int W, int Lk) {
+  return m < M ? Lk - W + (m % W) : -1;
+}
+
+// One lane's Q^T operand: 8 consecutive head-dim values from column d0 of
+// query row m (zeros for padding rows).  Q may have any strides.
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::v8 load_q_op(const T* __restrict__ q, int64_t q_sb, int64_t q_sh,
+                                                        int64_t q_ss, int64_t q_sd, int b, int hkv, int g, int W,
+                                                        int Lq, int M, int m, int d0) {
+  typename Elem<T>::v8 x;
+  const bool valid = m < M;
+  const int gi = valid ? m / W : 0;
+  const int w = valid ? m % W : 0;
+  const T* base = q + (int64_t)b * q_sb + (int64_t)(hkv * g + gi) * q_sh + (int64_t)(Lq - W + w) * q_ss;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = valid ? base[(int64_t)(d0 + e) * q_sd] : static_cast<T>(0.0f);
+  return x;
+}
+
+// Load the Q^T operands of one 16-row block (lane row m, lane group lg).
+template <typename T, int D>
+__device__ __forceinline__ void load_q_ops(typename Elem<T>::v8 (&qop)[D / 32], const T* __restrict__ q,
+                                           int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
+                                           int b, int hkv, int g, int W, int Lq, int M, int m, int lg) {
+  typedef typename Elem<T>::v8 v8;
+  const bool valid = m < M;
+  const int gi = valid ? m / W : 0;
+  const int w = valid ? m % W : 0;
+  const T* base = q + (int64_t)b * q_sb + (int64_t)(hkv * g + gi) * q_sh + (int64_t)(Lq - W + w) * q_ss;
+#pragma unroll
+  for (int kk = 0; kk < D / 32; ++kk) {
+    v8 x;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = 32 * kk + 8 * lg + e;
+      x[e] = valid ? base[(int64_t)d * q_sd] : static_cast<T>(0.0f);
+    }
+    qop[kk] = x;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1: split-K flash partials.  Workgroup = (head, row-chunk, key split);
+// each wave streams its own 32-key tiles; the four waves are merged in LDS at
+// the end.  Output per (head, chunk, split, row): running max (log2 domain),
+// running sum, and the unnormalised fp32 y row.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads, 2)
+pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
+             const T* __restrict__ kp, const T* __restrict__ vp,
+             int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int n_splits, int kps,
+             float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y) {
+  typedef typename Elem<T>::v8 v8;
+  constexpr int KK = D / 32;
+  constexpr int DT = D / 16;
+  constexpr int CPR = D / 8;           // 16-byte chunks per key row
+  constexpr int GRP = 64 / CPR;        // key pairs covered per load round
+  constexpr int NIT = (kTile / 2) / GRP;
+
+  __shared__ uint32_t lds[kWaves * D * kPitch];
+
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int mc = lid % n_mc;
+  const int split = (lid / n_mc) % n_splits;
+  const int head = lid / (n_mc * n_splits);
+  const int b = head / Hkv, hkv = head % Hkv;
+
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+
+  v8 qop[kMB][KK];
+  int bound[kMB];
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    const int m = mc * kRows + mb * 16 + li;
+    load_q_ops<T, D>(qop[mb], q, q_sb, q_sh, q_ss, q_sd, b, hkv, g, W, Lq, M, m, lg);
+    bound[mb] = row_bound(m, M, W, Lk);
+  }
+
+  const int64_t hoff = (int64_t)head * Lk * D;
+  const T* __restrict__ Kh = kp + hoff;
+  const T* __restrict__ Vh = vp + hoff;
+  uint32_t* vt = lds + wv * D * kPitch;
+
+  float m2[kMB], lsum[kMB];
+  f32x4 yacc[DT][kMB];
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    m2[mb] = -INFINITY;
+    lsum[mb] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int k_begin = split * kps;
+  const int k_end = min(k_begin + kps, Lk);
+
+  for (int t0 = k_begin + wv * kTile; t0 < k_end; t0 += kWaves * kTile) {
+    // K rows as the A operand: lane (li, lg) holds K[t0+16kb+li][32kk+8lg .. +7].
+    v8 kop[2][KK];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int n = min(t0 + 16 * kb + li, Lk - 1);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+        kop[kb][kk] = *reinterpret_cast<const v8*>(Kh + (int64_t)n * D + 32 * kk + 8 * lg);
+    }
+    // V rows in coalesced 16-byte chunks, two adjacent keys per lane.
+    u32x4 va[NIT], vb[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int p = it * GRP + lane / CPR;
+      const int c = lane % CPR;
+      const int n0 = min(t0 + 2 * p, Lk - 1), n1 = min(t0 + 2 * p + 1, Lk - 1);
+      va[it] = *reinterpret_cast<const u32x4*>(Vh + (int64_t)n0 * D + 8 * c);
+      vb[it] = *reinterpret_cast<const u32x4*>(Vh + (int64_t)n1 * D + 8 * c);
+    }
+
+    // S^T = K Q^T.
+    f32x4 s[2][kMB];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) acc = Elem<T>::mfma(kop[kb][kk], qop[mb][kk], acc);
+        s[kb][mb] = acc;
+      }
+
+    // Transposed V tile -> LDS: dword (d, pair p) = {V[2p][d], V[2p+1][d]}.
+    // The pair column is XOR-swizzled with bits 4-5 of d to spread banks.
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int p = it * GRP + lane / CPR;
+      const int c = lane % CPR;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t a = va[it][j], bb = vb[it][j];
+        const uint32_t lo = (a & 0xffffu) | (bb << 16);
+        const uint32_t hi = (a >> 16) | (bb & 0xffff0000u);
+        const int d0 = 8 * c + 2 * j, d1 = d0 + 1;
+        vt[d0 * kPitch + (p ^ (4 * ((d0 >> 4) & 3)))] = lo;
+        vt[d1 * kPitch + (p ^ (4 * ((d1 >> 4) & 3)))] = hi;
+      }
+    }
+
+    // Online softmax (base 2) for each row block; P hi/lo split for the MFMA.
+    v8 phi[kMB], plo[kMB];
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb) {
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n = t0 + 16 * kb + 4 * lg + r;
+          const float x = n <= bound[mb] ? s[kb][mb][r] * scale_log2 : -INFINITY;
+          s[kb][mb][r] = x;
+          tmax = fmaxf(tmax, x);
+        }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const float mnew = fmaxf(m2[mb], tmax);
+      const bool empty = mnew == -INFINITY;
+      const float alpha = empty ? 1.f : exp2f(m2[mb] - mnew);
+      float psum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pv = empty ? 0.f : exp2f(s[kb][mb][r] - mnew);
+          psum += pv;
+          const T h = static_cast<T>(pv);
+          phi[mb][4 * kb + r] = h;
+          plo[mb][4 * kb + r] = static_cast<T>(pv - static_cast<float>(h));
+        }
+      lsum[mb] = lsum[mb] * alpha + psum;
+      m2[mb] = mnew;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= alpha;
+    }
+
+    // Y^T += V^T P^T.  Lane (li, lg) reads V^T[16dt+li][keys 4lg..4lg+3, 16+4lg..+3].
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d = 16 * dt + li;
+      const int sw = 4 * (dt & 3);
+      const u32x2 x0 = *reinterpret_cast<const u32x2*>(vt + d * kPitch + ((2 * lg) ^ sw));
+      const u32x2 x1 = *reinterpret_cast<const u32x2*>(vt + d * kPitch + ((8 + 2 * lg) ^ sw));
+      const v8 aop = bitcast_u4<v8>(u32x4{x0[0], x0[1], x1[0], x1[1]});
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb) {
+        yacc[dt][mb] = Elem<T>::mfma(aop, phi[mb], yacc[dt][mb]);
+        yacc[dt][mb] = Elem<T>::mfma(aop, plo[mb], yacc[dt][mb]);
+      }
+    }
+  }
+
+  // Row sums are per lane-group partials; fold the four groups.
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    lsum[mb] += __shfl_xor(lsum[mb], 16);
+    lsum[mb] += __shfl_xor(lsum[mb], 32);
+  }
+
+  // Cross-wave merge in LDS (the V tiles are dead now).
+  __syncthreads();
+  float* sm_m = reinterpret_cast<float*>(lds);
+  float* sm_l = sm_m + kWaves * kRows;
+  float* ybuf = sm_l + kWaves * kRows;  // [kRows][D]
+  if (lg == 0) {
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb) {
+      sm_m[wv * kRows + 16 * mb + li] = m2[mb];
+      sm_l[wv * kRows + 16 * mb + li] = lsum[mb];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    const int row = 16 * mb + li;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, sm_m[w * kRows + row]);
+    const float f = (mx == -INFINITY) ? 0.f : exp2f(m2[mb] - mx);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= f;
+  }
+  for (int w = 0; w < kWaves; ++w) {
+    if (wv == w) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int idx = (16 * mb + li) * D + 16 * dt + 4 * lg + r;
+            ybuf[idx] = (w == 0 ? 0.f : ybuf[idx]) + yacc[dt][mb][r];
+          }
+    }
+    __syncthreads();
+  }
+
+  const int64_t slot = ((int64_t)head * n_mc + mc) * n_splits + split;
+  if (threadIdx.x < kRows) {
+    const int row = threadIdx.x;
+    float mx = -INFINITY;
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, sm_m[w * kRows + row]);
+    float l = 0.f;
+    if (mx != -INFINITY)
+      for (int w = 0; w < kWaves; ++w) l += sm_l[w * kRows + row] * exp2f(sm_m[w * kRows + row] - mx);
+    part_ml[(slot * kRows + row) * 2 + 0] = mx;
+    part_ml[(slot * kRows + row) * 2 + 1] = l;
+  }
+  float* py = part_y + slot * kRows * D;
+  for (int i = threadIdx.x; i < kRows * D; i += kThreads) py[i] = ybuf[i];
+}
+
+// ---------------------------------------------------------------------------
+// Merge: one workgroup per (head, padded row); thread d owns column d.
+// Writes y as (hi, lo) element pairs for the score pass, the row statistics
+// (lse in log2 units, |y|^2) and an fp32 copy of y for inspection.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ void __launch_bounds__(D)
+merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y, int n_mc, int n_splits,
+             int M, int y_round, T* __restrict__ yhl, float* __restrict__ ystat, float* __restrict__ yf32) {
+  const int mpad = n_mc * kRows;
+  const int head = blockIdx.x / mpad;
+  const int gr = blockIdx.x % mpad;
+  const int mc = gr / kRows, row = gr % kRows;
+  const int d = threadIdx.x;
+  const int64_t slot0 = ((int64_t)head * n_mc + mc) * n_splits;
+
+  float mx = -INFINITY;
+  for (int s = 0; s < n_splits; ++s) mx = fmaxf(mx, part_ml[((slot0 + s) * kRows + row) * 2]);
+  float l = 0.f, acc = 0.f;
+  if (mx != -INFINITY) {
+    for (int s = 0; s < n_splits; ++s) {
+      const float ms = part_ml[((slot0 + s) * kRows + row) * 2];
+      const float f = ms == -INFINITY ? 0.f : exp2f(ms - mx);
+      l += part_ml[((slot0 + s) * kRows + row) * 2 + 1] * f;
+      acc += part_y[((slot0 + s) * kRows + row) * D + d] * f;
+    }
+  }
+  const bool valid = gr < M && mx != -INFINITY;
+  float y = valid ? acc / l : 0.f;
+  T hi, lo;
+  if (y_round) {
+    hi = static_cast<T>(y);
+    y = static_cast<float>(hi);
+    lo = static_cast<T>(0.f);
+  } else {
+    hi = static_cast<T>(y);
+    lo = static_cast<T>(y - static_cast<float>(hi));
+  }
+  const int64_t rbase = (int64_t)head * mpad + gr;
+  yhl[(rbase * 2 + 0) * D + d] = hi;
+  yhl[(rbase * 2 + 1) * D + d] = lo;
+  yf32[rbase * D + d] = y;
+
+  __shared__ float red[D / 64];
+  float sq = wave_sum(y * y);
+  if ((d & 63) == 0) red[d >> 6] = sq;
+  __syncthreads();
+  if (d == 0) {
+    float tot = 0.f;
+    for (int i = 0; i < D / 64; ++i) tot += red[i];
+    ystat[rbase * 2 + 0] = valid ? mx + log2f(fmaxf(l, 1e-40f)) : INFINITY;
+    ystat[rbase * 2 + 1] = tot;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2: per-key score.  Workgroup = (head, key split); each wave streams 32
+// key tiles, recomputes S^T = K Q^T and G^T = V Y^T (Y as hi+lo), and folds
+// w * dist2 over all query rows.  The Q^T / Y^T operands of up to `cg`
+// row-chunks are staged in LDS in per-lane order (one conflict-free 16-byte
+// read per operand); more row-chunks than that are processed in groups, the
+// partial per-key sums being carried in the output array.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads, 2)
+pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
+             const T* __restrict__ kp, const T* __restrict__ vp,
+             int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int cg, int n_splits, int kps,
+             float scale_log2, float eps, int p_round,
+             const T* __restrict__ yhl, const float* __restrict__ ystat, float* __restrict__ scores) {
+  typedef typename Elem<T>::v8 v8;
+  constexpr int KK = D / 32;
+  constexpr int OPS = 3 * kMB * KK;  // operand slots per row-chunk (Q, Yhi, Ylo)
+  extern __shared__ u32x4 opnd[];    // [cg][OPS][64] then float stats [cg][kMB][2][16]
+  float* stat = reinterpret_cast<float*>(opnd + (size_t)cg * OPS * 64);
+
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int split = lid % n_splits;
+  const int head = lid / n_splits;
+  const int b = head / Hkv, hkv = head % Hkv;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int mpad = n_mc * kRows;
+
+  const int64_t hoff = (int64_t)head * Lk * D;
+  const T* __restrict__ Kh = kp + hoff;
+  const T* __restrict__ Vh = vp + hoff;
+  const float inv_g = 1.0f / static_cast<float>(g);
+  const int k_begin = split * kps;
+  const int k_end = min(k_begin + kps, Lk);
+
+  for (int c0 = 0; c0 < n_mc; c0 += cg) {
+    const int cn = min(cg, n_mc - c0);
+    const bool first = c0 == 0, last = c0 + cn >= n_mc;
+    __syncthreads();
+    for (int slot = wv; slot < cn * OPS; slot += kWaves) {
+      const int c = slot / OPS, o = slot % OPS;
+      const int which = o / (kMB * KK), mb = (o / KK) % kMB, kk = o % KK;
+      const int m = (c0 + c) * kRows + mb * 16 + li;
+      v8 val;
+      if (which == 0) {
+        val = load_q_op<T>(q, q_sb, q_sh, q_ss, q_sd, b, hkv, g, W, Lq, M, m, 32 * kk + 8 * lg);
+      } else {
+        const int64_t rbase = (int64_t)head * mpad + m;
+        val = *reinterpret_cast<const v8*>(yhl + (rbase * 2 + (which - 1)) * D + 32 * kk + 8 * lg);
+      }
+      opnd[(size_t)slot * 64 + lane] = __builtin_bit_cast(u32x4, val);
+    }
+    for (int t = threadIdx.x; t < cn * kMB * 16; t += kThreads) {
+      const int c = t / (kMB * 16), r = t % (kMB * 16);
+      const int64_t rbase = (int64_t)head * mpad + (c0 + c) * kRows + r;
+      stat[(c * kMB + r / 16) * 32 + (r % 16)] = ystat[rbase * 2 + 0];
+      stat[(c * kMB + r / 16) * 32 + 16 + (r % 16)] = ystat[rbase * 2 + 1];
+    }
+    __syncthreads();
+
+    for (int t0 = k_begin + wv * kTile; t0 < k_end; t0 += kWaves * kTile) {
+      // Keep the LDS operand reads inside the loop (hoisting them all out
+      // would need more registers than the kernel has).
+      asm volatile("" ::: "memory");
+      v8 kop[2][KK], vop[2][KK];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int n = min(t0 + 16 * kb + li, Lk - 1);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          kop[kb][kk] = *reinterpret_cast<const v8*>(Kh + (int64_t)n * D + 32 * kk + 8 * lg);
+          vop[kb][kk] = *reinterpret_cast<const v8*>(Vh + (int64_t)n * D + 32 * kk + 8 * lg);
+        }
+      }
+      // |v|^2 of key t0+16kb+li (fp32 from the exact operand values), then
+      // redistributed to the result layout (keys 16kb+4lg+r).
+      float vn2[2][4];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        float part = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = static_cast<float>(vop[kb][kk][e]);
+            part += x * x;
+          }
+        part += __shfl_xor(part, 16);
+        part += __shfl_xor(part, 32);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vn2[kb][r] = __shfl(part, 4 * lg + r);
+      }
+
+      float sc[2][4];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[kb][r] = 0.f;
+
+      for (int c = 0; c < cn; ++c) {
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb) {
+          const int m = (c0 + c) * kRows + mb * 16 + li;
+          const int bound = row_bound(m, M, W, Lk);
+          const float lse2 = stat[(c * kMB + mb) * 32 + li];
+          const float yn2 = stat[(c * kMB + mb) * 32 + 16 + li];
+          const u32x4* ob = opnd + (size_t)(c * OPS) * 64 + lane;
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, gacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+              const v8 qo = __builtin_bit_cast(v8, ob[(size_t)((0 * kMB + mb) * KK + kk) * 64]);
+              const v8 yh = __builtin_bit_cast(v8, ob[(size_t)((1 * kMB + mb) * KK + kk) * 64]);
+              const v8 yl = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
+              sacc = Elem<T>::mfma(kop[kb][kk], qo, sacc);
+              gacc = Elem<T>::mfma(vop[kb][kk], yh, gacc);
+              gacc = Elem<T>::mfma(vop[kb][kk], yl, gacc);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int n = t0 + 16 * kb + 4 * lg + r;
+              float p = n <= bound ? exp2f(sacc[r] * scale_log2 - lse2) : 0.f;
+              p = fminf(fmaxf(p, 0.f), 1.f);
+              if (p_round) p = round_through<T>(p);
+              const float ratio = p / (1.0f - p + eps);
+              const float dist2 = fmaxf(vn2[kb][r] - 2.0f * gacc[r] + yn2, 0.f);
+              sc[kb][r] += ratio * ratio * dist2;
+            }
+          }
+        }
+      }
+
+      // Sum over the 16 query rows held by lanes li = 0..15 as a
+      // reduce-scatter: afterwards lane li holds the total of key r = li/4
+      // (for li % 4 == 0), so each key is stored by one lane.
+      const bool h8 = li & 8, h4 = li & 4;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        float k0 = h8 ? sc[kb][2] : sc[kb][0];
+        float k1 = h8 ? sc[kb][3] : sc[kb][1];
+        k0 += __shfl_xor(h8 ? sc[kb][0] : sc[kb][2], 8);
+        k1 += __shfl_xor(h8 ? sc[kb][1] : sc[kb][3], 8);
+        float v = h4 ? k1 : k0;
+        v += __shfl_xor(h4 ? k0 : k1, 4);
+        v += __shfl_xor(v, 2);
+        v += __shfl_xor(v, 1);
+        const int n = t0 + 16 * kb + 4 * lg + (li >> 2);
+        if ((li & 3) == 0 && n < k_end) {
+          float* dst = scores + (int64_t)head * Lk + n;
+          if (!first) v += *dst;
+          *dst = last ? v * inv_g : v;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launch helpers (called from dkv_capi.hip).
+// ---------------------------------------------------------------------------
+
+
+static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W,
+                          int64_t splits) {
+  ScorePlan p;
+  p.heads = (int)(B * Hkv);
+  p.g = (int)(Hq / Hkv);
+  p.M = p.g * (int)W;
+  p.n_mc = ceil_div(p.M, kRows);
+  p.mpad = p.n_mc * kRows;
+  const int target = 512;  // two resident workgroups on each of 256 CUs
+  const int max_by_work = max(1, (int)(Lk / 256));
+  int s1 = splits > 0 ? (int)splits : ceil_div(target, (int64_t)p.heads * p.n_mc);
+  s1 = max(1, min(s1, max_by_work));
+  p.kps1 = ceil_div(ceil_div(Lk, s1), kTile) * kTile;
+  p.s1 = ceil_div(Lk, p.kps1);
+  int s2 = splits > 0 ? (int)splits : ceil_div(target, p.heads);
+  s2 = max(1, min(s2, max_by_work));
+  p.kps2 = ceil_div(ceil_div(Lk, s2), kTile) * kTile;
+  p.s2 = ceil_div(Lk, p.kps2);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off += (bytes + 255) & ~size_t(255);
+    return o;
+  };
+  const size_t slots = (size_t)p.heads * p.n_mc * p.s1;
+  p.off_ml = take(slots * kRows * 2 * sizeof(float));
+  p.off_y = take(slots * kRows * D * sizeof(float));
+  p.off_yhl = take((size_t)p.heads * p.mpad * 2 * D * 2);
+  p.off_stat = take((size_t)p.heads * p.mpad * 2 * sizeof(float));
+  p.off_yf = take((size_t)p.heads * p.mpad * D * sizeof(float));
+  p.total = off;
+  return p;
+}
+
+template <typename T, int D>
+static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
+                                  int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk, int W,
+                                  float eps, int p_round, int y_round, float* scores, char* ws,
+                                  hipStream_t st) {
+  const float scale_log2 = 1.4426950408889634f / sqrtf((float)D);
+  float* part_ml = reinterpret_cast<float*>(ws + p.off_ml);
+  float* part_y = reinterpret_cast<float*>(ws + p.off_y);
+  T* yhl = reinterpret_cast<T*>(ws + p.off_yhl);
+  float* ystat = reinterpret_cast<float*>(ws + p.off_stat);
+  float* yf = reinterpret_cast<float*>(ws + p.off_yf);
+  const T* qq = static_cast<const T*>(q);
+  const T* kk = static_cast<const T*>(k);
+  const T* vv = static_cast<const T*>(v);
+
+  hipLaunchKernelGGL((pass1_kernel<T, D>), dim3(p.heads * p.n_mc * p.s1), dim3(kThreads), 0, st, qq, q_sb, q_sh,
+                     q_ss, q_sd, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml,
+                     part_y);
+  hipLaunchKernelGGL((merge_kernel<T, D>), dim3(p.heads * p.mpad), dim3(D), 0, st, part_ml, part_y, p.n_mc,
+                     p.s1, p.M, y_round, yhl, ystat, yf);
+  const int cg = min(p.n_mc, 2);
+  const size_t lds2 = (size_t)cg * 3 * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
+  hipLaunchKernelGGL((pass2_kernel<T, D>), dim3(p.heads * p.s2), dim3(kThreads), lds2, st, qq, q_sb, q_sh, q_ss,
+                     q_sd, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round,
+                     yhl, ystat, scores);
+  return hipGetLastError();
+}
+
+hipError_t launch_scores(const ScorePlan& p, int dtype_bf16, int D, const void* q, int64_t q_sb, int64_t q_sh,
+                         int64_t q_ss, int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk,
+                         int W, float eps, int p_round, int y_round, float* scores, char* ws, hipStream_t st) {
+#define DKV_CASE(TT, DD)                                                                                     \
+  return launch_scores_t<TT, DD>(p, q, q_sb, q_sh, q_ss, q_sd, k, v, Hkv, Lq, Lk, W, eps, p_round, y_round, \
+                                 scores, ws, st)
+  if (dtype_bf16) {
+    if (D == 64) DKV_CASE(__bf16, 64);
+    if (D == 128) DKV_CASE(__bf16, 128);
+  } else {
+    if (D == 64) DKV_CASE(_Float16, 64);
+    if (D == 128) DKV_CASE(_Float16, 128);
+  }
+#undef DKV_CASE
+  return hipErrorInvalidValue;
+}
+
+// Debug: copy lse (natural log) and fp32 y for the valid rows out of the workspace.
+__global__ void debug_state_kernel(const float* __restrict__ ystat, const float* __restrict__ yf, int heads,
+                                   int mpad, int M, int D, float* __restrict__ lse_out, float* __restrict__ y_out) {
+  const int head = blockIdx.x / M, m = blockIdx.x % M;
+  const int64_t rbase = (int64_t)head * mpad + m;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) y_out[((int64_t)head * M + m) * D + d] = yf[rbase * D + d];
+  if (threadIdx.x == 0) lse_out[(int64_t)head * M + m] = ystat[rbase * 2] * 0.69314718055994531f;
+}
+
+hipError_t launch_debug_state(const ScorePlan& p, const char* ws, int D, float* lse_out, float* y_out,
+                              hipStream_t st) {
+  hipLaunchKernelGGL(debug_state_kernel, dim3(p.heads * p.M), dim3(64), 0, st,
+                     reinterpret_cast<const float*>(ws + p.off_stat), reinterpret_cast<const float*>(ws + p.off_yf),
+                     p.heads, p.mpad, p.M, D, lse_out, y_out);
+  return hipGetLastError();
+}
+
+// Matrix-core layout self-test: A[i][k] = i + k/32, B[k][j] = (k%4)-j/16 ... small exact integers.
+__global__ void mfma_selftest_kernel(float* out) {
+  typedef Elem<__bf16>::v8 v8;
+  const int lane = threadIdx.x;
+  const int li = lane & 15, lg = lane >> 4;
+  v8 a, bop;
+  for (int e = 0; e < 8; ++e) {
+    const int kidx = 8 * lg + e;
+    a[e] = static_cast<__bf16>((float)((li * 3 + kidx) % 7) - 3.0f);
+    bop[e] = static_cast<__bf16>((float)((li * 5 + 2 * kidx) % 5) - 2.0f);
+  }
+  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+  c = Elem<__bf16>::mfma(a, bop, c);
+  for (int r = 0; r < 4; ++r) out[(4 * lg + r) * 16 + li] = c[r];
+}
+
+hipError_t launch_mfma_selftest(float* out, hipStream_t st) {
+  hipLaunchKernelGGL(mfma_selftest_kernel, dim3(1), dim3(64), 0, st, out);
+  return hipGetLastError();
+}
+
+}  // namespace dkv

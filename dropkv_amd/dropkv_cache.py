@@ -1,0 +1,321 @@
+"""Drop-in for the reference's cache module (dropkv_cache.py), on gfx950.
+
+``DropKVCache`` and ``prefill_chunked`` keep the reference API, prefill modes,
+length bookkeeping and error types (dropkv_cache.py:310-807).  Scoring,
+pooling, top-k, sorting and gathering run in the HIP kernels of
+libdropkv_amd.so:
+
+* fast path (``use_triton=True`` and the scoring guards pass):
+  :func:`dropkv_amd.dropkv_triton.dropkv_scores_triton`;
+* otherwise the reference's deployed scoring semantics
+  (dropkv_cache.py:401-460: ``W = min(window, Lq)``, softmax rounded to the
+  input dtype, ``y = p @ V`` in the input dtype) run on the same kernels with
+  ``y`` rounded to the input dtype;
+* selection (dropkv_cache.py:464-475) and gather (:479-491) always run on the
+  HIP select / compact kernels.
+
+There is no CPU fallback: inputs the kernels cannot take (CPU tensors, fp32,
+an uncompiled head dimension) raise ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import logging
+from typing import Any, Iterable, Optional
+
+import torch
+
+from . import ops
+
+logger = logging.getLogger(__name__)
+
+
+class _LayerCache:
+    """Per-layer K/V lists with the legacy HF container protocol that the
+    reference's ``DropKVCache`` inherits (dropkv_cache.py:104-307): only the
+    parts the eviction path relies on (layout of ``key_cache`` /
+    ``value_cache``, ``_seen_tokens``, indexing, legacy conversion)."""
+
+    is_compileable = False
+
+    def __init__(self, _distributed_cache_data: Optional[Iterable] = None) -> None:
+        self._seen_tokens = 0
+        self.key_cache: list[torch.Tensor] = []
+        self.value_cache: list[torch.Tensor] = []
+        if _distributed_cache_data is not None:
+            for k, v in _distributed_cache_data:
+                self.key_cache.append(k)
+                self.value_cache.append(v)
+
+    def __getitem__(self, layer_idx: int):
+        if layer_idx < len(self):
+            return self.key_cache[layer_idx], self.value_cache[layer_idx]
+        raise KeyError(f"Cache only has {len(self)} layers, attempted to access layer with index {layer_idx}")
+
+    def __iter__(self):
+        for i in range(len(self)):
+            yield self.key_cache[i], self.value_cache[i]
+
+    def __len__(self):
+        return len(self.key_cache)
+
+    def get_max_cache_shape(self) -> Optional[int]:
+        return None
+
+    def to_legacy_cache(self):
+        return tuple((self.key_cache[i], self.value_cache[i]) for i in range(len(self)))
+
+    @classmethod
+    def from_legacy_cache(cls, past_key_values=None):
+        cache = cls()
+        if past_key_values is not None:
+            for i, (k, v) in enumerate(past_key_values):
+                cache.update(None, k, v, i)
+        return cache
+
+    def reorder_cache(self, beam_idx: torch.LongTensor):
+        for i in range(len(self.key_cache)):
+            if self.key_cache[i].numel():
+                dev = self.key_cache[i].device
+                self.key_cache[i] = self.key_cache[i].index_select(0, beam_idx.to(dev))
+            if self.value_cache[i].numel():
+                dev = self.value_cache[i].device
+                self.value_cache[i] = self.value_cache[i].index_select(0, beam_idx.to(dev))
+
+
+def _deployed_path_scores(query_states, key_states, value_states, window_size: int) -> torch.Tensor:
+    """Scores with the deployed PyTorch path's precision (dropkv_cache.py:401-460)
+    on the HIP kernels: ``W = min(window, Lq)``, p and y rounded to the input
+    dtype."""
+    Hq, Hkv = query_states.shape[1], key_states.shape[1]
+    if Hq % Hkv != 0:
+        raise ValueError(f"Query heads {Hq} must be divisible by KV heads {Hkv}")
+    W = min(window_size, query_states.shape[2])
+    return ops.scores(query_states, key_states, value_states, W, eps=1e-6, p_round=True, y_round=True)
+
+
+class DropKVCache(_LayerCache):
+    """KV cache that evicts at prefill by the DropKV score
+    (dropkv_cache.py:310-648)."""
+
+    def __init__(self, keep_ratio: float = 0.1, window_size: int = 8, kernel_size: int = 11,
+                 use_triton: bool = True) -> None:
+        super().__init__()
+        if not 0 < keep_ratio <= 1.0:
+            raise ValueError(f"keep_ratio must be in (0, 1], got {keep_ratio}")
+        self.keep_ratio = keep_ratio
+        if window_size <= 0:
+            raise ValueError(f"window_size must be positive, got {window_size}")
+        self.window_size = window_size
+        if kernel_size < 1 or kernel_size % 2 == 0:
+            raise ValueError(f"kernel_size must be a positive odd integer, got {kernel_size}")
+        self.kernel_size = kernel_size
+        self.use_triton = use_triton
+        # "single_pass" | "accumulate" | "evict_accumulated" (dropkv_cache.py:332-340)
+        self._prefill_mode = "single_pass"
+        self._evict_use_seen_tokens = False
+        self._budget_max_kv_tokens: Optional[int] = None
+
+    def batch_split(self, full_batch_size: int, split_size: int):
+        raise NotImplementedError(
+            "DropKVCache does not support batch_split (beam search). "
+            "Use DynamicCache for beam search or implement DropKV-aware splitting.")
+
+    @classmethod
+    def from_batch_splits(cls, splits, **kwargs):
+        raise NotImplementedError(
+            "DropKVCache does not support from_batch_splits (beam search). "
+            "Use DynamicCache for beam search or implement DropKV-aware merging.")
+
+    # -- keep length (dropkv_cache.py:470-473) ---------------------------------
+    def _keep_length(self, seq_len: int, total_tokens: Optional[int], max_keep_len: Optional[int]) -> int:
+        base = total_tokens if total_tokens is not None else seq_len
+        keep = min(seq_len, max(int(self.keep_ratio * base), self.window_size, 1))
+        if max_keep_len is not None:
+            keep = min(keep, max_keep_len)
+        return keep
+
+    def _compute_keep_indices(self, query_states: torch.Tensor, key_states: torch.Tensor,
+                              value_states: torch.Tensor, total_tokens: Optional[int] = None,
+                              max_keep_len: Optional[int] = None) -> torch.Tensor:
+        """Sorted indices [B, Hkv, keep] of the keys to retain
+        (dropkv_cache.py:355-477)."""
+        bsz, num_kv_heads, seq_len, head_dim = key_states.shape
+        num_query_heads = query_states.shape[1]
+        if num_query_heads % num_kv_heads != 0:
+            raise ValueError(f"Query heads {num_query_heads} must be divisible by KV heads {num_kv_heads}")
+
+        scores = None
+        if self.use_triton:
+            try:
+                from . import dropkv_triton as _scoring
+                scores = _scoring.dropkv_scores_triton(
+                    query_states, key_states.contiguous(), value_states.contiguous(),
+                    window_size=self.window_size)
+            except (ImportError, AssertionError):
+                scores = None
+        if scores is None:
+            scores = _deployed_path_scores(query_states, key_states, value_states, self.window_size)
+
+        keep_len = self._keep_length(seq_len, total_tokens, max_keep_len)
+        protect = min(self.window_size, seq_len)
+        return ops.select(scores, self.kernel_size, protect, keep_len)
+
+    @staticmethod
+    def _gather_compressed(key_states: torch.Tensor, value_states: torch.Tensor,
+                           keep_idx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Gather the retained rows (dropkv_cache.py:479-491), bit-exact."""
+        return ops.compact(key_states, value_states, keep_idx)
+
+    def update(self, query_states: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,
+               layer_idx: int, cache_kwargs: Optional[dict[str, Any]] = None):
+        """Same control flow as dropkv_cache.py:493-622."""
+        # HF 4-argument form: update(key, value, layer_idx, cache_kwargs).
+        if isinstance(value_states, int) and isinstance(layer_idx, dict):
+            cache_kwargs = layer_idx
+            layer_idx = value_states
+            value_states = key_states
+            key_states = query_states
+            query_states = cache_kwargs.get("query_states") if cache_kwargs else None
+            if query_states is None:
+                logger.warning(
+                    "DropKVCache.update() called without query_states — eviction disabled for this layer. "
+                    "Patch your transformers to pass query_states in cache_kwargs.")
+
+        if layer_idx == 0:
+            self._seen_tokens += key_states.shape[-2]
+
+        if len(self.key_cache) < layer_idx:
+            raise ValueError("Use DynamicCache.")
+        elif len(self.key_cache) == layer_idx:
+            # --- prefill ---
+            if query_states is None:
+                if self._prefill_mode != "single_pass":
+                    logger.warning("query_states is None at layer %d — storing full KV without eviction.",
+                                   layer_idx)
+                self.key_cache.append(key_states)
+                self.value_cache.append(value_states)
+                return key_states, value_states
+
+            seq_len = key_states.shape[2]
+            if self._prefill_mode not in ("single_pass", "accumulate", "evict_accumulated"):
+                raise ValueError(f"Invalid _prefill_mode: {self._prefill_mode!r}")
+            if self._prefill_mode == "accumulate" or seq_len < self.window_size:
+                self.key_cache.append(key_states)
+                self.value_cache.append(value_states)
+                return key_states, value_states
+
+            total_tok = self._seen_tokens if self._evict_use_seen_tokens else None
+            keep_idx = self._compute_keep_indices(query_states, key_states, value_states,
+                                                  total_tokens=total_tok,
+                                                  max_keep_len=self._budget_max_kv_tokens)
+            key_c, value_c = self._gather_compressed(key_states, value_states, keep_idx)
+            self.key_cache.append(key_c)
+            self.value_cache.append(value_c)
+            return key_states, value_states
+
+        # --- decode / chunked-prefill continuation ---
+        if self._prefill_mode == "accumulate":
+            self.key_cache[layer_idx] = torch.cat([self.key_cache[layer_idx], key_states], dim=-2)
+            self.value_cache[layer_idx] = torch.cat([self.value_cache[layer_idx], value_states], dim=-2)
+            return self.key_cache[layer_idx], self.value_cache[layer_idx]
+        if self._prefill_mode == "evict_accumulated":
+            full_key = torch.cat([self.key_cache[layer_idx], key_states], dim=-2)
+            full_value = torch.cat([self.value_cache[layer_idx], value_states], dim=-2)
+            if query_states is not None and full_key.shape[2] >= self.window_size:
+                total_tok = self._seen_tokens if self._evict_use_seen_tokens else None
+                keep_idx = self._compute_keep_indices(query_states, full_key, full_value,
+                                                      total_tokens=total_tok,
+                                                      max_keep_len=self._budget_max_kv_tokens)
+                key_c, value_c = self._gather_compressed(full_key, full_value, keep_idx)
+                self.key_cache[layer_idx] = key_c
+                self.value_cache[layer_idx] = value_c
+            else:
+                self.key_cache[layer_idx] = full_key
+                self.value_cache[layer_idx] = full_value
+            return full_key, full_value
+        if self._prefill_mode == "single_pass":
+            self.key_cache[layer_idx] = torch.cat([self.key_cache[layer_idx], key_states], dim=-2)
+            self.value_cache[layer_idx] = torch.cat([self.value_cache[layer_idx], value_states], dim=-2)
+            return self.key_cache[layer_idx], self.value_cache[layer_idx]
+        raise ValueError(f"Invalid _prefill_mode {self._prefill_mode!r} in decode path")
+
+    def get_seq_length(self, layer_idx: Optional[int] = 0) -> int:
+        """Logical length (tokens seen) for RoPE positions (dropkv_cache.py:624-633)."""
+        if len(self.key_cache) <= layer_idx:
+            return 0
+        return self._seen_tokens
+
+    def get_mask_sizes(self, cache_position: torch.Tensor, layer_idx: int = 0) -> tuple[int, int]:
+        """(stored length + query length, 0) for the attention mask
+        (dropkv_cache.py:635-648)."""
+        query_length = cache_position.shape[0]
+        empty = (len(self.key_cache) == 0 or len(self.key_cache) <= layer_idx
+                 or not self.key_cache[layer_idx].numel())
+        stored = 0 if empty else self.key_cache[layer_idx].shape[-2]
+        return stored + query_length, 0
+
+
+def prefill_chunked(model, input_ids, cache, chunk_size=4096, evict_strategy="last_chunk",
+                    max_kv_tokens=32768, **forward_kwargs):
+    """Chunked prefill with eviction strategies ``last_chunk`` / ``budget`` /
+    ``every_chunk`` (dropkv_cache.py:651-807).  Same validation errors, mode
+    schedule and cleanup on failure as the reference."""
+    if not isinstance(cache, DropKVCache):
+        raise TypeError(f"cache must be DropKVCache, got {type(cache).__name__}")
+    if len(cache.key_cache) > 0:
+        raise ValueError("prefill_chunked() requires a fresh (empty) cache. Create a new DropKVCache instance.")
+    if chunk_size < cache.window_size:
+        raise ValueError(f"chunk_size ({chunk_size}) must be >= window_size ({cache.window_size})")
+    bad = {"attention_mask", "position_ids", "cache_position"} & forward_kwargs.keys()
+    if bad:
+        raise ValueError(
+            f"prefill_chunked() does not support sequence-shaped kwargs {bad} — the model computes these "
+            f"internally per chunk. Remove them from forward_kwargs.")
+    strategies = ("last_chunk", "budget", "every_chunk")
+    if evict_strategy not in strategies:
+        raise ValueError(f"evict_strategy must be one of {strategies}, got {evict_strategy!r}")
+    if evict_strategy == "budget":
+        if max_kv_tokens is None:
+            raise ValueError("max_kv_tokens is required when evict_strategy='budget'")
+        if max_kv_tokens < cache.window_size:
+            raise ValueError(f"max_kv_tokens ({max_kv_tokens}) must be >= window_size ({cache.window_size}) "
+                             f"to preserve protected tail tokens")
+
+    B, L = input_ids.shape
+    if L <= chunk_size and evict_strategy == "last_chunk":
+        with torch.no_grad():
+            return model(input_ids, past_key_values=cache, use_cache=True, **forward_kwargs)
+
+    starts = list(range(0, L, chunk_size))
+    try:
+        cache._evict_use_seen_tokens = evict_strategy in ("budget", "every_chunk")
+        if evict_strategy == "budget":
+            cache._budget_max_kv_tokens = max_kv_tokens
+        with torch.no_grad():
+            output = None
+            for i, start in enumerate(starts):
+                end = min(start + chunk_size, L)
+                is_last = i == len(starts) - 1
+                if evict_strategy == "last_chunk":
+                    cache._prefill_mode = "evict_accumulated" if is_last else "accumulate"
+                elif evict_strategy == "every_chunk":
+                    cache._prefill_mode = "single_pass" if i == 0 else "evict_accumulated"
+                else:
+                    if is_last:
+                        cache._prefill_mode = "evict_accumulated"
+                    else:
+                        stored = cache.key_cache[0].shape[2] if cache.key_cache else 0
+                        cache._prefill_mode = ("evict_accumulated" if stored + (end - start) > max_kv_tokens
+                                               else "accumulate")
+                output = model(input_ids[:, start:end], past_key_values=cache, use_cache=True, **forward_kwargs)
+            return output
+    except BaseException:
+        cache.key_cache.clear()
+        cache.value_cache.clear()
+        cache._seen_tokens = 0
+        raise
+    finally:
+        cache._prefill_mode = "single_pass"
+        cache._evict_use_seen_tokens = False
+        cache._budget_max_kv_tokens = None

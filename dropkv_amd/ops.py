@@ -1,0 +1,199 @@
+"""Torch-tensor wrappers around the C ABI of libdropkv_amd.so.
+
+PyTorch provides device memory (its caching allocator, also for the
+workspaces) and the current HIP stream; all arithmetic runs in the HIP
+kernels.  The wrappers check what the kernels assume (device, dtype, layout,
+alignment) and raise ``RuntimeError`` otherwise; the reference-compatible
+``AssertionError`` guards live in :mod:`dropkv_amd.dropkv_triton`.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {torch.bfloat16: _lib.DROPKV_BF16, torch.float16: _lib.DROPKV_FP16}
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+
+def _aligned(t: torch.Tensor) -> bool:
+    return t.data_ptr() % 16 == 0
+
+
+def _kv_operand(t: torch.Tensor) -> torch.Tensor:
+    """K/V must be contiguous and 16-byte aligned for the vector loads."""
+    if not t.is_contiguous() or not _aligned(t):
+        t = t.contiguous() if not t.is_contiguous() else t.clone()
+    return t
+
+
+def _check_device(*ts: torch.Tensor) -> torch.device:
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise RuntimeError("DropKV HIP ops need tensors on a ROCm (cuda) device")
+    for t in ts[1:]:
+        if t.device != dev:
+            raise RuntimeError("all tensors must be on the same device")
+    return dev
+
+
+def scores(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, window: int, eps: float = 1e-6,
+           p_round: bool = True, y_round: bool = False, splits: int = 0,
+           return_workspace: bool = False):
+    """Per-key DropKV scores [B, Hkv, Lk] fp32 (see ``dropkv_scores`` in the C ABI)."""
+    dev = _check_device(Q, K, V)
+    if Q.dtype not in _DTYPE_CODE or K.dtype != Q.dtype or V.dtype != Q.dtype:
+        raise RuntimeError(f"unsupported dtype combination {Q.dtype}/{K.dtype}/{V.dtype}")
+    B, Hq, Lq, D = Q.shape
+    Hkv, Lk = K.shape[1], K.shape[2]
+    K = _kv_operand(K)
+    V = _kv_operand(V)
+    lib = _lib.load()
+    ws_bytes = lib.dropkv_scores_workspace_bytes(B, Hq, Hkv, Lk, D, window, splits)
+    ws = _workspace(ws_bytes, dev)
+    out = torch.empty(B, Hkv, Lk, dtype=torch.float32, device=dev)
+    rc = lib.dropkv_scores(Q.data_ptr(), *Q.stride(), K.data_ptr(), V.data_ptr(), _DTYPE_CODE[Q.dtype],
+                           B, Hq, Hkv, Lq, Lk, D, window, float(eps), int(bool(p_round)), int(bool(y_round)),
+                           int(splits), out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+    _lib.check(rc, "dropkv_scores")
+    if return_workspace:
+        return out, ws
+    return out
+
+
+def scores_debug_state(ws: torch.Tensor, B: int, Hq: int, Hkv: int, Lk: int, D: int, window: int,
+                       splits: int = 0):
+    """(lse [B,Hkv,M] natural log, y [B,Hkv,M,D] fp32) left in a scoring workspace."""
+    dev = ws.device
+    M = (Hq // Hkv) * window
+    lse = torch.empty(B, Hkv, M, dtype=torch.float32, device=dev)
+    y = torch.empty(B, Hkv, M, D, dtype=torch.float32, device=dev)
+    rc = _lib.load().dropkv_scores_debug_state(ws.data_ptr(), B, Hq, Hkv, Lk, D, window, splits,
+                                               lse.data_ptr(), y.data_ptr(), _stream(dev))
+    _lib.check(rc, "dropkv_scores_debug_state")
+    return lse, y
+
+
+def select(scores_t: torch.Tensor, kernel_size: int, window: int, keep: int, return_pooled: bool = False):
+    """Pool, protect, top-k and sort: int64 indices [..., keep], ascending."""
+    dev = _check_device(scores_t)
+    if scores_t.dtype != torch.float32:
+        raise RuntimeError("select expects fp32 scores")
+    s = scores_t.contiguous()
+    Lk = s.shape[-1]
+    rows = s.numel() // Lk
+    lib = _lib.load()
+    ws = _workspace(lib.dropkv_select_workspace_bytes(rows, Lk), dev)
+    idx = torch.empty(*s.shape[:-1], keep, dtype=torch.int64, device=dev)
+    pooled = torch.empty_like(s) if return_pooled else None
+    rc = lib.dropkv_select(s.data_ptr(), rows, Lk, kernel_size, window, keep, idx.data_ptr(),
+                           pooled.data_ptr() if pooled is not None else None, ws.data_ptr(), ws.numel(),
+                           _stream(dev))
+    _lib.check(rc, "dropkv_select")
+    if return_pooled:
+        return idx, pooled
+    return idx
+
+
+def _seg_strides(t: torch.Tensor):
+    if t.stride(3) != 1:
+        raise RuntimeError("the head-dim axis of K/V must be contiguous")
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def compact(K: torch.Tensor, V: torch.Tensor, idx: torch.Tensor):
+    """Bit-exact gather of rows ``idx`` [B,H,keep] from K/V [B,H,L,D]."""
+    dev = _check_device(K, V, idx)
+    if K.shape != V.shape or K.stride() != V.stride() or K.dtype != V.dtype:
+        raise RuntimeError("K and V must have the same shape, strides and dtype")
+    if K.stride(3) != 1:
+        K, V = K.contiguous(), V.contiguous()
+    idx = idx.to(torch.int64).contiguous()
+    B, H, L, D = K.shape
+    keep = idx.shape[-1]
+    ko = torch.empty(B, H, keep, D, dtype=K.dtype, device=dev)
+    vo = torch.empty_like(ko)
+    rc = _lib.load().dropkv_compact(K.data_ptr(), V.data_ptr(), *_seg_strides(K), K.element_size(), B, H, L, D,
+                                    idx.data_ptr(), keep, ko.data_ptr(), vo.data_ptr(), _stream(dev))
+    _lib.check(rc, "dropkv_compact")
+    return ko, vo
+
+
+def compact2(K0: torch.Tensor, V0: torch.Tensor, K1: torch.Tensor, V1: torch.Tensor, idx: torch.Tensor):
+    """Gather from the logical concatenation [K0 | K1] along the sequence axis."""
+    dev = _check_device(K0, V0, K1, V1, idx)
+    if K0.stride(3) != 1 or V0.stride(3) != 1:
+        K0, V0 = K0.contiguous(), V0.contiguous()
+    if K1.stride(3) != 1 or V1.stride(3) != 1:
+        K1, V1 = K1.contiguous(), V1.contiguous()
+    if K0.stride() != V0.stride() or K1.stride() != V1.stride():
+        K0, V0, K1, V1 = K0.contiguous(), V0.contiguous(), K1.contiguous(), V1.contiguous()
+    idx = idx.to(torch.int64).contiguous()
+    B, H, L0, D = K0.shape
+    L1 = K1.shape[2]
+    keep = idx.shape[-1]
+    ko = torch.empty(B, H, keep, D, dtype=K0.dtype, device=dev)
+    vo = torch.empty_like(ko)
+    rc = _lib.load().dropkv_compact2(K0.data_ptr(), V0.data_ptr(), *_seg_strides(K0), L0,
+                                     K1.data_ptr(), V1.data_ptr(), *_seg_strides(K1), L1,
+                                     K0.element_size(), B, H, D, idx.data_ptr(), keep, ko.data_ptr(),
+                                     vo.data_ptr(), _stream(dev))
+    _lib.check(rc, "dropkv_compact2")
+    return ko, vo
+
+
+class EvictPlan:
+    """Pre-sized workspace and outputs for repeated layer-calls of one shape
+    (``dropkv_evict``); avoids per-call allocation in tight loops."""
+
+    def __init__(self, Q: torch.Tensor, K: torch.Tensor, window: int, kernel_size: int, keep: int,
+                 protect_window: int | None = None, eps: float = 1e-6, p_round: bool = True,
+                 y_round: bool = False, splits: int = 0, keep_scores: bool = False):
+        dev = _check_device(Q, K)
+        B, Hq, Lq, D = Q.shape
+        Hkv, Lk = K.shape[1], K.shape[2]
+        self.shape = (B, Hq, Hkv, Lq, Lk, D)
+        self.dtype = Q.dtype
+        self.window, self.kernel_size, self.keep = int(window), int(kernel_size), int(keep)
+        self.protect_window = int(window if protect_window is None else protect_window)
+        self.eps, self.p_round, self.y_round, self.splits = float(eps), int(p_round), int(y_round), int(splits)
+        lib = _lib.load()
+        self.ws = _workspace(lib.dropkv_evict_workspace_bytes(B, Hq, Hkv, Lk, D, window, splits), dev)
+        self.scores = torch.empty(B, Hkv, Lk, dtype=torch.float32, device=dev) if keep_scores else None
+        self.keep_idx = torch.empty(B, Hkv, keep, dtype=torch.int64, device=dev)
+        self.k_out = torch.empty(B, Hkv, keep, D, dtype=Q.dtype, device=dev)
+        self.v_out = torch.empty_like(self.k_out)
+        self.dev = dev
+
+    def __call__(self, Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor):
+        B, Hq, Hkv, Lq, Lk, D = self.shape
+        if tuple(Q.shape) != (B, Hq, Lq, D) or tuple(K.shape) != (B, Hkv, Lk, D) or K.shape != V.shape:
+            raise RuntimeError("input shapes differ from the plan")
+        if Q.dtype != self.dtype or K.dtype != self.dtype or V.dtype != self.dtype:
+            raise RuntimeError("input dtype differs from the plan")
+        K = _kv_operand(K)
+        V = _kv_operand(V)
+        rc = _lib.load().dropkv_evict(
+            Q.data_ptr(), *Q.stride(), K.data_ptr(), V.data_ptr(), _DTYPE_CODE[self.dtype],
+            B, Hq, Hkv, Lq, Lk, D, self.window, self.eps, self.p_round, self.y_round, self.splits,
+            self.kernel_size, self.protect_window, self.keep,
+            self.scores.data_ptr() if self.scores is not None else None, self.keep_idx.data_ptr(),
+            self.k_out.data_ptr(), self.v_out.data_ptr(), self.ws.data_ptr(), self.ws.numel(),
+            _stream(self.dev))
+        _lib.check(rc, "dropkv_evict")
+        return self.keep_idx, self.k_out, self.v_out
+
+
+def mfma_selftest(device="cuda") -> torch.Tensor:
+    out = torch.empty(16, 16, dtype=torch.float32, device=device)
+    rc = _lib.load().dropkv_selftest_mfma(out.data_ptr(), _stream(out.device))
+    _lib.check(rc, "dropkv_selftest_mfma")
+    return out

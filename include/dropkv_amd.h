@@ -1,0 +1,148 @@
+/*
+ * dropkv_amd.h -- C ABI of the MI355X (gfx950) DropKV prefill KV-eviction path.
+ *
+ * Plain pointers, element strides and sizes; no framework types.  All device
+ * pointers are HIP device memory; `stream` is a hipStream_t passed as void*
+ * (NULL = the legacy default stream).  Every call only enqueues work on
+ * `stream` and returns without synchronising.  Inputs are never written.
+ *
+ * Return value: 0 on success, otherwise a nonzero DROPKV_E_* code; the
+ * message of the last failure on the calling thread is available from
+ * dropkv_last_error().  Argument checks happen before anything is enqueued.
+ *
+ * Citations refer to the reference checkout (AozhongZhang/DropKV).
+ */
+#ifndef DROPKV_AMD_H
+#define DROPKV_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element type codes */
+#define DROPKV_BF16 1
+#define DROPKV_FP16 2
+
+/* status codes */
+#define DROPKV_OK 0
+#define DROPKV_E_ARG 1         /* invalid shape / argument */
+#define DROPKV_E_UNSUPPORTED 2 /* valid but not implemented here (e.g. D) */
+#define DROPKV_E_WORKSPACE 3   /* workspace too small */
+#define DROPKV_E_HIP 4         /* HIP runtime error */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int dropkv_version(void);
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* dropkv_last_error(void);
+
+/* Head dimensions the scoring kernels are compiled for; writes up to `cap`
+ * values into `out` and returns how many exist. */
+int dropkv_supported_head_dims(int64_t* out, int cap);
+
+/* ------------------------------------------------------------------------
+ * Scoring.  Replaces dropkv_scores_triton (dropkv_triton.py:643-828) and its
+ * kernels _compute_logits_block / _dropkv_attn_fwd_kernel /
+ * _dropkv_attn_fwd_split_kernel / _dropkv_reduce_kernel /
+ * _dropkv_score_kernel (dropkv_triton.py:117-610); with y_round=1 and
+ * W=min(window,Lq) it also serves the deployed scoring path of
+ * DropKVCache._compute_keep_indices (dropkv_cache.py:401-460).
+ *
+ *   q      [B,Hq,Lq,D], arbitrary element strides q_s* (only the last W rows
+ *          along Lq are read; query row w sits at key position Lk-W+w)
+ *   k, v   [B,Hkv,Lk,D] contiguous, 16-byte aligned, same dtype as q
+ *   scores [B,Hkv,Lk] fp32 contiguous (output)
+ *   p_round 0: keep softmax probabilities in fp32; 1: round them to the input
+ *          dtype before w = (p/(1-p+eps))^2 (match_pytorch_precision=True,
+ *          dropkv_triton.py:584-587)
+ *   y_round 0: attention output y in fp32; 1: y rounded to the input dtype
+ *          (deployed path, dropkv_cache.py:434)
+ *   splits 0 = automatic split-K depth over keys, otherwise that many splits
+ *          per (b, hkv, row-chunk)
+ * Requires Hq % Hkv == 0, 1 <= W <= Lq <= Lk, D in the supported set.
+ * ------------------------------------------------------------------------ */
+size_t dropkv_scores_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk,
+                                     int64_t D, int64_t W, int64_t splits);
+
+int dropkv_scores(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
+                  const void* k, const void* v, int dtype,
+                  int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D,
+                  int64_t W, float eps, int p_round, int y_round, int64_t splits,
+                  float* scores, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Debug view of the scoring intermediates written by the last dropkv_scores
+ * call into `workspace`: lse [B*Hkv, M] (natural log) and y [B*Hkv, M, D] fp32
+ * (normalised attention output), M = (Hq/Hkv)*W.  Lets tests check the
+ * A<->B contract sum_j exp(l_j - lse) == 1 (reference tests:170-236). */
+int dropkv_scores_debug_state(const void* workspace, int64_t B, int64_t Hq, int64_t Hkv,
+                              int64_t Lk, int64_t D, int64_t W, int64_t splits,
+                              float* lse_out, float* y_out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Selection.  Replaces the pool / protect / top-k / sort sequence of
+ * DropKVCache._compute_keep_indices (dropkv_cache.py:464-475):
+ *   pooled = max_pool1d(scores, kernel_size, pad=kernel_size//2, stride 1)
+ *   pooled[..., Lk-window:] = max(pooled) + 1.0f
+ *   keep_idx = ascending indices of the `keep` largest pooled values, the
+ *              lowest indices first among values equal to the threshold.
+ *   scores   [rows, Lk] fp32 contiguous
+ *   keep_idx [rows, keep] int64 (output)
+ *   pooled   [rows, Lk] fp32 (optional output, may be NULL)
+ * ------------------------------------------------------------------------ */
+size_t dropkv_select_workspace_bytes(int64_t rows, int64_t Lk);
+
+int dropkv_select(const float* scores, int64_t rows, int64_t Lk, int64_t kernel_size,
+                  int64_t window, int64_t keep, int64_t* keep_idx, float* pooled,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Compaction.  Replaces DropKVCache._gather_compressed (dropkv_cache.py:479-491):
+ *   k_out[b,h,i,:] = k[b,h,idx[b,h,i],:]   (same for v), bit-exact copies.
+ * Sources have element strides (s_b, s_h, s_l) with the D axis contiguous;
+ * outputs are contiguous [B,H,keep,D].  elem_bytes is 2 for bf16/fp16.
+ * ------------------------------------------------------------------------ */
+int dropkv_compact(const void* k, const void* v, int64_t s_b, int64_t s_h, int64_t s_l,
+                   int64_t elem_bytes, int64_t B, int64_t H, int64_t L, int64_t D,
+                   const int64_t* idx, int64_t keep, void* k_out, void* v_out, void* stream);
+
+/* Two-segment compaction for the chunked-prefill continuation
+ * (dropkv_cache.py:581-607): the logical sequence is seg0 (length L0, the
+ * stored cache) followed by seg1 (length L1, the new chunk); index i < L0
+ * reads seg0[i], otherwise seg1[i-L0].  Same output layout as dropkv_compact. */
+int dropkv_compact2(const void* k0, const void* v0, int64_t s0_b, int64_t s0_h, int64_t s0_l,
+                    int64_t L0,
+                    const void* k1, const void* v1, int64_t s1_b, int64_t s1_h, int64_t s1_l,
+                    int64_t L1,
+                    int64_t elem_bytes, int64_t B, int64_t H, int64_t D,
+                    const int64_t* idx, int64_t keep, void* k_out, void* v_out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * One layer-call of prefill eviction: scores -> select -> compact, all
+ * enqueued on `stream` by one call.  Equivalent to
+ * DropKVCache._compute_keep_indices followed by _gather_compressed
+ * (dropkv_cache.py:355-491) on the fast path.  `scores`, `pooled` may be NULL
+ * (then they live in the workspace / are not written).
+ * ------------------------------------------------------------------------ */
+size_t dropkv_evict_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk,
+                                    int64_t D, int64_t W, int64_t splits);
+
+int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
+                 const void* k, const void* v, int dtype,
+                 int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D,
+                 int64_t W, float eps, int p_round, int y_round, int64_t splits,
+                 int64_t kernel_size, int64_t protect_window, int64_t keep,
+                 float* scores, int64_t* keep_idx, void* k_out, void* v_out,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Self-test of the matrix-core operand layout the kernels assume: computes a
+ * 16x16 fp32 product of fixed bf16 patterns with one MFMA and writes it to
+ * `out` (256 floats, device memory), row-major. */
+int dropkv_selftest_mfma(float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DROPKV_AMD_H */

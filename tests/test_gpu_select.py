@@ -1,0 +1,100 @@
+"""GPU parity of pool/protect/top-k/sort (select) and of the gather kernels.
+
+Bars: selected indices bit-exact against the oracle's deterministic rule
+(lowest index first among values equal to the threshold) on identical score
+inputs; pooled values bit-exact; gathered K/V bit-exact against torch.gather.
+"""
+
+import pytest
+import torch
+
+from oracle import dropkv_ref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _select_case(gpu, scores, ks, window, keep):
+    from dropkv_amd import ops
+    idx, pooled = ops.select(scores.to(gpu), ks, window, keep, return_pooled=True)
+    ref_pooled = R.pool_protect(scores.clone(), ks, window)
+    ref_idx = R.topk_sorted(ref_pooled, keep)
+    assert torch.equal(pooled.cpu(), ref_pooled)
+    assert torch.equal(idx.cpu(), ref_idx)
+
+
+@pytest.mark.parametrize("rows,Lk,keep", [(8, 32768, 3276), (2, 512, 51), (3, 100, 30), (1, 8, 8),
+                                          (4, 1000, 1), (2, 70000, 7000), (1, 4096, 4096)])
+def test_select_random(gpu, rows, Lk, keep):
+    g = torch.Generator().manual_seed(Lk + keep)
+    scores = torch.rand(1, rows, Lk, generator=g) * 1e-3
+    _select_case(gpu, scores, 11, 8, keep)
+
+
+def test_select_ties_and_plateaus(gpu):
+    """Integer-valued scores: pooling makes long plateaus, so the threshold
+    is tied many times over; the lowest indices must win."""
+    g = torch.Generator().manual_seed(1)
+    scores = torch.randint(0, 50, (1, 4, 20000), generator=g).float()
+    _select_case(gpu, scores, 11, 8, 2000)
+    _select_case(gpu, scores, 1, 8, 5000)
+    _select_case(gpu, torch.zeros(1, 2, 3000), 11, 8, 300)
+
+
+def test_select_big_absorbed(gpu):
+    """max >= 2^24: max + 1.0f == max, the protected tail ties with the maximum
+    (dropkv_cache.py:465-467 semantics in fp32)."""
+    scores = torch.zeros(1, 1, 512)
+    scores[0, 0, 100] = 2.0 ** 25
+    scores[0, 0, 300] = 2.0 ** 25
+    _select_case(gpu, scores, 11, 8, 20)
+    _select_case(gpu, scores, 11, 8, 8)
+
+
+def test_select_window_bigger_than_keep_floor(gpu):
+    g = torch.Generator().manual_seed(3)
+    scores = torch.rand(1, 2, 300, generator=g)
+    _select_case(gpu, scores, 3, 32, 32)
+    _select_case(gpu, scores, 11, 0, 40)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_compact_bit_exact(gpu, dtype):
+    from dropkv_amd import ops
+    g = torch.Generator().manual_seed(0)
+    B, H, L, D, keep = 2, 3, 777, 128, 100
+    K = torch.randn(B, H, L, D, generator=g).to(dtype)
+    V = torch.randn(B, H, L, D, generator=g).to(dtype)
+    idx = torch.sort(torch.stack([torch.randperm(L, generator=g)[:keep] for _ in range(B * H)]).view(B, H, keep),
+                     dim=-1).values
+    ko, vo = ops.compact(K.to(gpu), V.to(gpu), idx.to(gpu))
+    rk, rv = R.gather_compressed(K, V, idx)
+    assert torch.equal(ko.cpu().view(torch.int16), rk.view(torch.int16))
+    assert torch.equal(vo.cpu().view(torch.int16), rv.view(torch.int16))
+
+
+def test_compact_strided_and_odd_dim(gpu):
+    from dropkv_amd import ops
+    g = torch.Generator().manual_seed(2)
+    big = torch.randn(1, 4, 300, 72, generator=g).to(torch.bfloat16).to(gpu)
+    K = big[:, :, 50:250, :]          # non-contiguous along L/H (strided view)
+    V = (big * 2)[:, :, 50:250, :]
+    idx = torch.arange(0, 200, 3).view(1, 1, -1).expand(1, 4, -1).contiguous().to(gpu)
+    ko, vo = ops.compact(K, V, idx)
+    rk, rv = R.gather_compressed(K.cpu(), V.cpu(), idx.cpu())
+    assert torch.equal(ko.cpu(), rk) and torch.equal(vo.cpu(), rv)
+
+
+def test_compact2_matches_cat_gather(gpu):
+    """Two-segment gather == torch.cat then gather (dropkv_cache.py:581-607)."""
+    from dropkv_amd import ops
+    g = torch.Generator().manual_seed(5)
+    B, H, L0, L1, D, keep = 1, 8, 409, 4096, 128, 819
+    K0 = torch.randn(B, H, L0, D, generator=g).to(torch.bfloat16)
+    V0 = torch.randn(B, H, L0, D, generator=g).to(torch.bfloat16)
+    K1 = torch.randn(B, H, L1, D, generator=g).to(torch.bfloat16)
+    V1 = torch.randn(B, H, L1, D, generator=g).to(torch.bfloat16)
+    idx = torch.sort(torch.stack([torch.randperm(L0 + L1, generator=g)[:keep] for _ in range(B * H)])
+                     .view(B, H, keep), dim=-1).values
+    ko, vo = ops.compact2(K0.to(gpu), V0.to(gpu), K1.to(gpu), V1.to(gpu), idx.to(gpu))
+    rk, rv = R.gather_compressed(torch.cat([K0, K1], 2), torch.cat([V0, V1], 2), idx)
+    assert torch.equal(ko.cpu(), rk) and torch.equal(vo.cpu(), rv)
