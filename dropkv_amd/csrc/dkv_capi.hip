@@ -1,9 +1,12 @@
 // extern "C" entry points of libdropkv_amd.so (declared in include/dropkv_amd.h).
 // Argument validation happens here, before anything is enqueued.
 #include <cstdarg>
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/dropkv_amd.h"
 #include "dkv_internal.h"
@@ -59,7 +62,51 @@ int check_score_args(const void* q, const void* k, const void* v, int dtype, int
   return DROPKV_OK;
 }
 
+// Timestamp profiler state (dropkv_profile_*): one device slot of
+// 2*kNumStages uint64 per profiled layer-call.
+struct Profiler {
+  std::mutex mu;
+  bool armed = false;
+  int64_t max_calls = 0, calls = 0;
+  uint64_t* dev = nullptr;
+  double tick_ms = 0.0;  // wall-clock tick length in ms
+};
+Profiler g_prof;
+thread_local uint64_t* t_prof_slot = nullptr;
+
+void prof_release_locked() {
+  if (g_prof.dev) (void)hipFree(g_prof.dev);
+  g_prof.dev = nullptr;
+  g_prof.armed = false;
+  g_prof.max_calls = g_prof.calls = 0;
+}
+
+__global__ void prof_reset_kernel(uint64_t* slot) {
+  const int i = threadIdx.x;
+  if (i < 2 * dkv::kNumStages) slot[i] = (i & 1) ? 0ull : ~0ull;
+}
+
+int prof_slot_ms(const uint64_t* host_slot, double* stage_ms) {
+  for (int s = 0; s < dkv::kNumStages; ++s) {
+    const uint64_t t0 = host_slot[2 * s], t1 = host_slot[2 * s + 1];
+    stage_ms[s] = (t1 > 0 && t0 != ~0ull && t1 >= t0) ? (double)(t1 - t0) * g_prof.tick_ms : 0.0;
+  }
+  uint64_t first = ~0ull, last = 0;
+  for (int s = 0; s < dkv::kNumStages; ++s) {
+    if (host_slot[2 * s + 1] > 0 && host_slot[2 * s] != ~0ull) {
+      first = std::min(first, host_slot[2 * s]);
+      last = std::max(last, host_slot[2 * s + 1]);
+    }
+  }
+  stage_ms[dkv::kNumStages] = last > 0 ? (double)(last - first) * g_prof.tick_ms : 0.0;
+  return DROPKV_OK;
+}
+
 }  // namespace
+
+namespace dkv {
+uint64_t* prof_slot() { return t_prof_slot; }
+}  // namespace dkv
 
 extern "C" {
 
@@ -83,6 +130,7 @@ int dropkv_scores(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64
                   const void* v, int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D,
                   int64_t W, float eps, int p_round, int y_round, int64_t splits, float* scores, void* workspace,
                   size_t workspace_bytes, void* stream) {
+  (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
   int rc = check_score_args(q, k, v, dtype, B, Hq, Hkv, Lq, Lk, D, W);
   if (rc) return rc;
   if (!scores) return fail(DROPKV_E_ARG, "null scores pointer");
@@ -91,12 +139,13 @@ int dropkv_scores(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64
     return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", p.total, workspace_bytes);
   return hip_status(dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Hkv,
                                        (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, scores,
-                                       static_cast<char*>(workspace), static_cast<hipStream_t>(stream)),
+                                       static_cast<char*>(workspace), nullptr, 0, static_cast<hipStream_t>(stream)),
                     "dropkv_scores launch");
 }
 
 int dropkv_scores_debug_state(const void* workspace, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D,
                               int64_t W, int64_t splits, float* lse_out, float* y_out, void* stream) {
+  (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
   if (!workspace || !lse_out || !y_out) return fail(DROPKV_E_ARG, "null pointer");
   if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || W < 1 || Lk < W || !head_dim_supported(D))
     return fail(DROPKV_E_ARG, "invalid shape");
@@ -126,13 +175,14 @@ static int check_select_args(const float* scores, int64_t rows, int64_t Lk, int6
 
 int dropkv_select(const float* scores, int64_t rows, int64_t Lk, int64_t kernel_size, int64_t window, int64_t keep,
                   int64_t* keep_idx, float* pooled, void* workspace, size_t workspace_bytes, void* stream) {
+  (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
   int rc = check_select_args(scores, rows, Lk, kernel_size, window, keep, keep_idx);
   if (rc) return rc;
   const size_t need = dkv::select_workspace_bytes(rows, Lk);
   if (!workspace || workspace_bytes < need)
     return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
   return hip_status(dkv::launch_select(scores, (int)rows, (int)Lk, (int)kernel_size, (int)window, (int)keep, keep_idx,
-                                       pooled, static_cast<char*>(workspace), static_cast<hipStream_t>(stream)),
+                                       pooled, static_cast<char*>(workspace), false, static_cast<hipStream_t>(stream)),
                     "dropkv_select launch");
 }
 
@@ -148,6 +198,7 @@ static int check_compact_common(const int64_t* idx, int64_t eb, int64_t B, int64
 int dropkv_compact(const void* k, const void* v, int64_t s_b, int64_t s_h, int64_t s_l, int64_t elem_bytes,
                    int64_t B, int64_t H, int64_t L, int64_t D, const int64_t* idx, int64_t keep, void* k_out,
                    void* v_out, void* stream) {
+  (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
   int rc = check_compact_common(idx, elem_bytes, B, H, D, keep, k_out, v_out);
   if (rc) return rc;
   if (!k || !v) return fail(DROPKV_E_ARG, "null k/v pointer");
@@ -160,6 +211,7 @@ int dropkv_compact2(const void* k0, const void* v0, int64_t s0_b, int64_t s0_h, 
                     const void* k1, const void* v1, int64_t s1_b, int64_t s1_h, int64_t s1_l, int64_t L1,
                     int64_t elem_bytes, int64_t B, int64_t H, int64_t D, const int64_t* idx, int64_t keep,
                     void* k_out, void* v_out, void* stream) {
+  (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
   int rc = check_compact_common(idx, elem_bytes, B, H, D, keep, k_out, v_out);
   if (rc) return rc;
   if ((L0 > 0 && (!k0 || !v0)) || (L1 > 0 && (!k1 || !v1))) return fail(DROPKV_E_ARG, "null segment pointer");
@@ -182,6 +234,7 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
                  float eps, int p_round, int y_round, int64_t splits, int64_t kernel_size, int64_t protect_window,
                  int64_t keep, float* scores, int64_t* keep_idx, void* k_out, void* v_out, void* workspace,
                  size_t workspace_bytes, void* stream) {
+  (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
   int rc = check_score_args(q, k, v, dtype, B, Hq, Hkv, Lq, Lk, D, W);
   if (rc) return rc;
   rc = check_select_args(reinterpret_cast<const float*>(1), B * Hkv, Lk, kernel_size, protect_window, keep, keep_idx);
@@ -195,18 +248,89 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
   char* ws = static_cast<char*>(workspace);
   float* sc = scores ? scores : reinterpret_cast<float*>(ws + p.total);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  struct SlotGuard {
+    explicit SlotGuard(hipStream_t st) {
+      std::lock_guard<std::mutex> lk(g_prof.mu);
+      if (g_prof.armed && g_prof.calls < g_prof.max_calls) {
+        t_prof_slot = g_prof.dev + (size_t)(g_prof.calls++) * 2 * dkv::kNumStages;
+        hipLaunchKernelGGL(prof_reset_kernel, dim3(1), dim3(64), 0, st, t_prof_slot);
+      }
+    }
+    ~SlotGuard() { t_prof_slot = nullptr; }
+  } slot_guard(st);
+  char* sel_ws = ws + p.total + s_bytes;
   hipError_t e = dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Hkv,
-                                    (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws, st);
+                                    (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws,
+                                    reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv), st);
   if (e != hipSuccess) return hip_status(e, "dropkv_evict scores");
   e = dkv::launch_select(sc, (int)(B * Hkv), (int)Lk, (int)kernel_size, (int)protect_window, (int)keep, keep_idx,
-                         nullptr, ws + p.total + s_bytes, st);
+                         nullptr, sel_ws, true, st);
   if (e != hipSuccess) return hip_status(e, "dropkv_evict select");
   e = dkv::launch_compact(k, v, Hkv * Lk * D, Lk * D, D, Lk, nullptr, nullptr, 0, 0, 0, 0, 2, B, Hkv, D, keep_idx,
                           keep, k_out, v_out, st);
   return hip_status(e, "dropkv_evict compact");
 }
 
+int dropkv_profile_begin(int64_t max_calls) {
+  if (max_calls < 1 || max_calls > 100000) return fail(DROPKV_E_ARG, "max_calls must be in [1, 100000]");
+  (void)hipGetLastError();
+  std::lock_guard<std::mutex> lk(g_prof.mu);
+  prof_release_locked();
+  int dev = 0, khz = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err == hipSuccess) err = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+  if (err != hipSuccess || khz <= 0) return hip_status(err == hipSuccess ? hipErrorInvalidValue : err, "wall clock rate");
+  g_prof.tick_ms = 1.0 / (double)khz;
+  err = hipMalloc(reinterpret_cast<void**>(&g_prof.dev), (size_t)max_calls * 2 * dkv::kNumStages * sizeof(uint64_t));
+  if (err != hipSuccess) {
+    g_prof.dev = nullptr;
+    return hip_status(err, "hipMalloc(profile slots)");
+  }
+  g_prof.max_calls = max_calls;
+  g_prof.calls = 0;
+  g_prof.armed = true;
+  return DROPKV_OK;
+}
+
+int dropkv_profile_read(int64_t slot, double* stage_ms) {
+  std::lock_guard<std::mutex> lk(g_prof.mu);
+  if (!g_prof.dev || slot < 0 || slot >= g_prof.calls)
+    return fail(DROPKV_E_ARG, "no recorded profile slot %lld", (long long)slot);
+  uint64_t host[2 * dkv::kNumStages];
+  hipError_t err = hipDeviceSynchronize();
+  if (err == hipSuccess)
+    err = hipMemcpy(host, g_prof.dev + (size_t)slot * 2 * dkv::kNumStages, sizeof(host), hipMemcpyDeviceToHost);
+  if (err != hipSuccess) return hip_status(err, "profile read");
+  return prof_slot_ms(host, stage_ms);
+}
+
+int dropkv_profile_disarm(void) {
+  std::lock_guard<std::mutex> lk(g_prof.mu);
+  g_prof.armed = false;  // recorded slots stay readable until dropkv_profile_end
+  return DROPKV_OK;
+}
+
+int dropkv_profile_end(double* stage_ms, int64_t* calls) {
+  std::lock_guard<std::mutex> lk(g_prof.mu);
+  if (!g_prof.dev) return fail(DROPKV_E_ARG, "profiler not started");
+  for (int s = 0; s <= dkv::kNumStages; ++s) stage_ms[s] = 0.0;
+  std::vector<uint64_t> host((size_t)g_prof.calls * 2 * dkv::kNumStages);
+  hipError_t err = hipDeviceSynchronize();
+  if (err == hipSuccess && !host.empty())
+    err = hipMemcpy(host.data(), g_prof.dev, host.size() * sizeof(uint64_t), hipMemcpyDeviceToHost);
+  if (err != hipSuccess) return hip_status(err, "profile end");
+  for (int64_t i = 0; i < g_prof.calls; ++i) {
+    double ms[dkv::kNumStages + 1];
+    prof_slot_ms(&host[(size_t)i * 2 * dkv::kNumStages], ms);
+    for (int s = 0; s <= dkv::kNumStages; ++s) stage_ms[s] += ms[s];
+  }
+  if (calls) *calls = g_prof.calls;
+  prof_release_locked();
+  return DROPKV_OK;
+}
+
 int dropkv_selftest_mfma(float* out, void* stream) {
+  (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
   if (!out) return fail(DROPKV_E_ARG, "null out");
   return hip_status(dkv::launch_mfma_selftest(out, static_cast<hipStream_t>(stream)), "selftest launch");
 }

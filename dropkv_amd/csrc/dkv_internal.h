@@ -7,6 +7,14 @@
 
 namespace dkv {
 
+// Kernels of a layer-call, for the optional timestamp profiler
+// (dropkv_profile_*).  When a call is being profiled, prof_slot() returns a
+// device buffer of 2*kNumStages uint64 (per stage: first-workgroup start,
+// last-workgroup end, in wall-clock ticks) that the kernels update; otherwise
+// nullptr and the kernels skip the bookkeeping.
+enum Stage { kStPass1 = 0, kStMerge, kStPass2, kStSelZero, kStSelPool, kStSelTopk, kStCompact, kNumStages };
+uint64_t* prof_slot();
+
 // Launch geometry and workspace layout of one scoring call.
 struct ScorePlan {
   int heads, g, M, n_mc, mpad;
@@ -18,14 +26,18 @@ struct ScorePlan {
 ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W, int64_t splits);
 hipError_t launch_scores(const ScorePlan& p, int dtype_bf16, int D, const void* q, int64_t q_sb, int64_t q_sh,
                          int64_t q_ss, int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk, int W,
-                         float eps, int p_round, int y_round, float* scores, char* ws, hipStream_t st);
+                         float eps, int p_round, int y_round, float* scores, char* ws, uint32_t* zero_ptr,
+                         int64_t zero_words, hipStream_t st);
 hipError_t launch_debug_state(const ScorePlan& p, const char* ws, int D, float* lse_out, float* y_out,
                               hipStream_t st);
 hipError_t launch_mfma_selftest(float* out, hipStream_t st);
 
 size_t select_workspace_bytes(int64_t rows, int64_t Lk);
+// Words at the start of the selection workspace that must be zero on entry
+// (cleared by launch_select itself unless the caller already did it).
+int64_t select_zero_words(int64_t rows);
 hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int window, int keep, int64_t* out_idx,
-                         float* pooled_out, char* ws, hipStream_t st);
+                         float* pooled_out, char* ws, bool pre_zeroed, hipStream_t st);
 
 hipError_t launch_compact(const void* k0, const void* v0, int64_t s0b, int64_t s0h, int64_t s0l, int64_t L0,
                           const void* k1, const void* v1, int64_t s1b, int64_t s1h, int64_t s1l, int64_t L1,

@@ -86,7 +86,9 @@ __global__ void __launch_bounds__(kThreads, 2)
 pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
              const T* __restrict__ kp, const T* __restrict__ vp,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int n_splits, int kps,
-             float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y) {
+             float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y,
+             uint64_t* __restrict__ prof) {
+  prof_begin(prof, kStPass1);
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
   constexpr int DT = D / 16;
@@ -292,61 +294,106 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   }
   float* py = part_y + slot * kRows * D;
   for (int i = threadIdx.x; i < kRows * D; i += kThreads) py[i] = ybuf[i];
+  prof_end(prof, kStPass1);
 }
 
 // ---------------------------------------------------------------------------
-// Merge: one workgroup per (head, padded row); thread d owns column d.
+// Merge: one workgroup per (head, padded row).  The split weights
+// f_s = 2^(m_s - max_s m_s) go to LDS; thread (group, d) then sums the
+// weighted partial y rows of every G-th split, with many loads in flight.
 // Writes y as (hi, lo) element pairs for the score pass, the row statistics
-// (lse in log2 units, |y|^2) and an fp32 copy of y for inspection.
+// (lse in log2 units, |y|^2) and an fp32 copy of y for inspection.  Optionally
+// clears `zero_words` words at `zero_ptr` (the selection workspace of a fused
+// layer-call), so that needs no launch of its own.
 // ---------------------------------------------------------------------------
+constexpr int kMergeThreads = 256;
+constexpr int kMaxSplits = 1024;
+
+__device__ __forceinline__ float block_reduce(float x, float* red, bool is_max) {
+  x = is_max ? wave_max(x) : wave_sum(x);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = x;
+  __syncthreads();
+  float t = red[0];
+  for (int i = 1; i < (int)(blockDim.x >> 6); ++i) t = is_max ? fmaxf(t, red[i]) : t + red[i];
+  return t;
+}
+
 template <typename T, int D>
-__global__ void __launch_bounds__(D)
+__global__ void __launch_bounds__(kMergeThreads)
 merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y, int n_mc, int n_splits,
-             int M, int y_round, T* __restrict__ yhl, float* __restrict__ ystat, float* __restrict__ yf32) {
+             int M, int y_round, T* __restrict__ yhl, float* __restrict__ ystat, float* __restrict__ yf32,
+             uint32_t* __restrict__ zero_ptr, int64_t zero_words, uint64_t* __restrict__ prof) {
+  prof_begin(prof, kStMerge);
+  constexpr int G = kMergeThreads / D;
+  __shared__ float s_f[kMaxSplits];
+  __shared__ float s_red[kMergeThreads / 64];
+  __shared__ float s_acc[G][D];
+  const int tid = threadIdx.x;
+  if (zero_ptr)
+    for (int64_t i = (int64_t)blockIdx.x * kMergeThreads + tid; i < zero_words;
+         i += (int64_t)gridDim.x * kMergeThreads)
+      zero_ptr[i] = 0u;
+
   const int mpad = n_mc * kRows;
   const int head = blockIdx.x / mpad;
   const int gr = blockIdx.x % mpad;
   const int mc = gr / kRows, row = gr % kRows;
-  const int d = threadIdx.x;
   const int64_t slot0 = ((int64_t)head * n_mc + mc) * n_splits;
 
   float mx = -INFINITY;
-  for (int s = 0; s < n_splits; ++s) mx = fmaxf(mx, part_ml[((slot0 + s) * kRows + row) * 2]);
-  float l = 0.f, acc = 0.f;
-  if (mx != -INFINITY) {
-    for (int s = 0; s < n_splits; ++s) {
-      const float ms = part_ml[((slot0 + s) * kRows + row) * 2];
-      const float f = ms == -INFINITY ? 0.f : exp2f(ms - mx);
-      l += part_ml[((slot0 + s) * kRows + row) * 2 + 1] * f;
-      acc += part_y[((slot0 + s) * kRows + row) * D + d] * f;
-    }
+  for (int s = tid; s < n_splits; s += kMergeThreads) {
+    const float m = part_ml[((slot0 + s) * kRows + row) * 2];
+    s_f[s] = m;
+    mx = fmaxf(mx, m);
   }
-  const bool valid = gr < M && mx != -INFINITY;
-  float y = valid ? acc / l : 0.f;
-  T hi, lo;
-  if (y_round) {
-    hi = static_cast<T>(y);
-    y = static_cast<float>(hi);
-    lo = static_cast<T>(0.f);
-  } else {
-    hi = static_cast<T>(y);
-    lo = static_cast<T>(y - static_cast<float>(hi));
+  mx = block_reduce(mx, s_red, true);
+  float lpart = 0.f;
+  for (int s = tid; s < n_splits; s += kMergeThreads) {
+    const float m = s_f[s];
+    const float f = (m == -INFINITY || mx == -INFINITY) ? 0.f : exp2f(m - mx);
+    s_f[s] = f;
+    lpart += part_ml[((slot0 + s) * kRows + row) * 2 + 1] * f;
   }
-  const int64_t rbase = (int64_t)head * mpad + gr;
-  yhl[(rbase * 2 + 0) * D + d] = hi;
-  yhl[(rbase * 2 + 1) * D + d] = lo;
-  yf32[rbase * D + d] = y;
+  const float l = block_reduce(lpart, s_red, false);  // also orders the s_f writes
 
-  __shared__ float red[D / 64];
-  float sq = wave_sum(y * y);
-  if ((d & 63) == 0) red[d >> 6] = sq;
+  const int d = tid % D, grp = tid / D;
+  const float* py = part_y + (slot0 * kRows + row) * D + d;
+  float acc = 0.f;
+#pragma unroll 8
+  for (int s = grp; s < n_splits; s += G) acc += py[(int64_t)s * kRows * D] * s_f[s];
+  s_acc[grp][d] = acc;
   __syncthreads();
-  if (d == 0) {
-    float tot = 0.f;
-    for (int i = 0; i < D / 64; ++i) tot += red[i];
-    ystat[rbase * 2 + 0] = valid ? mx + log2f(fmaxf(l, 1e-40f)) : INFINITY;
-    ystat[rbase * 2 + 1] = tot;
+
+  const bool valid = gr < M && mx != -INFINITY;
+  float y = 0.f;
+  if (grp == 0) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < G; ++i) t += s_acc[i][d];
+    y = valid ? t / l : 0.f;
+    T hi, lo;
+    if (y_round) {
+      hi = static_cast<T>(y);
+      y = static_cast<float>(hi);
+      lo = static_cast<T>(0.f);
+    } else {
+      hi = static_cast<T>(y);
+      lo = static_cast<T>(y - static_cast<float>(hi));
+    }
+    const int64_t rbase = (int64_t)head * mpad + gr;
+    yhl[(rbase * 2 + 0) * D + d] = hi;
+    yhl[(rbase * 2 + 1) * D + d] = lo;
+    yf32[rbase * D + d] = y;
   }
+  const float yn2 = block_reduce(y * y, s_red, false);
+  if (tid == 0) {
+    const int64_t rbase = (int64_t)head * mpad + gr;
+    ystat[rbase * 2 + 0] = valid ? mx + log2f(fmaxf(l, 1e-40f)) : INFINITY;
+    ystat[rbase * 2 + 1] = yn2;
+  }
+  prof_end(prof, kStMerge);
 }
 
 // ---------------------------------------------------------------------------
@@ -363,7 +410,9 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
              const T* __restrict__ kp, const T* __restrict__ vp,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int cg, int n_splits, int kps,
              float scale_log2, float eps, int p_round,
-             const T* __restrict__ yhl, const float* __restrict__ ystat, float* __restrict__ scores) {
+             const T* __restrict__ yhl, const float* __restrict__ ystat, float* __restrict__ scores,
+             uint64_t* __restrict__ prof) {
+  prof_begin(prof, kStPass2);
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
   constexpr int OPS = 3 * kMB * KK;  // operand slots per row-chunk (Q, Yhi, Ylo)
@@ -506,6 +555,7 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
       }
     }
   }
+  prof_end(prof, kStPass2);
 }
 
 // ---------------------------------------------------------------------------
@@ -526,7 +576,7 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   const int target = 512;  // two resident workgroups on each of 256 CUs
   const int max_by_work = max(1, (int)(Lk / 256));
   int s1 = splits > 0 ? (int)splits : ceil_div(target, (int64_t)p.heads * p.n_mc);
-  s1 = max(1, min(s1, max_by_work));
+  s1 = max(1, min(min(s1, max_by_work), kMaxSplits));
   p.kps1 = ceil_div(ceil_div(Lk, s1), kTile) * kTile;
   p.s1 = ceil_div(Lk, p.kps1);
   int s2 = splits > 0 ? (int)splits : ceil_div(target, p.heads);
@@ -553,7 +603,7 @@ template <typename T, int D>
 static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
                                   int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk, int W,
                                   float eps, int p_round, int y_round, float* scores, char* ws,
-                                  hipStream_t st) {
+                                  uint32_t* zero_ptr, int64_t zero_words, hipStream_t st) {
   const float scale_log2 = 1.4426950408889634f / sqrtf((float)D);
   float* part_ml = reinterpret_cast<float*>(ws + p.off_ml);
   float* part_y = reinterpret_cast<float*>(ws + p.off_y);
@@ -564,25 +614,27 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   const T* kk = static_cast<const T*>(k);
   const T* vv = static_cast<const T*>(v);
 
+  uint64_t* prof = prof_slot();
   hipLaunchKernelGGL((pass1_kernel<T, D>), dim3(p.heads * p.n_mc * p.s1), dim3(kThreads), 0, st, qq, q_sb, q_sh,
                      q_ss, q_sd, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml,
-                     part_y);
-  hipLaunchKernelGGL((merge_kernel<T, D>), dim3(p.heads * p.mpad), dim3(D), 0, st, part_ml, part_y, p.n_mc,
-                     p.s1, p.M, y_round, yhl, ystat, yf);
+                     part_y, prof);
+  hipLaunchKernelGGL((merge_kernel<T, D>), dim3(p.heads * p.mpad), dim3(kMergeThreads), 0, st, part_ml, part_y,
+                     p.n_mc, p.s1, p.M, y_round, yhl, ystat, yf, zero_ptr, zero_words, prof);
   const int cg = min(p.n_mc, 2);
   const size_t lds2 = (size_t)cg * 3 * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
   hipLaunchKernelGGL((pass2_kernel<T, D>), dim3(p.heads * p.s2), dim3(kThreads), lds2, st, qq, q_sb, q_sh, q_ss,
                      q_sd, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round,
-                     yhl, ystat, scores);
+                     yhl, ystat, scores, prof);
   return hipGetLastError();
 }
 
 hipError_t launch_scores(const ScorePlan& p, int dtype_bf16, int D, const void* q, int64_t q_sb, int64_t q_sh,
                          int64_t q_ss, int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk,
-                         int W, float eps, int p_round, int y_round, float* scores, char* ws, hipStream_t st) {
+                         int W, float eps, int p_round, int y_round, float* scores, char* ws, uint32_t* zero_ptr,
+                         int64_t zero_words, hipStream_t st) {
 #define DKV_CASE(TT, DD)                                                                                     \
   return launch_scores_t<TT, DD>(p, q, q_sb, q_sh, q_ss, q_sd, k, v, Hkv, Lq, Lk, W, eps, p_round, y_round, \
-                                 scores, ws, st)
+                                 scores, ws, zero_ptr, zero_words, st)
   if (dtype_bf16) {
     if (D == 64) DKV_CASE(__bf16, 64);
     if (D == 128) DKV_CASE(__bf16, 128);

@@ -36,15 +36,18 @@ struct SelectWs {
 };
 
 __global__ void __launch_bounds__(kPoolThreads)
-sel_zero_kernel(uint32_t* __restrict__ p, int64_t n) {
+sel_zero_kernel(uint32_t* __restrict__ p, int64_t n, uint64_t* __restrict__ prof) {
+  prof_begin(prof, kStSelZero);
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     p[i] = 0u;
+  prof_end(prof, kStSelZero);
 }
 
 // Stage 1: grid = rows * ceil(Lk / kPoolChunk).
 __global__ void __launch_bounds__(kPoolThreads)
 sel_pool_kernel(const float* __restrict__ scores, int Lk, int ks, int window, int chunks,
-                float* __restrict__ pooled, uint32_t* __restrict__ rowws) {
+                float* __restrict__ pooled, uint32_t* __restrict__ rowws, uint64_t* __restrict__ prof) {
+  prof_begin(prof, kStSelPool);
   __shared__ uint32_t hist[kBins1];
   __shared__ uint32_t wmax[kPoolThreads / 64];
   const int row = blockIdx.x / chunks;
@@ -76,6 +79,7 @@ sel_pool_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
   }
   for (int i = threadIdx.x; i < kBins1; i += kPoolThreads)
     if (hist[i]) atomicAdd(&rw[1 + i], hist[i]);
+  prof_end(prof, kStSelPool);
 }
 
 // Inclusive suffix sums over `n` bins of `hist` (in place, n <= 2048) with
@@ -123,7 +127,8 @@ template <bool LDS_KEYS>
 __global__ void __launch_bounds__(kSelThreads)
 sel_topk_kernel(const float* __restrict__ pooled_in, int Lk, int window, int keep,
                 const uint32_t* __restrict__ rowws, uint32_t* __restrict__ gkeys,
-                int64_t* __restrict__ out_idx, float* __restrict__ pooled_out) {
+                int64_t* __restrict__ out_idx, float* __restrict__ pooled_out, uint64_t* __restrict__ prof) {
+  prof_begin(prof, kStSelTopk);
   extern __shared__ uint32_t dyn[];
   __shared__ uint32_t hist[kBins2];
   __shared__ uint32_t wsum[kSelWaves];
@@ -254,6 +259,7 @@ sel_topk_kernel(const float* __restrict__ pooled_in, int Lk, int window, int kee
     }
     __syncthreads();
   }
+  prof_end(prof, kStSelTopk);
 }
 
 size_t select_workspace_bytes(int64_t rows, int64_t Lk) {
@@ -264,20 +270,25 @@ size_t select_workspace_bytes(int64_t rows, int64_t Lk) {
   return b;
 }
 
+int64_t select_zero_words(int64_t rows) { return rows * SelectWs::kRowWords; }
+
 hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int window, int keep, int64_t* out_idx,
-                         float* pooled_out, char* ws, hipStream_t st) {
+                         float* pooled_out, char* ws, bool pre_zeroed, hipStream_t st) {
   uint32_t* rowws = reinterpret_cast<uint32_t*>(ws);
   size_t off = ((size_t)rows * SelectWs::kRowWords * 4 + 255) & ~size_t(255);
   float* pooled = reinterpret_cast<float*>(ws + off);
   off += ((size_t)rows * Lk * 4 + 255) & ~size_t(255);
   uint32_t* gkeys = reinterpret_cast<uint32_t*>(ws + off);
 
-  const int64_t zn = (int64_t)rows * SelectWs::kRowWords;
-  hipLaunchKernelGGL(sel_zero_kernel, dim3((unsigned)std::min<int64_t>((zn + 255) / 256, 1024)), dim3(256), 0, st,
-                     rowws, zn);
+  uint64_t* prof = prof_slot();
+  if (!pre_zeroed) {
+    const int64_t zn = (int64_t)rows * SelectWs::kRowWords;
+    hipLaunchKernelGGL(sel_zero_kernel, dim3((unsigned)std::min<int64_t>((zn + 255) / 256, 1024)), dim3(256), 0, st,
+                       rowws, zn, prof);
+  }
   const int chunks = (Lk + kPoolChunk - 1) / kPoolChunk;
   hipLaunchKernelGGL(sel_pool_kernel, dim3(rows * chunks), dim3(kPoolThreads), 0, st, scores, Lk, ks, window,
-                     chunks, pooled, rowws);
+                     chunks, pooled, rowws, prof);
   if (Lk <= kLdsKeys) {
     static bool attr_set = false;
     if (!attr_set) {
@@ -287,10 +298,10 @@ hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int wind
       attr_set = true;
     }
     hipLaunchKernelGGL((sel_topk_kernel<true>), dim3(rows), dim3(kSelThreads), (size_t)Lk * 4, st, pooled, Lk,
-                       window, keep, rowws, gkeys, out_idx, pooled_out);
+                       window, keep, rowws, gkeys, out_idx, pooled_out, prof);
   } else {
     hipLaunchKernelGGL((sel_topk_kernel<false>), dim3(rows), dim3(kSelThreads), 0, st, pooled, Lk, window, keep,
-                       rowws, gkeys, out_idx, pooled_out);
+                       rowws, gkeys, out_idx, pooled_out, prof);
   }
   return hipGetLastError();
 }

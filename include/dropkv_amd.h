@@ -137,6 +137,24 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
                  float* scores, int64_t* keep_idx, void* k_out, void* v_out,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* Kernel-time profiler for dropkv_evict (no counterpart in the reference,
+ * which has no timers).  dropkv_profile_begin(n) allocates n device slots and
+ * arms recording for the next n dropkv_evict calls in this process: each of
+ * those calls first clears its slot, then every kernel it launches records its
+ * first-workgroup start and last-workgroup end from the GPU wall clock.  A
+ * call captured into a HIP graph re-records its slot on every replay.
+ * Stage order: pass-1 partials, merge, pass-2 scores, select-clear (folded
+ * into the merge in dropkv_evict, so 0), select-pool, select-top-k, compact;
+ * element 7 is the span from the first kernel start to the last kernel end.
+ *   dropkv_profile_read(slot, ms[8])   waits for the device, reads one slot
+ *   dropkv_profile_disarm()            stop recording new slots
+ *   dropkv_profile_end(ms[8], calls)   sum over recorded slots, then free
+ * Not thread-safe against concurrent dropkv_evict calls. */
+int dropkv_profile_begin(int64_t max_calls);
+int dropkv_profile_read(int64_t slot, double* stage_ms);
+int dropkv_profile_disarm(void);
+int dropkv_profile_end(double* stage_ms, int64_t* calls);
+
 /* Self-test of the matrix-core operand layout the kernels assume: computes a
  * 16x16 fp32 product of fixed bf16 patterns with one MFMA and writes it to
  * `out` (256 floats, device memory), row-major. */
