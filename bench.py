@@ -26,7 +26,7 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0
-STAGES = ("pass1_partials", "merge", "pass2_scores", "select_clear", "select_pool", "select_topk", "compact")
+STAGES = ("pass1_partials", "merge", "pass2_scores", "select_final", "select_pool", "select_cand", "emit_compact")
 
 WORKLOADS = {
     "llama8b_layer_32k": dict(B=1, Hq=32, Hkv=8, D=128, Lq=32768, Lk=32768, window=8, kernel=11, ratio=0.1,
@@ -93,6 +93,8 @@ def main():
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (20 times), to calibrate HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the eviction path "
@@ -101,6 +103,17 @@ def main():
 
     import torch
     from dropkv_amd import _lib, ops
+
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        a = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        b = torch.empty_like(a)
+        for _ in range(20):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4,
+                          "launches": 20}))
+        return
 
     cfg = WORKLOADS[args.workload]
     B, Hq, Hkv, D, Lq, Lk, W = (cfg[k] for k in ("B", "Hq", "Hkv", "D", "Lq", "Lk", "window"))

@@ -165,8 +165,9 @@ static int check_select_args(const float* scores, int64_t rows, int64_t Lk, int6
   if (!scores || !keep_idx) return fail(DROPKV_E_ARG, "null scores/keep_idx pointer");
   if (rows < 1 || Lk < 1) return fail(DROPKV_E_ARG, "rows and Lk must be positive");
   if (rows > 65535 * 64) return fail(DROPKV_E_UNSUPPORTED, "too many rows");
-  if (Lk > kMaxLk) return fail(DROPKV_E_UNSUPPORTED, "Lk (%lld) too large", (long long)Lk);
+  if (Lk > dkv::select_max_len()) return fail(DROPKV_E_UNSUPPORTED, "Lk (%lld) too large", (long long)Lk);
   if (ks < 1 || ks % 2 == 0) return fail(DROPKV_E_ARG, "kernel_size must be a positive odd integer");
+  if (ks > 129) return fail(DROPKV_E_UNSUPPORTED, "kernel_size above 129 is not supported");
   if (window < 0 || window > Lk) return fail(DROPKV_E_ARG, "window must be in [0, Lk]");
   if (keep < 1 || keep > Lk) return fail(DROPKV_E_ARG, "keep (%lld) must be in [1, Lk=%lld]", (long long)keep,
                                          (long long)Lk);
@@ -182,7 +183,8 @@ int dropkv_select(const float* scores, int64_t rows, int64_t Lk, int64_t kernel_
   if (!workspace || workspace_bytes < need)
     return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
   return hip_status(dkv::launch_select(scores, (int)rows, (int)Lk, (int)kernel_size, (int)window, (int)keep, keep_idx,
-                                       pooled, static_cast<char*>(workspace), false, static_cast<hipStream_t>(stream)),
+                                       pooled, static_cast<char*>(workspace), false, nullptr,
+                                       static_cast<hipStream_t>(stream)),
                     "dropkv_select launch");
 }
 
@@ -263,9 +265,14 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
                                     (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws,
                                     reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv), st);
   if (e != hipSuccess) return hip_status(e, "dropkv_evict scores");
+  // The gather runs inside the selection's emit stage when the rows allow
+  // 16-byte copies; otherwise as its own kernel.
+  const bool fuse = (D * 2) % 16 == 0 && aligned16(k_out) && aligned16(v_out);
+  const dkv::SelectCompact cp{k, v, Hkv * Lk * D, Lk * D, D, 2, D, (int)Hkv, k_out, v_out};
   e = dkv::launch_select(sc, (int)(B * Hkv), (int)Lk, (int)kernel_size, (int)protect_window, (int)keep, keep_idx,
-                         nullptr, sel_ws, true, st);
+                         nullptr, sel_ws, true, fuse ? &cp : nullptr, st);
   if (e != hipSuccess) return hip_status(e, "dropkv_evict select");
+  if (fuse) return DROPKV_OK;
   e = dkv::launch_compact(k, v, Hkv * Lk * D, Lk * D, D, Lk, nullptr, nullptr, 0, 0, 0, 0, 2, B, Hkv, D, keep_idx,
                           keep, k_out, v_out, st);
   return hip_status(e, "dropkv_evict compact");

@@ -18,6 +18,10 @@ struct Seg {
   int64_t len;
 };
 
+// Each thread copies up to kItems (row, unit) pieces per round with every
+// index load, then every data load, in flight before the stores.
+constexpr int kItems = 4;
+
 template <typename U>
 __global__ void __launch_bounds__(kCopyThreads)
 compact_kernel(Seg s0, Seg s1, int H, int units_per_row, const int64_t* __restrict__ idx, int keep,
@@ -28,28 +32,39 @@ compact_kernel(Seg s0, Seg s1, int H, int units_per_row, const int64_t* __restri
   const int r0 = (blockIdx.x % blocks_per_head) * kRowsPerBlock;
   const int b = bh / H, h = bh % H;
   const int64_t out_row_bytes = (int64_t)units_per_row * sizeof(U);
-  const int total = kRowsPerBlock * units_per_row;
-  for (int t = threadIdx.x; t < total; t += kCopyThreads) {
-    const int r = r0 + t / units_per_row;
-    const int u = t % units_per_row;
-    if (r >= keep) break;
-    const int64_t src = idx[(int64_t)bh * keep + r];
-    U kval, vval;
-    if (src >= 0 && src < s0.len) {
-      const int64_t off = b * s0.sb + h * s0.sh + src * s0.sl;
-      kval = reinterpret_cast<const U*>(s0.k + off)[u];
-      vval = reinterpret_cast<const U*>(s0.v + off)[u];
-    } else if (src >= s0.len && src < s0.len + s1.len) {
-      const int64_t off = b * s1.sb + h * s1.sh + (src - s0.len) * s1.sl;
-      kval = reinterpret_cast<const U*>(s1.k + off)[u];
-      vval = reinterpret_cast<const U*>(s1.v + off)[u];
-    } else {
-      kval = U{};
-      vval = U{};
+  const int total = min(kRowsPerBlock, keep - r0) * units_per_row;
+  for (int t0 = threadIdx.x; t0 < total; t0 += kItems * kCopyThreads) {
+    int64_t src[kItems];
+#pragma unroll
+    for (int q = 0; q < kItems; ++q) {
+      const int t = t0 + q * kCopyThreads;
+      src[q] = t < total ? idx[(int64_t)bh * keep + r0 + t / units_per_row] : -1;
     }
-    const int64_t o = ((int64_t)bh * keep + r) * out_row_bytes;
-    reinterpret_cast<U*>(ko + o)[u] = kval;
-    reinterpret_cast<U*>(vo + o)[u] = vval;
+    U kval[kItems], vval[kItems];
+#pragma unroll
+    for (int q = 0; q < kItems; ++q) {
+      const int u = (t0 + q * kCopyThreads) % units_per_row;
+      kval[q] = U{};
+      vval[q] = U{};
+      if (src[q] >= 0 && src[q] < s0.len) {
+        const int64_t off = b * s0.sb + h * s0.sh + src[q] * s0.sl;
+        kval[q] = reinterpret_cast<const U*>(s0.k + off)[u];
+        vval[q] = reinterpret_cast<const U*>(s0.v + off)[u];
+      } else if (src[q] >= s0.len && src[q] < s0.len + s1.len) {
+        const int64_t off = b * s1.sb + h * s1.sh + (src[q] - s0.len) * s1.sl;
+        kval[q] = reinterpret_cast<const U*>(s1.k + off)[u];
+        vval[q] = reinterpret_cast<const U*>(s1.v + off)[u];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kItems; ++q) {
+      const int t = t0 + q * kCopyThreads;
+      if (t < total) {
+        const int64_t o = ((int64_t)bh * keep + r0 + t / units_per_row) * out_row_bytes;
+        reinterpret_cast<U*>(ko + o)[t % units_per_row] = kval[q];
+        reinterpret_cast<U*>(vo + o)[t % units_per_row] = vval[q];
+      }
+    }
   }
   prof_end(prof, kStCompact);
 }

@@ -12,6 +12,8 @@ namespace dkv {
 // device buffer of 2*kNumStages uint64 (per stage: first-workgroup start,
 // last-workgroup end, in wall-clock ticks) that the kernels update; otherwise
 // nullptr and the kernels skip the bookkeeping.
+// (kStSelZero times both the standalone workspace clear and the per-row
+// threshold stage; only one of them runs in a fused layer-call.)
 enum Stage { kStPass1 = 0, kStMerge, kStPass2, kStSelZero, kStSelPool, kStSelTopk, kStCompact, kNumStages };
 uint64_t* prof_slot();
 
@@ -20,6 +22,7 @@ struct ScorePlan {
   int heads, g, M, n_mc, mpad;
   int s1, kps1;  // pass 1: splits per (head, row-chunk), keys per split
   int s2, kps2;  // pass 2: splits per head, keys per split
+  int p1_waves, p1_occ, p2_waves;  // launch shapes
   size_t off_ml, off_y, off_yhl, off_stat, off_yf, total;
 };
 
@@ -36,8 +39,21 @@ size_t select_workspace_bytes(int64_t rows, int64_t Lk);
 // Words at the start of the selection workspace that must be zero on entry
 // (cleared by launch_select itself unless the caller already did it).
 int64_t select_zero_words(int64_t rows);
+// Longest row the selection kernels take.
+int64_t select_max_len();
+// Optional K/V gather fused into the selection's emit stage: rows of
+// [B, H, L, D] sources (element strides s_b, s_h, s_l; D contiguous; 16-byte
+// aligned rows) go to contiguous [B, H, keep, D] outputs.
+struct SelectCompact {
+  const void* k;
+  const void* v;
+  int64_t s_b, s_h, s_l, elem_bytes, D;
+  int H;
+  void* k_out;
+  void* v_out;
+};
 hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int window, int keep, int64_t* out_idx,
-                         float* pooled_out, char* ws, bool pre_zeroed, hipStream_t st);
+                         float* pooled_out, char* ws, bool pre_zeroed, const SelectCompact* cp, hipStream_t st);
 
 hipError_t launch_compact(const void* k0, const void* v0, int64_t s0b, int64_t s0h, int64_t s0l, int64_t L0,
                           const void* k1, const void* v1, int64_t s1b, int64_t s1h, int64_t s1l, int64_t L1,

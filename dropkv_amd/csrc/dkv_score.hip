@@ -23,10 +23,12 @@
 #include "dkv_common.h"
 #include "dkv_internal.h"
 
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
 namespace dkv {
 
-constexpr int kWaves = 4;           // waves per workgroup
-constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 32;           // keys per wave tile
 constexpr int kRows = 32;           // query rows per row-chunk (2 MFMA row blocks)
 constexpr int kMB = kRows / 16;
@@ -76,13 +78,50 @@ __device__ __forceinline__ void load_q_ops(typename Elem<T>::v8 (&qop)[D / 32], 
 }
 
 // ---------------------------------------------------------------------------
+// Tile loads shared by the two passes.
+// ---------------------------------------------------------------------------
+// 32 key rows as an MFMA A operand: lane (li, lg) holds row t0+16kb+li,
+// head-dim columns 32kk+8lg .. +7.  Rows past Lk are clamped (and masked by
+// the caller).
+template <typename T, int D>
+__device__ __forceinline__ void load_rows_op(typename Elem<T>::v8 (&op)[2][D / 32], const T* __restrict__ base,
+                                             int t0, int Lk, int li, int lg) {
+  typedef typename Elem<T>::v8 v8;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int n = min(t0 + 16 * kb + li, Lk - 1);
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) op[kb][kk] = *reinterpret_cast<const v8*>(base + (int64_t)n * D + 32 * kk + 8 * lg);
+  }
+}
+
+// 32 value rows in coalesced 16-byte chunks, two adjacent keys per lane
+// (pairs p, chunk c) for the transposed LDS tile.
+template <typename T, int D>
+__device__ __forceinline__ void load_v_pairs(u32x4 (&va)[(kTile / 2) / (64 / (D / 8))],
+                                             u32x4 (&vb)[(kTile / 2) / (64 / (D / 8))], const T* __restrict__ Vh,
+                                             int t0, int Lk, int lane) {
+  constexpr int CPR = D / 8, GRP = 64 / CPR, NIT = (kTile / 2) / GRP;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int p = it * GRP + lane / CPR;
+    const int c = lane % CPR;
+    const int n0 = min(t0 + 2 * p, Lk - 1), n1 = min(t0 + 2 * p + 1, Lk - 1);
+    va[it] = *reinterpret_cast<const u32x4*>(Vh + (int64_t)n0 * D + 8 * c);
+    vb[it] = *reinterpret_cast<const u32x4*>(Vh + (int64_t)n1 * D + 8 * c);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Pass 1: split-K flash partials.  Workgroup = (head, row-chunk, key split);
-// each wave streams its own 32-key tiles; the four waves are merged in LDS at
-// the end.  Output per (head, chunk, split, row): running max (log2 domain),
+// each of its WAVES waves streams its own 32-key tiles, issuing the loads of
+// its next tile as soon as the current tile's K/V registers are consumed, so
+// they overlap the softmax and P.V work.  The waves are merged in LDS at the
+// end.  Output per (head, chunk, split, row): running max (log2 domain),
 // running sum, and the unnormalised fp32 y row.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
-__global__ void __launch_bounds__(kThreads, 2)
+template <typename T, int D, int WAVES, int MINW>
+__global__ void __launch_bounds__(64 * WAVES, MINW)
 pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
              const T* __restrict__ kp, const T* __restrict__ vp,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int n_splits, int kps,
@@ -95,8 +134,9 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   constexpr int CPR = D / 8;           // 16-byte chunks per key row
   constexpr int GRP = 64 / CPR;        // key pairs covered per load round
   constexpr int NIT = (kTile / 2) / GRP;
+  constexpr int NT = 64 * WAVES;
 
-  __shared__ uint32_t lds[kWaves * D * kPitch];
+  __shared__ uint32_t lds[WAVES * D * kPitch];
 
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   const int mc = lid % n_mc;
@@ -115,6 +155,10 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     load_q_ops<T, D>(qop[mb], q, q_sb, q_sh, q_ss, q_sd, b, hkv, g, W, Lq, M, m, lg);
     bound[mb] = row_bound(m, M, W, Lk);
   }
+  // Tiles wholly below every row's causal bound need no masking (unless this
+  // chunk holds padding rows).
+  const bool pad_chunk = mc * kRows + kRows > M;
+  const int unmasked_end = Lk - W + 1;
 
   const int64_t hoff = (int64_t)head * Lk * D;
   const T* __restrict__ Kh = kp + hoff;
@@ -134,27 +178,14 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   const int k_begin = split * kps;
   const int k_end = min(k_begin + kps, Lk);
 
-  for (int t0 = k_begin + wv * kTile; t0 < k_end; t0 += kWaves * kTile) {
-    // K rows as the A operand: lane (li, lg) holds K[t0+16kb+li][32kk+8lg .. +7].
-    v8 kop[2][KK];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int n = min(t0 + 16 * kb + li, Lk - 1);
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk)
-        kop[kb][kk] = *reinterpret_cast<const v8*>(Kh + (int64_t)n * D + 32 * kk + 8 * lg);
-    }
-    // V rows in coalesced 16-byte chunks, two adjacent keys per lane.
-    u32x4 va[NIT], vb[NIT];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int p = it * GRP + lane / CPR;
-      const int c = lane % CPR;
-      const int n0 = min(t0 + 2 * p, Lk - 1), n1 = min(t0 + 2 * p + 1, Lk - 1);
-      va[it] = *reinterpret_cast<const u32x4*>(Vh + (int64_t)n0 * D + 8 * c);
-      vb[it] = *reinterpret_cast<const u32x4*>(Vh + (int64_t)n1 * D + 8 * c);
-    }
-
+  v8 kop[2][KK];
+  u32x4 va[NIT], vb[NIT];
+  int t0 = k_begin + wv * kTile;
+  if (t0 < k_end) {
+    load_rows_op<T, D>(kop, Kh, t0, Lk, li, lg);
+    load_v_pairs<T, D>(va, vb, Vh, t0, Lk, lane);
+  }
+  for (; t0 < k_end; t0 += WAVES * kTile) {
     // S^T = K Q^T.
     f32x4 s[2][kMB];
 #pragma unroll
@@ -184,7 +215,15 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
       }
     }
 
+    // The K/V registers are free again: start the next tile's loads now.
+    const int tn = t0 + WAVES * kTile;
+    if (tn < k_end) {
+      load_rows_op<T, D>(kop, Kh, tn, Lk, li, lg);
+      load_v_pairs<T, D>(va, vb, Vh, tn, Lk, lane);
+    }
+
     // Online softmax (base 2) for each row block; P hi/lo split for the MFMA.
+    const bool masked = pad_chunk || t0 + kTile > unmasked_end;
     v8 phi[kMB], plo[kMB];
 #pragma unroll
     for (int mb = 0; mb < kMB; ++mb) {
@@ -193,8 +232,8 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int n = t0 + 16 * kb + 4 * lg + r;
-          const float x = n <= bound[mb] ? s[kb][mb][r] * scale_log2 : -INFINITY;
+          float x = s[kb][mb][r] * scale_log2;
+          if (masked) x = (t0 + 16 * kb + 4 * lg + r) <= bound[mb] ? x : -INFINITY;
           s[kb][mb][r] = x;
           tmax = fmaxf(tmax, x);
         }
@@ -216,8 +255,11 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
         }
       lsum[mb] = lsum[mb] * alpha + psum;
       m2[mb] = mnew;
+      // Rescale only when some row's maximum moved (rare after a few tiles).
+      if (__any(alpha != 1.f)) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= alpha;
+        for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= alpha;
+      }
     }
 
     // Y^T += V^T P^T.  Lane (li, lg) reads V^T[16dt+li][keys 4lg..4lg+3, 16+4lg..+3].
@@ -246,8 +288,8 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   // Cross-wave merge in LDS (the V tiles are dead now).
   __syncthreads();
   float* sm_m = reinterpret_cast<float*>(lds);
-  float* sm_l = sm_m + kWaves * kRows;
-  float* ybuf = sm_l + kWaves * kRows;  // [kRows][D]
+  float* sm_l = sm_m + WAVES * kRows;
+  float* ybuf = sm_l + WAVES * kRows;  // [kRows][D]
   if (lg == 0) {
 #pragma unroll
     for (int mb = 0; mb < kMB; ++mb) {
@@ -261,12 +303,12 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     const int row = 16 * mb + li;
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, sm_m[w * kRows + row]);
+    for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, sm_m[w * kRows + row]);
     const float f = (mx == -INFINITY) ? 0.f : exp2f(m2[mb] - mx);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= f;
   }
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < WAVES; ++w) {
     if (wv == w) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
@@ -285,15 +327,15 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   if (threadIdx.x < kRows) {
     const int row = threadIdx.x;
     float mx = -INFINITY;
-    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, sm_m[w * kRows + row]);
+    for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, sm_m[w * kRows + row]);
     float l = 0.f;
     if (mx != -INFINITY)
-      for (int w = 0; w < kWaves; ++w) l += sm_l[w * kRows + row] * exp2f(sm_m[w * kRows + row] - mx);
+      for (int w = 0; w < WAVES; ++w) l += sm_l[w * kRows + row] * exp2f(sm_m[w * kRows + row] - mx);
     part_ml[(slot * kRows + row) * 2 + 0] = mx;
     part_ml[(slot * kRows + row) * 2 + 1] = l;
   }
   float* py = part_y + slot * kRows * D;
-  for (int i = threadIdx.x; i < kRows * D; i += kThreads) py[i] = ybuf[i];
+  for (int i = threadIdx.x; i < kRows * D; i += NT) py[i] = ybuf[i];
   prof_end(prof, kStPass1);
 }
 
@@ -397,15 +439,40 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2: per-key score.  Workgroup = (head, key split); each wave streams 32
-// key tiles, recomputes S^T = K Q^T and G^T = V Y^T (Y as hi+lo), and folds
-// w * dist2 over all query rows.  The Q^T / Y^T operands of up to `cg`
-// row-chunks are staged in LDS in per-lane order (one conflict-free 16-byte
-// read per operand); more row-chunks than that are processed in groups, the
-// partial per-key sums being carried in the output array.
+// Pass 2: per-key score.  Workgroup = (head, key split); each of its WAVES
+// waves streams 32-key tiles, recomputes S^T = K Q^T and G^T = V Y^T (Y as
+// hi+lo) and folds w * dist2 over all query rows.  The next tile's loads are
+// issued right after the last MFMA of the current tile, overlapping the
+// per-element work.  The Q^T / Y^T operands of up to `cg` row-chunks are
+// staged in LDS in per-lane order (one conflict-free 16-byte read per
+// operand); more row-chunks are processed in groups, the partial per-key sums
+// being carried in the output array.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
-__global__ void __launch_bounds__(kThreads, 2)
+template <typename T>
+__device__ __forceinline__ float sumsq8(typename Elem<T>::v8 x, float acc);
+template <>
+__device__ __forceinline__ float sumsq8<__bf16>(Elem<__bf16>::v8 x, float acc) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const bf2 t = {x[e], x[e + 1]};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(t, t, acc, false);
+  }
+  return acc;
+}
+template <>
+__device__ __forceinline__ float sumsq8<_Float16>(Elem<_Float16>::v8 x, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const h2 t = {x[e], x[e + 1]};
+    acc = __builtin_amdgcn_fdot2(t, t, acc, false);
+  }
+  return acc;
+}
+
+template <typename T, int D, int WAVES, int MINW>
+__global__ void __launch_bounds__(64 * WAVES, MINW)
 pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
              const T* __restrict__ kp, const T* __restrict__ vp,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int cg, int n_splits, int kps,
@@ -416,6 +483,7 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
   constexpr int OPS = 3 * kMB * KK;  // operand slots per row-chunk (Q, Yhi, Ylo)
+  constexpr int NT = 64 * WAVES;
   extern __shared__ u32x4 opnd[];    // [cg][OPS][64] then float stats [cg][kMB][2][16]
   float* stat = reinterpret_cast<float*>(opnd + (size_t)cg * OPS * 64);
 
@@ -433,12 +501,14 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   const float inv_g = 1.0f / static_cast<float>(g);
   const int k_begin = split * kps;
   const int k_end = min(k_begin + kps, Lk);
+  const bool pad_rows = mpad > M;
+  const int unmasked_end = Lk - W + 1;
 
   for (int c0 = 0; c0 < n_mc; c0 += cg) {
     const int cn = min(cg, n_mc - c0);
     const bool first = c0 == 0, last = c0 + cn >= n_mc;
     __syncthreads();
-    for (int slot = wv; slot < cn * OPS; slot += kWaves) {
+    for (int slot = wv; slot < cn * OPS; slot += WAVES) {
       const int c = slot / OPS, o = slot % OPS;
       const int which = o / (kMB * KK), mb = (o / KK) % kMB, kk = o % KK;
       const int m = (c0 + c) * kRows + mb * 16 + li;
@@ -451,7 +521,7 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
       }
       opnd[(size_t)slot * 64 + lane] = __builtin_bit_cast(u32x4, val);
     }
-    for (int t = threadIdx.x; t < cn * kMB * 16; t += kThreads) {
+    for (int t = threadIdx.x; t < cn * kMB * 16; t += NT) {
       const int c = t / (kMB * 16), r = t % (kMB * 16);
       const int64_t rbase = (int64_t)head * mpad + (c0 + c) * kRows + r;
       stat[(c * kMB + r / 16) * 32 + (r % 16)] = ystat[rbase * 2 + 0];
@@ -459,38 +529,28 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     }
     __syncthreads();
 
-    for (int t0 = k_begin + wv * kTile; t0 < k_end; t0 += kWaves * kTile) {
-      // Keep the LDS operand reads inside the loop (hoisting them all out
-      // would need more registers than the kernel has).
-      asm volatile("" ::: "memory");
-      v8 kop[2][KK], vop[2][KK];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int n = min(t0 + 16 * kb + li, Lk - 1);
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          kop[kb][kk] = *reinterpret_cast<const v8*>(Kh + (int64_t)n * D + 32 * kk + 8 * lg);
-          vop[kb][kk] = *reinterpret_cast<const v8*>(Vh + (int64_t)n * D + 32 * kk + 8 * lg);
-        }
-      }
-      // |v|^2 of key t0+16kb+li (fp32 from the exact operand values), then
+    v8 kop[2][KK], vop[2][KK];
+    int t0 = k_begin + wv * kTile;
+    if (t0 < k_end) {
+      load_rows_op<T, D>(kop, Kh, t0, Lk, li, lg);
+      load_rows_op<T, D>(vop, Vh, t0, Lk, li, lg);
+    }
+    for (; t0 < k_end; t0 += WAVES * kTile) {
+      // |v|^2 of key t0+16kb+li (fp32 dot of the exact operand values), then
       // redistributed to the result layout (keys 16kb+4lg+r).
       float vn2[2][4];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         float part = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float x = static_cast<float>(vop[kb][kk][e]);
-            part += x * x;
-          }
+        for (int kk = 0; kk < KK; ++kk) part = sumsq8<T>(vop[kb][kk], part);
         part += __shfl_xor(part, 16);
         part += __shfl_xor(part, 32);
 #pragma unroll
         for (int r = 0; r < 4; ++r) vn2[kb][r] = __shfl(part, 4 * lg + r);
       }
+      const bool masked = pad_rows || t0 + kTile > unmasked_end;
+      const int tn = t0 + WAVES * kTile;
 
       float sc[2][4];
 #pragma unroll
@@ -499,36 +559,53 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
         for (int r = 0; r < 4; ++r) sc[kb][r] = 0.f;
 
       for (int c = 0; c < cn; ++c) {
+        f32x4 sacc[2][kMB], gacc[2][kMB];
+        const u32x4* ob = opnd + (size_t)(c * OPS) * 64 + lane;
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            sacc[kb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            gacc[kb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) {
+            const v8 qo = __builtin_bit_cast(v8, ob[(size_t)((0 * kMB + mb) * KK + kk) * 64]);
+            const v8 yh = __builtin_bit_cast(v8, ob[(size_t)((1 * kMB + mb) * KK + kk) * 64]);
+            const v8 yl = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+              sacc[kb][mb] = Elem<T>::mfma(kop[kb][kk], qo, sacc[kb][mb]);
+              gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], yh, gacc[kb][mb]);
+              gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], yl, gacc[kb][mb]);
+            }
+          }
+        // After the last row-chunk's MFMAs the K/V registers are free: start
+        // the next tile's loads.
+        if (c == cn - 1 && tn < k_end) {
+          load_rows_op<T, D>(kop, Kh, tn, Lk, li, lg);
+          load_rows_op<T, D>(vop, Vh, tn, Lk, li, lg);
+        }
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb) {
           const int m = (c0 + c) * kRows + mb * 16 + li;
           const int bound = row_bound(m, M, W, Lk);
           const float lse2 = stat[(c * kMB + mb) * 32 + li];
           const float yn2 = stat[(c * kMB + mb) * 32 + 16 + li];
-          const u32x4* ob = opnd + (size_t)(c * OPS) * 64 + lane;
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb) {
-            f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, gacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-              const v8 qo = __builtin_bit_cast(v8, ob[(size_t)((0 * kMB + mb) * KK + kk) * 64]);
-              const v8 yh = __builtin_bit_cast(v8, ob[(size_t)((1 * kMB + mb) * KK + kk) * 64]);
-              const v8 yl = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
-              sacc = Elem<T>::mfma(kop[kb][kk], qo, sacc);
-              gacc = Elem<T>::mfma(vop[kb][kk], yh, gacc);
-              gacc = Elem<T>::mfma(vop[kb][kk], yl, gacc);
-            }
+          for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int n = t0 + 16 * kb + 4 * lg + r;
-              float p = n <= bound ? exp2f(sacc[r] * scale_log2 - lse2) : 0.f;
-              p = fminf(fmaxf(p, 0.f), 1.f);
+              float p = exp2f(sacc[kb][mb][r] * scale_log2 - lse2);
+              if (masked) p = (t0 + 16 * kb + 4 * lg + r) <= bound ? p : 0.f;
+              p = fminf(p, 1.f);
               if (p_round) p = round_through<T>(p);
-              const float ratio = p / (1.0f - p + eps);
-              const float dist2 = fmaxf(vn2[kb][r] - 2.0f * gacc[r] + yn2, 0.f);
+              const float ratio = p * __builtin_amdgcn_rcpf(1.0f - p + eps);
+              const float dist2 = fmaxf(vn2[kb][r] - 2.0f * gacc[kb][mb][r] + yn2, 0.f);
               sc[kb][r] += ratio * ratio * dist2;
             }
-          }
         }
       }
 
@@ -565,21 +642,51 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 
 static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
+// Launch-shape tuning.  Defaults come from sweeps on MI355X; the
+// DROPKV_TUNE environment variable ("p1w=8,p1occ=1,p2w=4,s1=32,s2=32",
+// any subset) overrides them for experiments.
+struct Tune {
+  int p1w = 4, p1occ = 1, p2w = 4, s1 = 0, s2 = 0, target = 256;
+};
+static Tune read_tune() {
+  Tune t;
+  const char* e = getenv("DROPKV_TUNE");
+  if (!e) return t;
+  char key[16];
+  int val, n = 0;
+  while (sscanf(e, " %15[a-z0-9_]=%d%n", key, &val, &n) == 2) {
+    if (!strcmp(key, "p1w")) t.p1w = val;
+    else if (!strcmp(key, "p1occ")) t.p1occ = val;
+    else if (!strcmp(key, "p2w")) t.p2w = val;
+    else if (!strcmp(key, "s1")) t.s1 = val;
+    else if (!strcmp(key, "s2")) t.s2 = val;
+    else if (!strcmp(key, "target")) t.target = val;
+    e += n;
+    if (*e == ',') ++e;
+    n = 0;
+  }
+  return t;
+}
+
 ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W,
                           int64_t splits) {
+  static const Tune tune = read_tune();
   ScorePlan p;
   p.heads = (int)(B * Hkv);
   p.g = (int)(Hq / Hkv);
   p.M = p.g * (int)W;
   p.n_mc = ceil_div(p.M, kRows);
   p.mpad = p.n_mc * kRows;
-  const int target = 512;  // two resident workgroups on each of 256 CUs
+  p.p1_waves = tune.p1w == 8 ? 8 : 4;
+  p.p1_occ = tune.p1occ == 2 ? 2 : 1;
+  p.p2_waves = tune.p2w == 8 ? 8 : 4;
+  const int target = max(1, tune.target);  // workgroups per pass (one per CU)
   const int max_by_work = max(1, (int)(Lk / 256));
-  int s1 = splits > 0 ? (int)splits : ceil_div(target, (int64_t)p.heads * p.n_mc);
+  int s1 = splits > 0 ? (int)splits : (tune.s1 > 0 ? tune.s1 : ceil_div(target, (int64_t)p.heads * p.n_mc));
   s1 = max(1, min(min(s1, max_by_work), kMaxSplits));
   p.kps1 = ceil_div(ceil_div(Lk, s1), kTile) * kTile;
   p.s1 = ceil_div(Lk, p.kps1);
-  int s2 = splits > 0 ? (int)splits : ceil_div(target, p.heads);
+  int s2 = splits > 0 ? (int)splits : (tune.s2 > 0 ? tune.s2 : ceil_div(target, p.heads));
   s2 = max(1, min(s2, max_by_work));
   p.kps2 = ceil_div(ceil_div(Lk, s2), kTile) * kTile;
   p.s2 = ceil_div(Lk, p.kps2);
@@ -615,16 +722,31 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   const T* vv = static_cast<const T*>(v);
 
   uint64_t* prof = prof_slot();
-  hipLaunchKernelGGL((pass1_kernel<T, D>), dim3(p.heads * p.n_mc * p.s1), dim3(kThreads), 0, st, qq, q_sb, q_sh,
-                     q_ss, q_sd, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml,
-                     part_y, prof);
+  const dim3 g1(p.heads * p.n_mc * p.s1);
+  if (p.p1_waves == 8) {
+    hipLaunchKernelGGL((pass1_kernel<T, D, 8, 1>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, Hkv,
+                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, prof);
+  } else if (p.p1_occ == 1) {
+    hipLaunchKernelGGL((pass1_kernel<T, D, 4, 1>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, Hkv,
+                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, prof);
+  } else {
+    hipLaunchKernelGGL((pass1_kernel<T, D, 4, 2>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, Hkv,
+                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, prof);
+  }
   hipLaunchKernelGGL((merge_kernel<T, D>), dim3(p.heads * p.mpad), dim3(kMergeThreads), 0, st, part_ml, part_y,
                      p.n_mc, p.s1, p.M, y_round, yhl, ystat, yf, zero_ptr, zero_words, prof);
   const int cg = min(p.n_mc, 2);
   const size_t lds2 = (size_t)cg * 3 * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
-  hipLaunchKernelGGL((pass2_kernel<T, D>), dim3(p.heads * p.s2), dim3(kThreads), lds2, st, qq, q_sb, q_sh, q_ss,
-                     q_sd, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round,
-                     yhl, ystat, scores, prof);
+  const dim3 g2(p.heads * p.s2);
+  if (p.p2_waves == 8) {
+    hipLaunchKernelGGL((pass2_kernel<T, D, 8, 1>), g2, dim3(512), lds2, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, Hkv,
+                       Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, yhl, ystat, scores,
+                       prof);
+  } else {
+    hipLaunchKernelGGL((pass2_kernel<T, D, 4, 2>), g2, dim3(256), lds2, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, Hkv,
+                       Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, yhl, ystat, scores,
+                       prof);
+  }
   return hipGetLastError();
 }
 

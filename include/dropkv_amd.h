@@ -143,9 +143,10 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
  * those calls first clears its slot, then every kernel it launches records its
  * first-workgroup start and last-workgroup end from the GPU wall clock.  A
  * call captured into a HIP graph re-records its slot on every replay.
- * Stage order: pass-1 partials, merge, pass-2 scores, select-clear (folded
- * into the merge in dropkv_evict, so 0), select-pool, select-top-k, compact;
- * element 7 is the span from the first kernel start to the last kernel end.
+ * Stage order: pass-1 partials, merge, pass-2 scores, select-final (the
+ * per-row threshold; in a standalone dropkv_select it also covers the
+ * workspace clear), select-pool, select-candidates, emit+compact; element 7
+ * is the span from the first kernel start to the last kernel end.
  *   dropkv_profile_read(slot, ms[8])   waits for the device, reads one slot
  *   dropkv_profile_disarm()            stop recording new slots
  *   dropkv_profile_end(ms[8], calls)   sum over recorded slots, then free

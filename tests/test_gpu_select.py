@@ -98,3 +98,27 @@ def test_compact2_matches_cat_gather(gpu):
     ko, vo = ops.compact2(K0.to(gpu), V0.to(gpu), K1.to(gpu), V1.to(gpu), idx.to(gpu))
     rk, rv = R.gather_compressed(torch.cat([K0, K1], 2), torch.cat([V0, V1], 2), idx)
     assert torch.equal(ko.cpu(), rk) and torch.equal(vo.cpu(), rv)
+
+
+@pytest.mark.parametrize("shape", [(1, 32, 8, 128, 2048, 2048), (2, 14, 2, 64, 3000, 5000), (1, 8, 8, 128, 64, 700)])
+def test_evict_fused_matches_ops(gpu, shape):
+    """One dropkv_evict call (score -> select -> gather fused in the emit
+    stage) equals the separate ops and torch.gather bit for bit."""
+    from dropkv_amd import ops
+    B, Hq, Hkv, D, Lq, Lk = shape
+    g = torch.Generator().manual_seed(Lk)
+    Q = torch.randn(B, Hq, Lq, D, generator=g).to(torch.bfloat16).to(gpu)
+    K = torch.randn(B, Hkv, Lk, D, generator=g).to(torch.bfloat16).to(gpu)
+    V = torch.randn(B, Hkv, Lk, D, generator=g).to(torch.bfloat16).to(gpu)
+    keep = max(int(0.1 * Lk), 8, 1)
+    plan = ops.EvictPlan(Q, K, 8, 11, keep, keep_scores=True)
+    idx, ko, vo = plan(Q, K, V)
+    s = ops.scores(Q, K, V, 8)
+    assert torch.equal(plan.scores, s)
+    ref_idx = ops.select(s, 11, 8, keep)
+    assert torch.equal(idx, ref_idx)
+    rk, rv = R.gather_compressed(K.cpu(), V.cpu(), idx.cpu())
+    assert torch.equal(ko.cpu(), rk) and torch.equal(vo.cpu(), rv)
+    # and against the oracle's selection on the same scores
+    pooled = R.pool_protect(s.cpu().clone(), 11, 8)
+    assert torch.equal(idx.cpu(), R.topk_sorted(pooled, keep))
