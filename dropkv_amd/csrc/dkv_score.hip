@@ -40,41 +40,37 @@ __device__ __forceinline__ int row_bound(int m, int M, int W, int Lk) {
 }
 
 // One lane's Q^T operand: 8 consecutive head-dim values from column d0 of
-// query row m (zeros for padding rows).  Q may have any strides.
+// query row m (zeros for padding rows).  With `qvec` (head-dim stride 1 and
+// 16-byte aligned rows, checked by the host) one 16-byte load; otherwise
+// eight element loads, so Q may have any strides.
 template <typename T>
 __device__ __forceinline__ typename Elem<T>::v8 load_q_op(const T* __restrict__ q, int64_t q_sb, int64_t q_sh,
-                                                        int64_t q_ss, int64_t q_sd, int b, int hkv, int g, int W,
-                                                        int Lq, int M, int m, int d0) {
-  typename Elem<T>::v8 x;
+                                                        int64_t q_ss, int64_t q_sd, bool qvec, int b, int hkv,
+                                                        int g, int W, int Lq, int M, int m, int d0) {
+  typedef typename Elem<T>::v8 v8;
   const bool valid = m < M;
-  const int gi = valid ? m / W : 0;
-  const int w = valid ? m % W : 0;
+  const int mm = valid ? m : 0;  // padding rows read row 0, then zero it
+  const int gi = mm / W, w = mm % W;
   const T* base = q + (int64_t)b * q_sb + (int64_t)(hkv * g + gi) * q_sh + (int64_t)(Lq - W + w) * q_ss;
+  v8 x;
+  if (qvec) {
+    x = *reinterpret_cast<const v8*>(base + d0);
+  } else {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) x[e] = valid ? base[(int64_t)(d0 + e) * q_sd] : static_cast<T>(0.0f);
+    for (int e = 0; e < 8; ++e) x[e] = base[(int64_t)(d0 + e) * q_sd];
+  }
+  if (!valid) x = v8{};
   return x;
 }
 
 // Load the Q^T operands of one 16-row block (lane row m, lane group lg).
 template <typename T, int D>
 __device__ __forceinline__ void load_q_ops(typename Elem<T>::v8 (&qop)[D / 32], const T* __restrict__ q,
-                                           int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
+                                           int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
                                            int b, int hkv, int g, int W, int Lq, int M, int m, int lg) {
-  typedef typename Elem<T>::v8 v8;
-  const bool valid = m < M;
-  const int gi = valid ? m / W : 0;
-  const int w = valid ? m % W : 0;
-  const T* base = q + (int64_t)b * q_sb + (int64_t)(hkv * g + gi) * q_sh + (int64_t)(Lq - W + w) * q_ss;
 #pragma unroll
-  for (int kk = 0; kk < D / 32; ++kk) {
-    v8 x;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = 32 * kk + 8 * lg + e;
-      x[e] = valid ? base[(int64_t)d * q_sd] : static_cast<T>(0.0f);
-    }
-    qop[kk] = x;
-  }
+  for (int kk = 0; kk < D / 32; ++kk)
+    qop[kk] = load_q_op<T>(q, q_sb, q_sh, q_ss, q_sd, qvec, b, hkv, g, W, Lq, M, m, 32 * kk + 8 * lg);
 }
 
 // ---------------------------------------------------------------------------
@@ -122,7 +118,7 @@ __device__ __forceinline__ void load_v_pairs(u32x4 (&va)[(kTile / 2) / (64 / (D 
 // ---------------------------------------------------------------------------
 template <typename T, int D, int WAVES, int MINW>
 __global__ void __launch_bounds__(64 * WAVES, MINW)
-pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
+pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
              const T* __restrict__ kp, const T* __restrict__ vp,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int n_splits, int kps,
              float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y,
@@ -136,7 +132,10 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   constexpr int NIT = (kTile / 2) / GRP;
   constexpr int NT = 64 * WAVES;
 
-  __shared__ uint32_t lds[WAVES * D * kPitch];
+  constexpr int kYPitch = D + 4;  // fp32 row pitch of the merge buffer
+  constexpr int kLdsTiles = WAVES * D * kPitch;
+  constexpr int kLdsMerge = 3 * WAVES * kRows + WAVES * kRows * kYPitch;
+  __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsTiles > kLdsMerge ? kLdsTiles : kLdsMerge];
 
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   const int mc = lid % n_mc;
@@ -152,7 +151,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
     const int m = mc * kRows + mb * 16 + li;
-    load_q_ops<T, D>(qop[mb], q, q_sb, q_sh, q_ss, q_sd, b, hkv, g, W, Lq, M, m, lg);
+    load_q_ops<T, D>(qop[mb], q, q_sb, q_sh, q_ss, q_sd, qvec, b, hkv, g, W, Lq, M, m, lg);
     bound[mb] = row_bound(m, M, W, Lk);
   }
   // Tiles wholly below every row's causal bound need no masking (unless this
@@ -241,13 +240,13 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
       const float mnew = fmaxf(m2[mb], tmax);
       const bool empty = mnew == -INFINITY;
-      const float alpha = empty ? 1.f : exp2f(m2[mb] - mnew);
+      const float alpha = empty ? 1.f : __builtin_amdgcn_exp2f(m2[mb] - mnew);
       float psum = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float pv = empty ? 0.f : exp2f(s[kb][mb][r] - mnew);
+          const float pv = empty ? 0.f : __builtin_amdgcn_exp2f(s[kb][mb][r] - mnew);
           psum += pv;
           const T h = static_cast<T>(pv);
           phi[mb][4 * kb + r] = h;
@@ -285,11 +284,14 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     lsum[mb] += __shfl_xor(lsum[mb], 32);
   }
 
-  // Cross-wave merge in LDS (the V tiles are dead now).
+  // Cross-wave merge in LDS (the V tiles are dead now): every wave stores
+  // its unscaled accumulator once; then all threads combine the waves with
+  // weights 2^(m_w - max_w m_w) and write the workgroup's partial.
   __syncthreads();
   float* sm_m = reinterpret_cast<float*>(lds);
   float* sm_l = sm_m + WAVES * kRows;
-  float* ybuf = sm_l + WAVES * kRows;  // [kRows][D]
+  float* sm_f = sm_l + WAVES * kRows;
+  float* wbuf = sm_f + WAVES * kRows;  // [WAVES][kRows][kYPitch]
   if (lg == 0) {
 #pragma unroll
     for (int mb = 0; mb < kMB; ++mb) {
@@ -297,45 +299,37 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
       sm_l[wv * kRows + 16 * mb + li] = lsum[mb];
     }
   }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb)
+      *reinterpret_cast<f32x4*>(wbuf + ((size_t)wv * kRows + 16 * mb + li) * kYPitch + 16 * dt + 4 * lg) =
+          yacc[dt][mb];
   __syncthreads();
-#pragma unroll
-  for (int mb = 0; mb < kMB; ++mb) {
-    const int row = 16 * mb + li;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, sm_m[w * kRows + row]);
-    const float f = (mx == -INFINITY) ? 0.f : exp2f(m2[mb] - mx);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= f;
-  }
-  for (int w = 0; w < WAVES; ++w) {
-    if (wv == w) {
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int mb = 0; mb < kMB; ++mb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int idx = (16 * mb + li) * D + 16 * dt + 4 * lg + r;
-            ybuf[idx] = (w == 0 ? 0.f : ybuf[idx]) + yacc[dt][mb][r];
-          }
-    }
-    __syncthreads();
-  }
-
   const int64_t slot = ((int64_t)head * n_mc + mc) * n_splits + split;
   if (threadIdx.x < kRows) {
     const int row = threadIdx.x;
     float mx = -INFINITY;
     for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, sm_m[w * kRows + row]);
     float l = 0.f;
-    if (mx != -INFINITY)
-      for (int w = 0; w < WAVES; ++w) l += sm_l[w * kRows + row] * exp2f(sm_m[w * kRows + row] - mx);
+    for (int w = 0; w < WAVES; ++w) {
+      const float mw = sm_m[w * kRows + row];
+      const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - mx);
+      sm_f[w * kRows + row] = f;
+      l += sm_l[w * kRows + row] * f;
+    }
     part_ml[(slot * kRows + row) * 2 + 0] = mx;
     part_ml[(slot * kRows + row) * 2 + 1] = l;
   }
+  __syncthreads();
   float* py = part_y + slot * kRows * D;
-  for (int i = threadIdx.x; i < kRows * D; i += NT) py[i] = ybuf[i];
+  for (int i = threadIdx.x; i < kRows * D; i += NT) {
+    const int row = i / D, d = i % D;
+    float y = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) y += wbuf[((size_t)w * kRows + row) * kYPitch + d] * sm_f[w * kRows + row];
+    py[i] = y;
+  }
   prof_end(prof, kStPass1);
 }
 
@@ -384,6 +378,17 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   const int mc = gr / kRows, row = gr % kRows;
   const int64_t slot0 = ((int64_t)head * n_mc + mc) * n_splits;
 
+  // Issue every load up front: the partial y values of this thread's splits
+  // (the first kPre of them) and the per-split statistics.
+  const int d = tid % D, grp = tid / D;
+  const float* py = part_y + (slot0 * kRows + row) * D + d;
+  constexpr int kPre = 16;
+  float yv[kPre];
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int s = grp + i * G;
+    yv[i] = s < n_splits ? py[(int64_t)s * kRows * D] : 0.f;
+  }
   float mx = -INFINITY;
   for (int s = tid; s < n_splits; s += kMergeThreads) {
     const float m = part_ml[((slot0 + s) * kRows + row) * 2];
@@ -400,11 +405,14 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   }
   const float l = block_reduce(lpart, s_red, false);  // also orders the s_f writes
 
-  const int d = tid % D, grp = tid / D;
-  const float* py = part_y + (slot0 * kRows + row) * D + d;
   float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int s = grp + i * G;
+    if (s < n_splits) acc += yv[i] * s_f[s];
+  }
 #pragma unroll 8
-  for (int s = grp; s < n_splits; s += G) acc += py[(int64_t)s * kRows * D] * s_f[s];
+  for (int s = grp + kPre * G; s < n_splits; s += G) acc += py[(int64_t)s * kRows * D] * s_f[s];
   s_acc[grp][d] = acc;
   __syncthreads();
 
@@ -473,7 +481,7 @@ __device__ __forceinline__ float sumsq8<_Float16>(Elem<_Float16>::v8 x, float ac
 
 template <typename T, int D, int WAVES, int MINW>
 __global__ void __launch_bounds__(64 * WAVES, MINW)
-pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
+pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
              const T* __restrict__ kp, const T* __restrict__ vp,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int cg, int n_splits, int kps,
              float scale_log2, float eps, int p_round,
@@ -514,7 +522,7 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
       const int m = (c0 + c) * kRows + mb * 16 + li;
       v8 val;
       if (which == 0) {
-        val = load_q_op<T>(q, q_sb, q_sh, q_ss, q_sd, b, hkv, g, W, Lq, M, m, 32 * kk + 8 * lg);
+        val = load_q_op<T>(q, q_sb, q_sh, q_ss, q_sd, qvec, b, hkv, g, W, Lq, M, m, 32 * kk + 8 * lg);
       } else {
         const int64_t rbase = (int64_t)head * mpad + m;
         val = *reinterpret_cast<const v8*>(yhl + (rbase * 2 + (which - 1)) * D + 32 * kk + 8 * lg);
@@ -598,7 +606,7 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              float p = exp2f(sacc[kb][mb][r] * scale_log2 - lse2);
+              float p = __builtin_amdgcn_exp2f(sacc[kb][mb][r] * scale_log2 - lse2);
               if (masked) p = (t0 + 16 * kb + 4 * lg + r) <= bound ? p : 0.f;
               p = fminf(p, 1.f);
               if (p_round) p = round_through<T>(p);
@@ -646,7 +654,7 @@ static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b)
 // DROPKV_TUNE environment variable ("p1w=8,p1occ=1,p2w=4,s1=32,s2=32",
 // any subset) overrides them for experiments.
 struct Tune {
-  int p1w = 4, p1occ = 1, p2w = 4, s1 = 0, s2 = 0, target = 256;
+  int p1w = 4, p1occ = 1, p2w = 8, s1 = 0, s2 = 0, target = 256;
 };
 static Tune read_tune() {
   Tune t;
@@ -722,15 +730,17 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   const T* vv = static_cast<const T*>(v);
 
   uint64_t* prof = prof_slot();
+  const bool qvec = q_sd == 1 && (q_sb % 8) == 0 && (q_sh % 8) == 0 && (q_ss % 8) == 0 &&
+                    (reinterpret_cast<uintptr_t>(q) & 15u) == 0;
   const dim3 g1(p.heads * p.n_mc * p.s1);
   if (p.p1_waves == 8) {
-    hipLaunchKernelGGL((pass1_kernel<T, D, 8, 1>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, Hkv,
+    hipLaunchKernelGGL((pass1_kernel<T, D, 8, 1>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
                        Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, prof);
   } else if (p.p1_occ == 1) {
-    hipLaunchKernelGGL((pass1_kernel<T, D, 4, 1>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, Hkv,
+    hipLaunchKernelGGL((pass1_kernel<T, D, 4, 1>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
                        Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, prof);
   } else {
-    hipLaunchKernelGGL((pass1_kernel<T, D, 4, 2>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, Hkv,
+    hipLaunchKernelGGL((pass1_kernel<T, D, 4, 2>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
                        Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, prof);
   }
   hipLaunchKernelGGL((merge_kernel<T, D>), dim3(p.heads * p.mpad), dim3(kMergeThreads), 0, st, part_ml, part_y,
@@ -739,11 +749,11 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   const size_t lds2 = (size_t)cg * 3 * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
   const dim3 g2(p.heads * p.s2);
   if (p.p2_waves == 8) {
-    hipLaunchKernelGGL((pass2_kernel<T, D, 8, 1>), g2, dim3(512), lds2, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, Hkv,
+    hipLaunchKernelGGL((pass2_kernel<T, D, 8, 1>), g2, dim3(512), lds2, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
                        Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, yhl, ystat, scores,
                        prof);
   } else {
-    hipLaunchKernelGGL((pass2_kernel<T, D, 4, 2>), g2, dim3(256), lds2, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, Hkv,
+    hipLaunchKernelGGL((pass2_kernel<T, D, 4, 2>), g2, dim3(256), lds2, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
                        Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, yhl, ystat, scores,
                        prof);
   }

@@ -37,6 +37,7 @@ constexpr int kBins3 = 1024;          // key bits 9..0
 constexpr int kMaxHalo = 64;          // kernel_size <= 2*kMaxHalo+1
 constexpr int kMaxChunks = 4096;      // Lk <= kMaxChunks * kChunk
 constexpr int kBatch = 8;             // independent loads in flight per thread
+constexpr int kCandLds = 8192;        // candidates staged in LDS by the final stage
 
 // Per-row words that must be zero on entry:
 //   [0] max pooled key, [1 .. kBins1] top-digit histogram of the unprotected
@@ -233,7 +234,7 @@ sel_cand_kernel(int Lk, int window, int keep, int chunks, SelWs ws, uint64_t* __
   __shared__ uint32_t wsum[8];
   __shared__ int s_bin;
   __shared__ uint32_t s_above;
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x;
   const int row = blockIdx.x / chunks;
   const int c = blockIdx.x % chunks;
   uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
@@ -259,34 +260,37 @@ sel_cand_kernel(int Lk, int window, int keep, int chunks, SelWs ws, uint64_t* __
   find_bin<kBins1>(hist, (uint32_t)keep, &s_bin, &s_above, wsum);
   const uint32_t b1 = (uint32_t)s_bin;
 
-  uint32_t above = 0u;
+  // Count this thread's keys above / inside the boundary bin, then reserve
+  // the block's candidate slots with a single atomic.
+  uint32_t above = 0u, ncand = 0u;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int j = c * kChunk + tid + i * kSelT;
-    const bool valid = j < Lk;
-    above += (valid && (keys[i] >> 21) > b1) ? 1u : 0u;
-    const bool cand = valid && (keys[i] >> 21) == b1;
-    const unsigned long long m = __ballot(cand);
-    if (m) {
-      const int leader = __ffsll((long long)m) - 1;
-      uint32_t base = 0u;
-      if (lane == leader) base = atomicAdd(&rw[kCandCount], (uint32_t)__popcll(m));
-      base = (uint32_t)__shfl((int)base, leader);
-      if (cand) {
-        const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
-        const uint32_t pos = base + (uint32_t)__popcll(m & below);
-        ckey[pos] = keys[i];
-        cidx[pos] = (uint32_t)j;
-      }
+    if (j < Lk) {
+      above += (keys[i] >> 21) > b1 ? 1u : 0u;
+      ncand += (keys[i] >> 21) == b1 ? 1u : 0u;
     }
   }
-  uint32_t tot_above, dummy, pa, pb;
-  block_excl_scan2(above, 0u, &pa, &pb, &tot_above, &dummy, wsum);
+  uint32_t pa, pc, tot_above, tot_cand;
+  block_excl_scan2(above, ncand, &pa, &pc, &tot_above, &tot_cand, wsum);
+  __shared__ uint32_t s_base;
   if (tid == 0) {
+    s_base = tot_cand ? atomicAdd(&rw[kCandCount], tot_cand) : 0u;
     ws.above[(int64_t)row * chunks + c] = tot_above;
     if (c == 0) {
       ws.thr[row * 2 + 0] = b1;  // boundary bin and what remains to take in it
       ws.thr[row * 2 + 1] = (uint32_t)keep - s_above;
+    }
+  }
+  __syncthreads();
+  uint32_t pos = s_base + pc;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = c * kChunk + tid + i * kSelT;
+    if (j < Lk && (keys[i] >> 21) == b1) {
+      ckey[pos] = keys[i];
+      cidx[pos] = (uint32_t)j;
+      ++pos;
     }
   }
   prof_end(prof, kStSelTopk);
@@ -308,11 +312,35 @@ sel_final_kernel(int chunks, SelWs ws, int64_t Lk, uint64_t* __restrict__ prof) 
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
   const uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
-  const uint32_t* ckey = ws.cand_key + (int64_t)row * Lk;
-  const uint32_t* cidx = ws.cand_idx + (int64_t)row * Lk;
   const uint32_t nc = rw[kCandCount];
   const uint32_t b1 = ws.thr[row * 2 + 0];
   const uint32_t k1 = ws.thr[row * 2 + 1];
+  // The candidates (typically a few percent of the row) are read three
+  // times: stage them in LDS when they fit.
+  __shared__ uint32_t lkey[kCandLds], lidx[kCandLds];
+  const uint32_t* ckey = ws.cand_key + (int64_t)row * Lk;
+  const uint32_t* cidx = ws.cand_idx + (int64_t)row * Lk;
+  if (nc <= (uint32_t)kCandLds) {
+    for (uint32_t base = 0; base < nc; base += kSelT * kBatch) {
+      uint32_t kv[kBatch], iv[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const uint32_t p = base + tid + i * kSelT;
+        kv[i] = p < nc ? ckey[p] : 0u;
+        iv[i] = p < nc ? cidx[p] : 0u;
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const uint32_t p = base + tid + i * kSelT;
+        if (p < nc) {
+          lkey[p] = kv[i];
+          lidx[p] = iv[i];
+        }
+      }
+    }
+    ckey = lkey;
+    cidx = lidx;
+  }
 
   // Digit 2 over the candidates.
   for (int i = tid; i < kBins2; i += kSelT) hist[i] = 0u;
