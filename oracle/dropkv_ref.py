@@ -10,23 +10,37 @@ PyTorch ops, and cites the reference file:line it follows (paths relative to
 the reference checkout, ``AozhongZhang/DropKV``).
 
 Pinning (how each function is checked independently of this file; the checks
-live in ``tests/test_oracle.py``):
+live in ``tests/test_oracle.py``, the fixtures in ``tests/golden/``):
 
-* ``dropkv_scores_reference``  -- float64 brute force with the *direct*
-  ``||v_j - y_m||^2`` formula (not termA-termB+termC) on tiny shapes; closed
-  forms V=0 -> 0, Q=0 -> uniform softmax with y = causal prefix mean, g=1;
-  Lq-invariance (only the Q tail is read); scores >= 0 up to rounding;
-  golden vectors written by the reference itself (``tests/golden``).
+* ``dropkv_scores_reference`` -- float64 brute force with the *direct*
+  ``||v_j - y_m||^2`` distance (not termA-termB+termC) on small shapes,
+  including Lq < Lk, g = 1 and B = 2; golden fixtures written by
+  ``tests/golden/make_golden.py`` (an independent NumPy float64 brute force);
+  closed forms V = 0 -> 0, Q = 0 -> uniform softmax with y = causal prefix
+  mean, a two-key logit gap; invariants: duplicated query heads leave the
+  score unchanged (the 1/g average), contiguous head grouping, only the Q
+  tail is read, scores >= 0.  ``eps`` is pinned only by presence: the Lk == W
+  case (p = 1) stays finite; its value is below the float32 resolution of the
+  reference's own expansion wherever that expansion is accurate.
 * ``fallback_scores`` (deployed ``use_triton=False`` path) -- float64 brute
-  force with emulated round-to-nearest-even of p and y to the input dtype;
-  golden vectors written by the reference itself.
-* ``pool_protect`` -- brute-force sliding max; closed form of the protected
-  tail ``max+1``.
-* ``keep_length`` -- the reference's own keep-length table (survey 8c) and
-  the reference tests' arithmetic.
-* ``topk_sorted`` -- brute force over all subsets on tiny rows, and the
-  tie-aware comparison against ``torch.topk``.
-* ``gather_compressed`` -- bit equality with ``torch.gather`` / fancy indexing.
+  force with round-to-nearest-even of p and y to bf16; golden fixtures
+  (including a final chunk shorter than the window); the reference tests'
+  own bound against ``dropkv_scores_reference(match_pytorch_precision=True)``.
+* ``pool_protect`` -- brute-force sliding max; the protected tail is
+  ``max + 1`` in float32, absorbed at max >= 2^24.
+* ``keep_length`` -- the keep-length table of the BASELINE configs and the
+  reference tests' arithmetic (tests/test_dropkv_triton.py:909-937, :1183-1262).
+* ``topk_sorted`` -- a rank rule on rows full of ties (i is kept iff
+  #greater + #equal-with-lower-index < keep) and the tie-aware comparison
+  against ``torch.topk``.
+* ``gather_compressed`` -- bit equality with per-row fancy indexing.
+* ``index_overlap`` -- planted mistakes (a non-tied swap is counted, a swap
+  among threshold ties is excused).
+
+No golden vectors were written by the reference itself: the reference's tests
+hold none (they compare implementations on unseeded random inputs), and every
+function here is pinned by the checks above, so the reference module was not
+imported.
 
 Tie rule: among keys whose pooled score equals the k-th largest value, the
 lowest indices are kept.  The reference uses ``torch.topk``, whose choice among

@@ -41,3 +41,42 @@ def gpu():
     from dropkv_amd import _lib
     _lib.load()
     return torch.device("cuda:0")
+
+
+# ---------------------------------------------------------------------------
+# Golden fixtures (tests/golden/dropkv_golden.npz, written by make_golden.py)
+# ---------------------------------------------------------------------------
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "dropkv_golden.npz")
+
+
+def _bf16_from_bits(u):
+    import numpy as np
+    return torch.from_numpy((u.astype(np.uint32) << 16).view(np.float32).copy()).to(torch.bfloat16)
+
+
+def golden_names():
+    import numpy as np
+    with np.load(GOLDEN) as z:
+        return sorted({k.split("/")[0] for k in z.files})
+
+
+def golden_case(name):
+    """Inputs as bf16 tensors (q is the stored query tail) and float64 /
+    float32 / int64 expectations of one golden case."""
+    import numpy as np
+    with np.load(GOLDEN) as z:
+        d = {k.split("/", 1)[1]: z[k] for k in z.files if k.startswith(name + "/")}
+    out = {"meta": [int(x) for x in d["meta"]], "ratio": float(d["ratio"])}
+    out["q"], out["k"], out["v"] = (_bf16_from_bits(d[x]) for x in ("q_tail", "k", "v"))
+    for key in ("exact", "bf16p", "deployed"):
+        if key in d:
+            out[key] = torch.from_numpy(d[key].copy())
+    if "bf16p" in d:
+        out["bf16p_np"] = d["bf16p"]
+    for key in ("pooled_bf16p", "pooled_deployed"):
+        if key in d:
+            out[key] = torch.from_numpy(d[key].copy())
+    for key in ("keep_idx_bf16p", "keep_idx_deployed"):
+        if key in d:
+            out[key] = torch.from_numpy(d[key].copy())
+    return out

@@ -1,0 +1,97 @@
+"""The C-ABI library loads and exports every entry point that
+include/dropkv_amd.h declares; host-side argument checks and workspace
+queries behave as documented.  No GPU work is launched (CPU suite)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from dropkv_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dropkv_amd.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(dropkv_[a-z_0-9]+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from dropkv_amd import _build
+        _build.build()
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    names = _declared_functions()
+    assert "dropkv_scores" in names and "dropkv_evict" in names and len(names) >= 10
+
+
+def test_every_declared_symbol_is_exported(lib):
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in _declared_functions() if not hasattr(raw, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_binding_table_matches_header():
+    """The ctypes signature table covers exactly the declared functions."""
+    assert sorted(_lib._SIGNATURES) == _declared_functions()
+
+
+def test_version_and_head_dims(lib):
+    assert lib.dropkv_version() >= 100
+    assert _lib.supported_head_dims() == (64, 128)
+
+
+def test_workspace_queries(lib):
+    # invalid shapes report 0 bytes
+    assert lib.dropkv_scores_workspace_bytes(1, 7, 2, 100, 64, 8, 0) == 0
+    assert lib.dropkv_select_workspace_bytes(0, 100) == 0
+    a = lib.dropkv_scores_workspace_bytes(1, 32, 8, 32768, 128, 8, 0)
+    b = lib.dropkv_select_workspace_bytes(8, 32768)
+    c = lib.dropkv_evict_workspace_bytes(1, 32, 8, 32768, 128, 8, 0)
+    assert a > 0 and b > 0 and c >= a + b + 8 * 32768 * 4
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    # (q, k, v) null
+    (dict(q=None), 1, "null q/k/v"),
+    (dict(dtype=3), 1, "bf16 or fp16"),
+    (dict(Hq=30), 1, "divisible"),
+    (dict(W=0), 1, "window must be positive"),
+    (dict(Lq=4), 1, "must be >= window_size"),
+    (dict(Lq=200), 1, "must be <= Lk"),
+    (dict(D=96), 2, "head dim"),
+])
+def test_score_argument_checks(lib, args, code, msg):
+    """Checks happen on the host before anything is enqueued."""
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: the checks fail first
+    a = dict(q=fake, k=fake, v=fake, dtype=1, B=1, Hq=32, Hkv=8, Lq=64, Lk=100, D=128, W=8)
+    a.update(args)
+    rc = lib.dropkv_scores(a["q"], 0, 0, 0, 1, a["k"], a["v"], a["dtype"], a["B"], a["Hq"], a["Hkv"], a["Lq"],
+                           a["Lk"], a["D"], a["W"], 1e-6, 1, 0, 0, None, None, 0, None)
+    assert rc == code
+    assert msg in lib.dropkv_last_error().decode()
+
+
+def test_select_argument_checks(lib):
+    fake = ctypes.c_void_p(1 << 20)
+    assert lib.dropkv_select(fake, 8, 100, 10, 8, 10, fake, None, fake, 1 << 20, None) == 1   # even kernel
+    assert "odd" in lib.dropkv_last_error().decode()
+    assert lib.dropkv_select(fake, 8, 100, 11, 8, 101, fake, None, fake, 1 << 20, None) == 1  # keep > Lk
+    assert lib.dropkv_select(fake, 8, 100, 11, 8, 10, fake, None, fake, 16, None) == 3        # workspace
+    assert "workspace too small" in lib.dropkv_last_error().decode()
+
+
+def test_compact_argument_checks(lib):
+    fake = ctypes.c_void_p(1 << 20)
+    assert lib.dropkv_compact(fake, fake, 0, 0, 0, 3, 1, 1, 10, 8, fake, 4, fake, fake, None) == 1
+    assert "elem_bytes" in lib.dropkv_last_error().decode()
+    assert lib.dropkv_compact2(fake, fake, 0, 0, 0, -1, fake, fake, 0, 0, 0, 5, 2, 1, 1, 8, fake, 4, fake, fake,
+                               None) == 1

@@ -1,0 +1,364 @@
+"""Host-side behaviour of DropKVCache / prefill_chunked / the scoring guards
+that needs no GPU compute: constructor checks, prefill modes that only store,
+length bookkeeping, HF 4-argument form, prefill_chunked validation, mode
+schedule and cleanup on failure (reference tests:535-1330, :1831-1899), and
+the absence of any CPU fallback in the product path.  CPU only."""
+
+import logging
+
+import pytest
+import torch
+
+from conftest import LLAMA_CFG, make_qkv
+from dropkv_amd import DropKVCache, dropkv_scores_triton, ops, prefill_chunked
+from dropkv_amd.dropkv_cache import _LayerCache
+
+
+def _cache(**kw):
+    d = dict(keep_ratio=0.3, window_size=8, kernel_size=11, use_triton=False)
+    d.update(kw)
+    return DropKVCache(**d)
+
+
+# --- constructor (dropkv_cache.py:321-330) ---------------------------------
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(keep_ratio=0.0), "keep_ratio"), (dict(keep_ratio=1.5), "keep_ratio"),
+    (dict(window_size=0), "window_size"), (dict(kernel_size=4), "kernel_size"),
+    (dict(kernel_size=0), "kernel_size"),
+])
+def test_constructor_rejects(kw, msg):
+    with pytest.raises(ValueError, match=msg):
+        DropKVCache(**kw)
+
+
+def test_defaults_and_mode_attributes():
+    c = DropKVCache()
+    assert (c.keep_ratio, c.window_size, c.kernel_size, c.use_triton) == (0.1, 8, 11, True)
+    assert c._prefill_mode == "single_pass" and c._evict_use_seen_tokens is False
+    assert c._budget_max_kv_tokens is None and c._seen_tokens == 0
+
+
+def test_beam_search_unsupported():
+    with pytest.raises(NotImplementedError):
+        _cache().batch_split(2, 1)
+    with pytest.raises(NotImplementedError):
+        DropKVCache.from_batch_splits([])
+
+
+# --- keep length (dropkv_cache.py:470-473) ----------------------------------
+
+def test_keep_length():
+    c = _cache(keep_ratio=0.3)
+    assert c._keep_length(128, None, None) == 38
+    assert c._keep_length(128, 512, None) == 128
+    assert c._keep_length(128, 200, None) == 60
+    assert _cache(keep_ratio=0.01)._keep_length(64, 10, None) == 8
+    assert _cache(keep_ratio=0.8)._keep_length(512, 512, 100) == 100
+
+
+# --- store-only prefill paths -----------------------------------------------
+
+def test_accumulate_grows_cache_and_seen_tokens():
+    Q, K, V = make_qkv(LLAMA_CFG, 64)
+    c = _cache()
+    c._prefill_mode = "accumulate"
+    rk, _ = c.update(Q[:, :, :32], K[:, :, :32], V[:, :, :32], layer_idx=0)
+    assert c.key_cache[0].shape[2] == 32 and rk.shape[2] == 32
+    rk, rv = c.update(Q[:, :, 32:], K[:, :, 32:], V[:, :, 32:], layer_idx=0)
+    assert c.key_cache[0].shape[2] == 64 and rk.shape[2] == 64
+    assert torch.equal(c.key_cache[0], K) and torch.equal(c.value_cache[0], V)
+    assert c._seen_tokens == 64
+
+
+def test_seen_tokens_counted_on_layer_zero_only():
+    Q, K, V = make_qkv(LLAMA_CFG, 16)
+    c = _cache()
+    c._prefill_mode = "accumulate"
+    for layer in range(3):
+        c.update(Q, K, V, layer_idx=layer)
+    assert c._seen_tokens == 16 and len(c) == 3
+
+
+def test_short_sequence_stored_without_eviction():
+    Q, K, V = make_qkv(LLAMA_CFG, 6)
+    c = _cache(window_size=8)
+    rk, _ = c.update(Q, K, V, layer_idx=0)
+    assert c.key_cache[0].shape[2] == 6 and rk is K
+
+
+def test_hf_4arg_without_query_states_stores_full(caplog):
+    _, K, V = make_qkv(LLAMA_CFG, 128)
+    c = _cache()
+    with caplog.at_level(logging.WARNING):
+        c.update(K, V, 0, {"sin": None, "cos": None})
+    assert c.key_cache[0].shape[2] == 128
+    assert "without query_states" in caplog.text
+
+
+def test_layer_gap_rejected():
+    _, K, V = make_qkv(LLAMA_CFG, 16)
+    with pytest.raises(ValueError, match="DynamicCache"):
+        _cache().update(None, K, V, layer_idx=2)
+
+
+@pytest.mark.parametrize("L", [128, 6])
+def test_invalid_prefill_mode_raises(L):
+    Q, K, V = make_qkv(LLAMA_CFG, L)
+    c = _cache(window_size=16)
+    c._prefill_mode = "typo_mode"
+    with pytest.raises(ValueError, match="Invalid _prefill_mode"):
+        c.update(Q, K, V, layer_idx=0)
+
+
+def test_invalid_mode_on_continuation_path_raises():
+    Q, K, V = make_qkv(LLAMA_CFG, 64)
+    c = _cache()
+    c._prefill_mode = "accumulate"
+    c.update(Q, K, V, layer_idx=0)
+    c._prefill_mode = "bogus"
+    with pytest.raises(ValueError, match="Invalid _prefill_mode"):
+        c.update(Q[:, :, :1], K[:, :, :1], V[:, :, :1], layer_idx=0)
+
+
+def test_decode_append_single_pass_mode():
+    Q, K, V = make_qkv(LLAMA_CFG, 40)
+    c = _cache()
+    c._prefill_mode = "accumulate"
+    c.update(Q[:, :, :39], K[:, :, :39], V[:, :, :39], layer_idx=0)
+    c._prefill_mode = "single_pass"
+    rk, _ = c.update(Q[:, :, 39:], K[:, :, 39:], V[:, :, 39:], layer_idx=0)
+    assert rk.shape[2] == 40 and c.key_cache[0].shape[2] == 40
+
+
+def test_lengths_for_rope_and_mask():
+    """get_seq_length = tokens seen (RoPE), get_mask_sizes = stored + q_len
+    (dropkv_cache.py:624-648)."""
+    Q, K, V = make_qkv(LLAMA_CFG, 50)
+    c = _cache()
+    assert c.get_seq_length() == 0
+    assert c.get_mask_sizes(torch.arange(5), 0) == (5, 0)
+    c._prefill_mode = "accumulate"
+    c.update(Q, K, V, layer_idx=0)
+    c.key_cache[0] = c.key_cache[0][:, :, :20]      # as after an eviction
+    assert c.get_seq_length() == 50
+    assert c.get_mask_sizes(torch.arange(1), 0) == (21, 0)
+    assert c.get_seq_length(3) == 0
+
+
+def test_legacy_round_trip_stores_without_eviction():
+    _, K, V = make_qkv(LLAMA_CFG, 30)
+    legacy = ((K, V), (K * 2, V * 2))
+    c = DropKVCache.from_legacy_cache(legacy)
+    assert len(c) == 2 and c._seen_tokens == 30
+    out = c.to_legacy_cache()
+    assert torch.equal(out[1][0], K * 2) and torch.equal(out[0][1], V)
+    assert isinstance(c, _LayerCache)
+
+
+# --- no CPU fallback in the product path ------------------------------------
+
+def test_eviction_on_cpu_tensors_fails_loudly():
+    """Scoring/selection/gather run only on the HIP kernels: CPU tensors are
+    rejected with RuntimeError instead of silently computing on the CPU."""
+    Q, K, V = make_qkv(LLAMA_CFG, 64)
+    with pytest.raises(RuntimeError):
+        _cache().update(Q, K, V, layer_idx=0)
+    with pytest.raises(RuntimeError):
+        ops.scores(Q, K, V, 8)
+    with pytest.raises(RuntimeError):
+        ops.select(torch.zeros(1, 2, 64), 11, 8, 10)
+    with pytest.raises(RuntimeError):
+        ops.compact(K, V, torch.zeros(1, 8, 4, dtype=torch.int64))
+
+
+# --- scoring guards reachable without a GPU (dropkv_triton.py:680-693) -------
+
+def test_guard_window_size():
+    Q, K, V = make_qkv(LLAMA_CFG, 64)
+    with pytest.raises(AssertionError, match="positive int"):
+        dropkv_scores_triton(Q, K, V, window_size=0)
+
+
+def test_guard_lengths():
+    Q, K, V = make_qkv(LLAMA_CFG, 4)
+    with pytest.raises(AssertionError, match="must be >= window_size"):
+        dropkv_scores_triton(Q, K, V)
+    Q, K, V = make_qkv(LLAMA_CFG, 6, 64)
+    with pytest.raises(AssertionError, match=r"Lq.*must be >= window_size"):
+        dropkv_scores_triton(Q, K, V)
+    Q, _, _ = make_qkv(LLAMA_CFG, 64)
+    _, K, V = make_qkv(LLAMA_CFG, 6)
+    with pytest.raises(AssertionError, match=r"Lk.*must be >= window_size"):
+        dropkv_scores_triton(Q[:, :, :8], K, V)
+    Q, K, V = make_qkv(LLAMA_CFG, 64, 32)
+    with pytest.raises(AssertionError, match=r"Lq.*must be <= Lk"):
+        dropkv_scores_triton(Q, K, V)
+
+
+def test_guard_divisible_and_device():
+    Q = torch.randn(1, 7, 64, 128, dtype=torch.bfloat16)
+    K = torch.randn(1, 4, 64, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="divisible"):
+        dropkv_scores_triton(Q, K, K)
+    Q, K, V = make_qkv(LLAMA_CFG, 64)
+    with pytest.raises(AssertionError, match="CUDA"):
+        dropkv_scores_triton(Q, K, V)
+
+
+def test_fast_path_guard_falls_back_to_deployed_semantics(monkeypatch):
+    """_compute_keep_indices catches AssertionError from the fast path and
+    uses the deployed-path scoring (dropkv_cache.py:389-400); a RuntimeError
+    propagates (reference tests:1944-1945)."""
+    import dropkv_amd.dropkv_cache as C
+    calls = []
+
+    def fast(*a, **k):
+        calls.append("fast")
+        raise AssertionError("guard")
+
+    def deployed(q, k, v, w):
+        calls.append(("deployed", w))
+        return torch.zeros(k.shape[0], k.shape[1], k.shape[2])
+
+    monkeypatch.setattr("dropkv_amd.dropkv_triton.dropkv_scores_triton", fast)
+    monkeypatch.setattr(C, "_deployed_path_scores", deployed)
+    monkeypatch.setattr(C.ops, "select", lambda s, ks, w, keep: ("select", ks, w, keep))
+    Q, K, V = make_qkv(LLAMA_CFG, 64)
+    c = _cache(use_triton=True)
+    assert c._compute_keep_indices(Q, K, V) == ("select", 11, 8, 19)
+    assert calls == ["fast", ("deployed", 8)]
+
+    def boom(*a, **k):
+        raise RuntimeError("kernel failure")
+
+    monkeypatch.setattr("dropkv_amd.dropkv_triton.dropkv_scores_triton", boom)
+    with pytest.raises(RuntimeError, match="kernel failure"):
+        c._compute_keep_indices(Q, K, V)
+
+
+# --- prefill_chunked (dropkv_cache.py:651-807) --------------------------------
+
+def test_prefill_chunked_rejects_wrong_cache_type():
+    with pytest.raises(TypeError, match="DropKVCache"):
+        prefill_chunked(object(), torch.zeros(1, 100), object())
+
+
+def test_prefill_chunked_rejects_populated_cache():
+    c = _cache()
+    c.key_cache.append(torch.zeros(1, 8, 10, 128))
+    c.value_cache.append(torch.zeros(1, 8, 10, 128))
+    with pytest.raises(ValueError, match="fresh.*empty.*cache"):
+        prefill_chunked(object(), torch.zeros(1, 100), c)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(chunk_size=4), "chunk_size.*window_size"),
+    (dict(chunk_size=32, attention_mask=torch.ones(1, 100)), "sequence-shaped"),
+    (dict(chunk_size=32, evict_strategy="invalid"), "evict_strategy"),
+    (dict(chunk_size=32, evict_strategy="budget", max_kv_tokens=4), "window_size"),
+    (dict(chunk_size=32, evict_strategy="budget", max_kv_tokens=None), "max_kv_tokens is required"),
+])
+def test_prefill_chunked_validation(kw, msg):
+    with pytest.raises(ValueError, match=msg):
+        prefill_chunked(object(), torch.zeros(1, 100), _cache(), **kw)
+
+
+class BrokenModel:
+    def __call__(self, *args, **kwargs):
+        raise RuntimeError("simulated failure")
+
+
+@pytest.mark.parametrize("kw", [dict(chunk_size=32), dict(chunk_size=32, evict_strategy="budget", max_kv_tokens=64)])
+def test_prefill_chunked_cleans_up_on_error(kw):
+    c = _cache()
+    with pytest.raises(RuntimeError, match="simulated failure"):
+        prefill_chunked(BrokenModel(), torch.zeros(1, 100), c, **kw)
+    assert c._prefill_mode == "single_pass" and c._evict_use_seen_tokens is False
+    assert c._budget_max_kv_tokens is None
+    assert len(c.key_cache) == 0 and len(c.value_cache) == 0 and c._seen_tokens == 0
+
+
+def test_cleanup_after_mid_forward_failure():
+    calls = 0
+
+    class FailAfterFirst:
+        def __call__(self, chunk, past_key_values=None, **kw):
+            nonlocal calls
+            calls += 1
+            if calls > 1:
+                raise RuntimeError("OOM on chunk 2")
+            Q, K, V = make_qkv(LLAMA_CFG, chunk.shape[1])
+            for layer in range(2):
+                past_key_values.update(Q, K, V, layer_idx=layer)
+            return "out"
+
+    c = _cache()
+    with pytest.raises(RuntimeError, match="OOM on chunk 2"):
+        prefill_chunked(FailAfterFirst(), torch.zeros(1, 100), c, chunk_size=32)
+    assert len(c.key_cache) == 0 and c._seen_tokens == 0 and c._prefill_mode == "single_pass"
+
+
+class RecordingModel:
+    """Records the cache mode per chunk; stores K/V lengths like a model would
+    (accumulate: append; evict modes: the keep length the cache would keep)."""
+
+    def __init__(self):
+        self.log = []
+
+    def __call__(self, chunk, past_key_values=None, use_cache=True, **kw):
+        c = past_key_values
+        n = chunk.shape[1]
+        self.log.append((c._prefill_mode, c._evict_use_seen_tokens, c._budget_max_kv_tokens, n))
+        c._seen_tokens += n
+        stored = c.key_cache[0].shape[2] if c.key_cache else 0
+        if c._prefill_mode == "accumulate":
+            new = stored + n
+        else:
+            total = stored + n
+            base = c._seen_tokens if c._evict_use_seen_tokens else total
+            new = c._keep_length(total, base if c._evict_use_seen_tokens else None, c._budget_max_kv_tokens)
+        t = torch.zeros(1, 1, new, 1)
+        if c.key_cache:
+            c.key_cache[0], c.value_cache[0] = t, t
+        else:
+            c.key_cache.append(t)
+            c.value_cache.append(t)
+        return self.log[-1]
+
+
+def test_prefill_chunked_schedule_last_chunk():
+    m = RecordingModel()
+    c = _cache()
+    prefill_chunked(m, torch.zeros(1, 100, dtype=torch.long), c, chunk_size=32)
+    assert [e[0] for e in m.log] == ["accumulate"] * 3 + ["evict_accumulated"]
+    assert all(e[1] is False and e[2] is None for e in m.log)
+    assert [e[3] for e in m.log] == [32, 32, 32, 4]
+    assert c._prefill_mode == "single_pass"
+
+
+def test_prefill_chunked_schedule_every_chunk():
+    m = RecordingModel()
+    prefill_chunked(m, torch.zeros(1, 100, dtype=torch.long), _cache(), chunk_size=32, evict_strategy="every_chunk")
+    assert [e[0] for e in m.log] == ["single_pass"] + ["evict_accumulated"] * 3
+    assert all(e[1] is True for e in m.log)
+
+
+def test_prefill_chunked_schedule_budget():
+    m = RecordingModel()
+    c = _cache(keep_ratio=0.3)
+    prefill_chunked(m, torch.zeros(1, 256, dtype=torch.long), c, chunk_size=64, evict_strategy="budget",
+                    max_kv_tokens=128)
+    modes = [e[0] for e in m.log]
+    # 64 -> 128 (at budget, not over) -> 192 > 128: evict -> ... last: evict
+    assert modes[:3] == ["accumulate", "accumulate", "evict_accumulated"]
+    assert modes[-1] == "evict_accumulated"
+    assert all(e[2] == 128 for e in m.log)
+    assert c._budget_max_kv_tokens is None and c._evict_use_seen_tokens is False
+
+
+def test_prefill_chunked_single_chunk_shortcut():
+    m = RecordingModel()
+    c = _cache()
+    prefill_chunked(m, torch.zeros(1, 30, dtype=torch.long), c, chunk_size=32)
+    assert [e[0] for e in m.log] == ["single_pass"]

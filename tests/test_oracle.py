@@ -1,0 +1,368 @@
+"""Pins the CPU oracle (oracle/dropkv_ref.py) independently of its own code.
+
+Each oracle function is checked against something that does not share its
+formula: a float64 brute force with the direct ||v - y||^2 distance, closed
+forms, invariants and the golden fixtures (written by
+tests/golden/make_golden.py from the mathematics).  A plausible mistake --
+a dropped 1/g, a causal bound off by one, the wrong head grouping, eps
+missing, the protect value, the tie rule -- fails at least one of these.
+CPU only.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden_case, golden_names, make_qkv
+from oracle import dropkv_ref as R
+
+EPS = 1e-6
+
+
+def brute_fp64(Q, K, V, W, p_round=None, y_round=None):
+    """float64 brute force over (b, hkv, gi, w) with the direct distance
+    ||v_j - y_m||^2 (dropkv_triton.py:29-109 semantics; rounding optional)."""
+    Q, K, V = Q.double(), K.double(), V.double()
+    B, Hq, Lq, D = Q.shape
+    Hkv, Lk = K.shape[1], K.shape[2]
+    g = Hq // Hkv
+    out = torch.zeros(B, Hkv, Lk, dtype=torch.float64)
+    for b in range(B):
+        for h in range(Hkv):
+            for gi in range(g):
+                for w in range(W):
+                    q = Q[b, h * g + gi, Lq - W + w]
+                    bound = Lk - W + w
+                    logit = K[b, h, :bound + 1] @ q / math.sqrt(D)
+                    p = torch.softmax(logit, 0)
+                    if p_round is not None:
+                        p = p.float().to(p_round).double()
+                    y = p @ V[b, h, :bound + 1]
+                    if y_round is not None:
+                        y = y.float().to(y_round).double()
+                    wt = (p / (1.0 - p + EPS)) ** 2
+                    d2 = ((V[b, h, :bound + 1] - y) ** 2).sum(-1)
+                    out[b, h, :bound + 1] += wt * d2
+            out[b, h] /= g
+    return out
+
+
+def assert_rel(got, ref, rtol):
+    """|got-ref| <= rtol*|ref| + 1e-6*rowmax (scores span orders of magnitude)."""
+    got, ref = got.double(), ref.double()
+    atol = 1e-6 * ref.abs().amax(dim=-1, keepdim=True)
+    bad = (got - ref).abs() > rtol * ref.abs() + atol
+    assert not bad.any(), f"{int(bad.sum())} keys outside rtol {rtol}"
+
+
+SHAPES = [
+    # (B, Hq, Hkv, D, Lq, Lk, W)
+    (1, 4, 2, 32, 40, 40, 8),
+    (2, 6, 3, 16, 12, 50, 4),      # Lq < Lk, B=2, g=2
+    (1, 3, 3, 32, 20, 33, 8),      # MHA (g=1)
+    (1, 8, 2, 32, 12, 12, 9),      # Lk close to W: the first row sees 4 keys
+]
+
+
+def test_reference_l_equals_w_finite():
+    """Lk == W: row 0 sees one key, p = 1 and w = 1/eps^2; the fp32
+    expansion termA - termB + termC then cancels catastrophically at that key
+    (the reference's tests check only finiteness there, tests:385-396)."""
+    Q, K, V = make_qkv(dict(B=1, Hq=8, Hkv=2, D=32), 9, 9, dtype=torch.float32, seed=13)
+    s = R.dropkv_scores_reference(Q, K, V, 9)
+    assert torch.isfinite(s).all()
+    assert_rel(s[..., 1:], brute_fp64(Q, K, V, 9)[..., 1:], 1e-3)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_reference_fp32_vs_bruteforce(shape):
+    B, Hq, Hkv, D, Lq, Lk, W = shape
+    cfg = dict(B=B, Hq=Hq, Hkv=Hkv, D=D)
+    Q, K, V = make_qkv(cfg, Lq, Lk, dtype=torch.float32, seed=sum(shape))
+    got = R.dropkv_scores_reference(Q, K, V, W, match_pytorch_precision=False)
+    assert got.dtype == torch.float32 and got.shape == (B, Hkv, Lk)
+    assert_rel(got, brute_fp64(Q, K, V, W), 1e-4)
+
+
+@pytest.mark.parametrize("shape", SHAPES[:3])
+def test_reference_bf16_mode_vs_bruteforce(shape):
+    """p rounded to bf16 before the weight (dropkv_triton.py:88-92)."""
+    B, Hq, Hkv, D, Lq, Lk, W = shape
+    cfg = dict(B=B, Hq=Hq, Hkv=Hkv, D=D)
+    Q, K, V = make_qkv(cfg, Lq, Lk, dtype=torch.bfloat16, seed=1 + sum(shape))
+    got = R.dropkv_scores_reference(Q, K, V, W, match_pytorch_precision=True)
+    ref = brute_fp64(Q, K, V, W, p_round=torch.bfloat16)
+    # p computed in float32 vs float64 can round to different bf16 neighbours
+    # when it sits next to a rounding boundary: w then moves by ~2^-7.
+    rel = (got.double() - ref).abs() / ref.abs().clamp_min(1e-30)
+    assert rel.max() < 2e-2
+    assert (rel > 1e-4).double().mean() < 0.03
+
+
+@pytest.mark.parametrize("shape", SHAPES[:3] + [(1, 4, 2, 32, 3, 40, 8)])
+def test_fallback_vs_bruteforce(shape):
+    """Deployed path: W = min(window, Lq), p and y rounded to the input dtype
+    (dropkv_cache.py:407, :431, :434)."""
+    B, Hq, Hkv, D, Lq, Lk, W = shape
+    cfg = dict(B=B, Hq=Hq, Hkv=Hkv, D=D)
+    Q, K, V = make_qkv(cfg, Lq, Lk, dtype=torch.bfloat16, seed=2 + sum(shape))
+    got = R.fallback_scores(Q, K, V, W)
+    ref = brute_fp64(Q, K, V, min(W, Lq), p_round=torch.bfloat16, y_round=torch.bfloat16)
+    # y rounding from a float32 vs float64 accumulation can land on either
+    # side of a bf16 boundary; that moves a key's distance by ~2^-8 relative.
+    rel = (got.double() - ref).abs() / ref.abs().clamp_min(1e-30)
+    assert rel.max() < 2e-2
+    assert (rel > 1e-4).double().mean() < 0.02
+
+
+def test_fallback_close_to_reference_bf16_mode():
+    """The reference's own relation between its oracle (match=True) and the
+    deployed path (tests/test_dropkv_triton.py:105-115: rtol 5e-2, atol 5e-3)."""
+    Q, K, V = make_qkv(dict(B=1, Hq=8, Hkv=2, D=64), 256, dtype=torch.bfloat16, seed=3)
+    a = R.dropkv_scores_reference(Q, K, V, 8, match_pytorch_precision=True)
+    b = R.fallback_scores(Q, K, V, 8)
+    torch.testing.assert_close(a, b, rtol=5e-2, atol=5e-3)
+
+
+def test_v_zero_scores_zero():
+    Q, K, V = make_qkv(dict(B=1, Hq=4, Hkv=2, D=32), 30, dtype=torch.float32, seed=4)
+    s = R.dropkv_scores_reference(Q, K, torch.zeros_like(V), 8)
+    assert torch.count_nonzero(s) == 0
+
+
+def test_q_zero_uniform_closed_form():
+    """Q = 0: row w attends uniformly to keys 0..Lk-W+w, y_w = prefix mean;
+    score_j = (1/g) sum_w [j <= b_w] (p_w/(1-p_w+eps))^2 ||v_j - mean_w||^2
+    with p_w = 1/(b_w+1).  g copies of the same rows average to one copy."""
+    cfg = dict(B=1, Hq=2, Hkv=1, D=16)
+    _, K, V = make_qkv(cfg, 20, 20, dtype=torch.float32, seed=5)
+    Q = torch.zeros(1, 2, 20, 16)
+    W, Lk = 4, 20
+    got = R.dropkv_scores_reference(Q, K, V, W).double()
+    Vd = V[0, 0].double()
+    ref = torch.zeros(Lk, dtype=torch.float64)
+    for w in range(W):
+        bnd = Lk - W + w
+        p = 1.0 / (bnd + 1)
+        mean = Vd[:bnd + 1].mean(0)
+        ref[:bnd + 1] += (p / (1 - p + EPS)) ** 2 * ((Vd[:bnd + 1] - mean) ** 2).sum(-1)
+    torch.testing.assert_close(got[0, 0], ref, rtol=1e-5, atol=1e-9)
+
+
+def test_two_key_logit_gap_closed_form():
+    """Row 0 of a Lk = W+1 head sees keys 0 and 1.  With a logit gap of 4,
+    p0 = 1/(1+e^-4), y = p0 v0 + p1 v1, so row 0 gives key 0
+    (p0/(p1+eps))^2 * p1^2 ||v0-v1||^2 -- pins the weight (p/(1-p+eps))^2
+    (a weight of p^2, or of p/(1-p) unsquared, misses by orders of magnitude).
+    eps itself is below the float32 resolution of the reference's expansion
+    here; its presence is pinned by the p = 1 case of
+    test_reference_l_equals_w_finite (without it the weight is infinite)."""
+    D, W = 16, 4
+    Lk = W + 1
+    q = torch.zeros(1, 1, Lk, D)
+    q[0, 0, Lk - W, 0] = 4.0 * math.sqrt(D)    # row 0 (position Lk-W): logit gap 4
+    K = torch.zeros(1, 1, Lk, D)
+    K[0, 0, 0, 0] = 1.0                          # key 0: logit 4, key 1: logit 0
+    g = torch.Generator().manual_seed(6)
+    V = torch.randn(1, 1, Lk, D, generator=g)
+    got = R.dropkv_scores_reference(q, K, V, W).double()[0, 0, 0]
+    p0 = 1.0 / (1.0 + math.exp(-4.0))
+    p1 = 1.0 - p0
+    d01 = float(((V[0, 0, 0] - V[0, 0, 1]).double() ** 2).sum())
+    # rows w >= 1 have zero queries: uniform over keys 0..w+1
+    others = 0.0
+    for w in range(1, W):
+        n = Lk - W + w + 1
+        p = 1.0 / n
+        mean = V[0, 0, :n].double().mean(0)
+        others += (p / (1 - p + EPS)) ** 2 * float(((V[0, 0, 0].double() - mean) ** 2).sum())
+    ref = (p0 / (p1 + EPS)) ** 2 * p1 ** 2 * d01 + others
+    assert abs(got - ref) / ref < 1e-3
+
+
+def test_gqa_grouping_and_average():
+    """Query heads hkv*g .. hkv*g+g-1 belong to KV head hkv (contiguous
+    grouping, dropkv_triton.py:73); duplicating every query head g times
+    leaves the score unchanged (the 1/g average), and permuting heads inside
+    a group does not matter while moving one across groups does."""
+    cfg = dict(B=1, Hq=3, Hkv=3, D=32)
+    Q1, K, V = make_qkv(cfg, 24, 24, dtype=torch.float32, seed=7)
+    s1 = R.dropkv_scores_reference(Q1, K, V, 8)
+    Q2 = Q1.repeat_interleave(2, dim=1)        # heads 2h, 2h+1 = head h
+    s2 = R.dropkv_scores_reference(Q2, K, V, 8)
+    torch.testing.assert_close(s2, s1, rtol=1e-5, atol=1e-9)
+    Q4 = torch.cat([Q1, Q1.flip(1)], dim=1).reshape(1, 2, 3, 24, 32).transpose(1, 2).reshape(1, 6, 24, 32)
+    s4 = R.dropkv_scores_reference(Q4, K, V, 8)
+    Q5 = Q4[:, [1, 0, 2, 3, 4, 5]]             # swap inside group 0
+    torch.testing.assert_close(R.dropkv_scores_reference(Q5, K, V, 8), s4, rtol=1e-5, atol=1e-9)
+    Q6 = Q4[:, [2, 1, 0, 3, 4, 5]]             # move a head across groups
+    assert not torch.allclose(R.dropkv_scores_reference(Q6, K, V, 8), s4, rtol=1e-3)
+
+
+def test_only_query_tail_is_read():
+    """scores(Q) == scores(Q[..., -W:, :]) bit for bit; rows before the tail
+    can hold anything."""
+    cfg = dict(B=1, Hq=4, Hkv=2, D=32)
+    Q, K, V = make_qkv(cfg, 40, 64, dtype=torch.float32, seed=8)
+    a = R.dropkv_scores_reference(Q, K, V, 8)
+    Qn = Q.clone()
+    Qn[:, :, :-8] = float("nan")
+    b = R.dropkv_scores_reference(Qn[:, :, -8:], K, V, 8)
+    c = R.dropkv_scores_reference(Qn, K, V, 8)
+    assert torch.equal(a, b) and torch.equal(a, c)
+
+
+def test_causal_bound_tail_aligned():
+    """Key Lk-W+w+1 .. is invisible to window row w: changing the last key
+    only changes the score of that key through the last row."""
+    cfg = dict(B=1, Hq=2, Hkv=1, D=16)
+    Q, K, V = make_qkv(cfg, 16, 16, dtype=torch.float64, seed=9)
+    W = 4
+    ref = brute_fp64(Q, K, V, W)
+    K2 = K.clone()
+    K2[0, 0, -1] *= 3.0
+    ref2 = brute_fp64(Q, K2, V, W)
+    # rows 0..W-2 never see key Lk-1; only the last row does -> every key's
+    # score changes (through that row's softmax) but the contribution of rows
+    # 0..W-2 to key Lk-2 is unchanged: check via the brute force per row
+    got = R.dropkv_scores_reference(Q.float(), K.float(), V.float(), W).double()
+    got2 = R.dropkv_scores_reference(Q.float(), K2.float(), V.float(), W).double()
+    torch.testing.assert_close(got, ref, rtol=1e-5, atol=1e-9)
+    torch.testing.assert_close(got2, ref2, rtol=1e-5, atol=1e-9)
+
+
+def test_scores_nonnegative_up_to_rounding():
+    Q, K, V = make_qkv(dict(B=1, Hq=8, Hkv=2, D=64), 128, dtype=torch.bfloat16, seed=10)
+    s = R.dropkv_scores_reference(Q, K, V, 8, match_pytorch_precision=True)
+    assert (s >= -1e-6 * s.abs().max()).all()
+
+
+# ---------------------------------------------------------------------------
+# pool / protect / keep length / top-k / gather
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("ks,window", [(11, 8), (1, 8), (3, 0), (7, 32)])
+def test_pool_protect_bruteforce(ks, window):
+    g = torch.Generator().manual_seed(ks * 10 + window)
+    s = torch.randn(2, 3, 100, generator=g)
+    got = R.pool_protect(s.clone(), ks, window)
+    h = ks // 2
+    ref = torch.empty_like(s)
+    for j in range(100):
+        ref[..., j] = s[..., max(0, j - h):min(100, j + h + 1)].amax(-1)
+    big = ref.amax(-1, keepdim=True) + 1.0
+    if window > 0:
+        ref[..., 100 - window:] = big
+    assert torch.equal(got, ref)
+
+
+def test_protect_big_absorbed_in_float32():
+    """max >= 2^24: max + 1.0f == max (dropkv_cache.py:465 in fp32)."""
+    s = torch.zeros(1, 1, 50)
+    s[0, 0, 10] = 2.0 ** 25
+    got = R.pool_protect(s.clone(), 3, 4)
+    assert (got[0, 0, -4:] == 2.0 ** 25).all()
+
+
+@pytest.mark.parametrize("ratio,L,expect", [
+    (0.1, 512, 51), (0.1, 32768, 3276), (0.1, 16384, 1638), (0.1, 65536, 6553),
+    (0.05, 131072, 6553), (0.3, 128, 38), (0.01, 64, 8), (1.0, 100, 100),
+])
+def test_keep_length_table(ratio, L, expect):
+    assert R.keep_length(ratio, L, 8) == expect
+
+
+def test_keep_length_total_tokens_and_cap():
+    """Reference tests:909-937, :1183-1204."""
+    assert R.keep_length(0.3, 128, 8, total_tokens=512) == 128     # capped at seq_len
+    assert R.keep_length(0.3, 128, 8, total_tokens=200) == 60
+    assert R.keep_length(0.01, 64, 8, total_tokens=10) == 8         # window floor
+    assert R.keep_length(0.8, 512, 8, total_tokens=512, max_keep_len=100) == 100
+    assert R.keep_length(0.5, 4, 8) == 4                            # never above seq_len
+
+
+def _rank_rule(x, keep):
+    n = x.numel()
+    return [i for i in range(n)
+            if int((x > x[i]).sum()) + int((x[:i] == x[i]).sum()) < keep]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_topk_sorted_rank_rule(seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randint(0, 6, (4, 40), generator=g).float()
+    keep = 1 + seed * 5
+    got = R.topk_sorted(x.view(1, 4, 40), keep)[0]
+    for r in range(4):
+        assert got[r].tolist() == _rank_rule(x[r], keep)
+
+
+def test_topk_sorted_vs_torch_topk_tie_aware():
+    g = torch.Generator().manual_seed(11)
+    x = torch.randint(0, 30, (1, 3, 500), generator=g).float()
+    pooled = R.pool_protect(x.clone(), 11, 8)
+    keep = 77
+    mine = R.topk_sorted(pooled, keep)
+    theirs = torch.sort(torch.topk(pooled, keep, dim=-1).indices, dim=-1).values
+    worst, unexcused = R.index_overlap(mine, theirs, pooled)
+    assert unexcused == 0 and worst == 1.0
+    for r in range(3):   # equal multisets of kept values
+        assert torch.equal(torch.sort(pooled[0, r, mine[0, r]]).values,
+                           torch.sort(pooled[0, r, theirs[0, r]]).values)
+
+
+def test_index_overlap_catches_planted_mistake():
+    pooled = torch.arange(20, dtype=torch.float32).view(1, 1, 20).clone()
+    pooled[0, 0, 10] = pooled[0, 0, 11] = 100.0          # a tie pair, above everything
+    ref = R.topk_sorted(pooled, 5)                        # 10, 11, 17, 18, 19
+    assert ref[0, 0].tolist() == [10, 11, 17, 18, 19]
+    wrong = ref.clone()
+    wrong[0, 0, 3] = 3                                    # 18 -> 3: neither is a tie
+    worst, unexcused = R.index_overlap(torch.sort(wrong, -1).values, ref, pooled)
+    assert unexcused == 2 and worst == pytest.approx(1 - 2 / 5)
+    wrong = ref.clone()
+    wrong[0, 0, 2] = 3                                    # 17 (the threshold) -> 3
+    worst, unexcused = R.index_overlap(torch.sort(wrong, -1).values, ref, pooled)
+    assert unexcused == 1                                 # only 3 is unexcused
+    pooled2 = pooled.clone()
+    pooled2[0, 0, 16] = pooled2[0, 0, 17]                 # 16 ties the threshold 17
+    ref2 = R.topk_sorted(pooled2, 5)
+    assert ref2[0, 0].tolist() == [10, 11, 16, 18, 19]   # lowest index wins the tie
+    swapped = ref2.clone()
+    swapped[0, 0, 2] = 17
+    worst, unexcused = R.index_overlap(torch.sort(swapped, -1).values, ref2, pooled2)
+    assert unexcused == 0
+
+
+def test_gather_bit_exact():
+    g = torch.Generator().manual_seed(12)
+    K = torch.randn(2, 3, 50, 8, generator=g).to(torch.bfloat16)
+    V = torch.randn(2, 3, 50, 8, generator=g).to(torch.bfloat16)
+    idx = torch.sort(torch.randint(0, 50, (2, 3, 9), generator=g), -1).values
+    k, v = R.gather_compressed(K, V, idx)
+    for b in range(2):
+        for h in range(3):
+            assert torch.equal(k[b, h], K[b, h, idx[b, h]])
+            assert torch.equal(v[b, h], V[b, h, idx[b, h]])
+
+
+# ---------------------------------------------------------------------------
+# golden fixtures (float64 brute force written by tests/golden/make_golden.py)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", golden_names())
+def test_oracle_vs_golden(name):
+    c = golden_case(name)
+    B, Hq, Hkv, D, Lq, Lk, W, ks, keep = c["meta"]
+    q, k, v = c["q"], c["k"], c["v"]
+    if "exact" in c:
+        assert_rel(R.dropkv_scores_reference(q, k, v, W, match_pytorch_precision=False), c["exact"], 1e-4)
+        assert_rel(R.dropkv_scores_reference(q, k, v, W, match_pytorch_precision=True), c["bf16p"], 1e-4)
+        assert torch.equal(R.topk_sorted(c["pooled_bf16p"], keep), c["keep_idx_bf16p"])
+        assert torch.equal(R.pool_protect(torch.from_numpy(c["bf16p_np"].astype(np.float32)), ks, W),
+                           c["pooled_bf16p"])
+    assert_rel(R.fallback_scores(q, k, v, W), c["deployed"], 1e-4)
+    assert torch.equal(R.topk_sorted(c["pooled_deployed"], keep), c["keep_idx_deployed"])
+    assert R.keep_length(float(c["ratio"]), Lk, W) == keep
