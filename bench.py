@@ -9,24 +9,35 @@ cache, i.e. one ``dropkv_evict`` call on inputs already resident in HBM.
 
 Prints one JSON line.  ``value`` is the K/V bytes read once per layer-call
 (2*B*Hkv*Lk*D*2 = 134,217,728 B) divided by the measured time per step, in
-GB/s.  ``roofline`` describes the longest kernel of the call, timed with HIP
-events recorded on the library's stream inside the timed region.
-``cpu_baseline`` times the CPU oracle of the deployed path
+GB/s.  ``roofline`` describes the longest kernel of the call: its duration is
+measured with HIP events that the library records on its own launch stream
+right before and after each kernel (``dropkv_timing_*``), averaged over the
+timed steps.  ``cpu_baseline`` times the CPU oracle of the deployed path
 (score -> pool -> top-k -> sort -> gather) on the same inputs.
+
+Other modes: ``--kernels-only`` (warm-up + steps, no extras; for profiler
+runs), ``--copy-calibration MIB`` (a plain device copy, to scale the HBM byte
+counters), ``--pmc-summary DIR...`` (turn rocprofv3 counter CSVs into the
+traffic summary kept under profiles/).
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes
+import glob
 import json
 import os
 import statistics
 import sys
 import time
 
+ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBPS = 8000.0
-STAGES = ("pass1_partials", "merge", "pass2_scores", "select_final", "select_pool", "select_cand", "emit_compact")
+# kernels of one dropkv_evict call, in launch order
+STAGES = ("pass1_partials", "merge", "pass2_scores", "select_pool", "select_cand", "select_final", "emit_compact")
+STREAM_STAGES = ("pass1_partials", "pass2_scores")  # the kernels that stream all of K and V
 
 WORKLOADS = {
     "llama8b_layer_32k": dict(B=1, Hq=32, Hkv=8, D=128, Lq=32768, Lk=32768, window=8, kernel=11, ratio=0.1,
@@ -51,12 +62,14 @@ def make_inputs(cfg, seed=0):
     return Q, K.to(torch.bfloat16), V
 
 
-def cpu_baseline(Qt, K, V, cfg, keep, reps=3):
-    """Deployed path restated on the CPU (oracle), timed on this host."""
+def cpu_baseline(Qt, K, V, cfg, min_seconds=10.0, max_reps=400):
+    """Deployed path restated on the CPU (oracle), timed on this host: the
+    full layer-call repeated until ``min_seconds`` of samples (at least 3)."""
     import torch
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, ROOT)
     from oracle import dropkv_ref as R
-    n = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    n = len(os.sched_getaffinity(0))
+    n = min(n, int(os.environ.get("OMP_NUM_THREADS", n)))
     torch.set_num_threads(n)
 
     def one():
@@ -65,14 +78,15 @@ def cpu_baseline(Qt, K, V, cfg, keep, reps=3):
 
     one()  # warm-up
     times = []
-    for _ in range(reps):
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < min_seconds and len(times) < max_reps):
         t0 = time.perf_counter()
         one()
         times.append(time.perf_counter() - t0)
-    return statistics.median(times), n, reps
+    return statistics.median(times), n, len(times), sum(times)
 
 
-def parity(Qt, K, V, cfg, keep, gpu_idx):
+def parity(Qt, K, V, cfg, gpu_idx):
     """Tie-aware overlap of the GPU selection with the oracle's (scores from
     dropkv_scores_reference(match_pytorch_precision=True), pool, protect,
     top-k)."""
@@ -80,8 +94,58 @@ def parity(Qt, K, V, cfg, keep, gpu_idx):
     ref_scores = R.dropkv_scores_reference(Qt, K, V, cfg["window"], match_pytorch_precision=True)
     ref_idx, pooled = R.compute_keep_indices(Qt, K, V, cfg["ratio"], cfg["window"], cfg["kernel"],
                                              scores=ref_scores)
-    worst, unexcused = R.index_overlap(gpu_idx, ref_idx, pooled)
-    return worst, unexcused
+    return R.index_overlap(gpu_idx, ref_idx, pooled)
+
+
+def _read_counter_csvs(d):
+    """{kernel name: [per-dispatch value]} from a rocprofv3 --pmc run dir
+    (``*counter_collection.csv``)."""
+    out = {}
+    for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                out.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return out
+
+
+def pmc_summary(fetch_dir, write_dir, calib_fetch_dir, calib_write_dir, calib_mib, workload):
+    """HBM bytes per launch of each kernel: FETCH_SIZE / WRITE_SIZE (KiB per
+    dispatch) scaled by what the same counters read for a plain copy of
+    ``calib_mib`` MiB (read and written once)."""
+    fetch, write = _read_counter_csvs(fetch_dir), _read_counter_csvs(write_dir)
+    cf, cw = _read_counter_csvs(calib_fetch_dir), _read_counter_csvs(calib_write_dir)
+    copy_f = statistics.median(max(cf.values(), key=len))
+    copy_w = statistics.median(max(cw.values(), key=len))
+    true_kib = calib_mib * 1024.0
+    sf, sw = true_kib / copy_f, true_kib / copy_w
+    rows = {}
+    for name, vals in fetch.items():
+        short = next((s for s in ("pass1", "pass2", "merge", "sel_pool", "sel_cand", "sel_final", "sel_emit",
+                                  "compact") if s in name), None)
+        if short is None:
+            continue
+        fk = statistics.mean(vals)
+        wk = statistics.mean(write.get(name, [0.0]))
+        rows[short] = {"fetch_bytes": round(fk * sf * 1024), "write_bytes": round(wk * sw * 1024),
+                       "fetch_kib_raw": round(fk, 1), "write_kib_raw": round(wk, 1), "dispatches": len(vals)}
+    summary = {"workload": workload,
+               "commands": [
+                   "rocprofv3 --pmc FETCH_SIZE -f csv -d FETCH_DIR -o f -- python -u bench.py --kernels-only "
+                   f"--workload {workload} --steps 10 --warmup 2",
+                   "rocprofv3 --pmc WRITE_SIZE -f csv -d WRITE_DIR -o w -- python -u bench.py --kernels-only "
+                   f"--workload {workload} --steps 10 --warmup 2",
+                   f"rocprofv3 --pmc FETCH_SIZE -f csv -d CAL_FETCH_DIR -o cf -- python -u bench.py "
+                   f"--copy-calibration {calib_mib:g}",
+                   f"rocprofv3 --pmc WRITE_SIZE -f csv -d CAL_WRITE_DIR -o cw -- python -u bench.py "
+                   f"--copy-calibration {calib_mib:g}",
+                   f"python bench.py --workload {workload} --pmc-summary FETCH_DIR WRITE_DIR CAL_FETCH_DIR "
+                   f"CAL_WRITE_DIR {calib_mib:g}"],
+               "units": "bytes per dispatch = counter KiB per dispatch * 1024 * scale; scale = true copy "
+                        "KiB / counter KiB of the calibration copy",
+               "copy_calibration_mib": calib_mib, "fetch_scale": round(sf, 4),
+               "write_scale": round(sw, 4), "kernels": rows}
+    print(json.dumps(summary, indent=1))
+    return summary
 
 
 def main():
@@ -93,12 +157,20 @@ def main():
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--kernels-only", action="store_true", help="warm-up + timed steps only (profiler runs)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (20 times), to calibrate HBM byte counters")
+    ap.add_argument("--pmc-summary", nargs=5, metavar=("FETCH_DIR", "WRITE_DIR", "CAL_FETCH_DIR", "CAL_WRITE_DIR",
+                                                        "CAL_MIB"))
     args = ap.parse_args()
+    if args.pmc_summary:
+        f, w, cf, cw, mib = args.pmc_summary
+        pmc_summary(f, w, cf, cw, float(mib), args.workload)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the eviction path "
-              f"shards by KV head with no communication, see DESIGN.md", file=sys.stderr)
+              f"shards by KV head with no communication (see DESIGN.md, 'Sharding')", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -127,7 +199,6 @@ def main():
     for _ in range(args.warmup):
         plan(Qg, Kg, Vg)
     torch.cuda.synchronize()
-    lib = _lib.load()
 
     def timed(fn, steps):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -140,51 +211,53 @@ def main():
         torch.cuda.synchronize()
         return start.elapsed_time(end) / steps, 1e3 * (time.perf_counter() - t0) / steps
 
-    # Eager: one dropkv_evict call per step, exactly what a caller of the
-    # drop-in API does; this is the headline figure.
+    # Headline: one dropkv_evict call per step, exactly what a caller of the
+    # drop-in API does, K steps bracketed by events on the launch stream.
+    print(f"[bench] timing {args.steps} layer-calls", file=sys.stderr, flush=True)
     ms_per_step, wall_ms = timed(lambda: plan(Qg, Kg, Vg), args.steps)
+    if args.kernels_only:
+        print(json.dumps({"workload": args.workload, "steps": args.steps, "ms_per_step": round(ms_per_step, 5)}))
+        return
 
     # Graph: the layer-call captured once as a HIP graph and replayed.
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         plan(Qg, Kg, Vg)
     graph.replay()
-    graph_ms, graph_wall_ms = timed(graph.replay, args.steps)
+    graph_ms, _ = timed(graph.replay, args.steps)
 
-    # Per-kernel durations, live: a second capture with the library's
-    # profiler armed; every kernel of the captured call stamps its first-
-    # workgroup start / last-workgroup end from the GPU wall clock into a
-    # device slot that each replay rewrites and that is read after it.
-    stage_buf = (ctypes.c_double * (len(STAGES) + 1))()
-    sums = [0.0] * (len(STAGES) + 1)
-    _lib.check(lib.dropkv_profile_begin(1), "dropkv_profile_begin")
+    # Per-kernel durations with HIP events recorded by the library on its
+    # launch stream around each kernel (eager calls, one read per call).
+    lib = _lib.load()
+    buf = (ctypes.c_double * 16)()
+    sums, nk = None, 0
+    _lib.check(lib.dropkv_timing_enable(1), "dropkv_timing_enable")
     try:
-        g2 = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g2):
-            plan(Qg, Kg, Vg)
-        _lib.check(lib.dropkv_profile_disarm(), "dropkv_profile_disarm")
         for _ in range(args.steps):
-            g2.replay()
-            _lib.check(lib.dropkv_profile_read(0, stage_buf), "dropkv_profile_read")
-            for i in range(len(sums)):
-                sums[i] += stage_buf[i]
+            plan(Qg, Kg, Vg)
+            nk = lib.dropkv_timing_read(buf, 16)
+            if nk < 0:
+                _lib.check(-nk, "dropkv_timing_read")
+            sums = [0.0] * nk if sums is None else sums
+            for i in range(nk):
+                sums[i] += buf[i]
     finally:
-        lib.dropkv_profile_end(stage_buf, ctypes.byref(ctypes.c_int64(0)))
-    nprof = args.steps
-    prof_mode = "graph replay, GPU wall-clock stamps per kernel"
-    per_stage_us = {s: 1e3 * sums[i] / nprof for i, s in enumerate(STAGES)}
-    span_us = 1e3 * sums[len(STAGES)] / nprof
+        lib.dropkv_timing_enable(0)
+    names = STAGES if nk == len(STAGES) else tuple(f"kernel{i}" for i in range(nk))
+    kernel_us = {names[i]: 1e3 * sums[i] / args.steps for i in range(nk)}
 
     bytes_alg = 2 * B * Hkv * Lk * D * 2
     value = bytes_alg / (ms_per_step * 1e-3) / 1e9
-    dom = max(("pass1_partials", "pass2_scores"), key=lambda s: per_stage_us[s])
-    achieved = bytes_alg / (per_stage_us[dom] * 1e-6) / 1e9
+    dom = max((s for s in STREAM_STAGES if s in kernel_us), key=lambda s: kernel_us[s])
+    achieved = bytes_alg / (kernel_us[dom] * 1e-6) / 1e9
 
     traffic = None
-    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"traffic_{args.workload}.json")
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
     if os.path.exists(tfile):
         with open(tfile) as f:
-            traffic = json.load(f).get(dom)
+            t = json.load(f)["kernels"].get(dom.split("_")[0])
+        if t:
+            traffic = t["fetch_bytes"] + t["write_bytes"]
 
     out = {
         "metric": "K/V GB/s (% HBM peak) + ms/layer for score+topk+compact at Lk=32k",
@@ -203,13 +276,12 @@ def main():
                    "window": W, "kernel_size": cfg["kernel"], "keep_ratio": cfg["ratio"], "keep": keep,
                    "parallelism": "single GPU"},
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
-        "timing": "one dropkv_evict call per step (HIP events around the steps); graph = the call replayed as a HIP graph",
+        "timing": "steps x one dropkv_evict call, HIP events around the steps on the launch stream",
         "wall_ms_per_step": round(wall_ms, 5),
         "graph_ms_per_step": round(graph_ms, 5),
-        "graph_wall_ms_per_step": round(graph_wall_ms, 5),
-        "kernel_us": {k: round(v, 3) for k, v in per_stage_us.items()},
-        "kernel_timing": prof_mode,
-        "kernel_span_us": round(span_us, 3),
+        "kernel_us": {k: round(v, 3) for k, v in kernel_us.items()},
+        "kernel_timing": "HIP events recorded by the library on its launch stream before/after each kernel "
+                         "(includes the dispatch gap), mean over the steps",
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "bytes_per_launch": bytes_alg},
@@ -218,17 +290,18 @@ def main():
     Qt = Q[:, :, -W:, :].contiguous()  # only the tail is ever read
     if not args.no_parity:
         print("[bench] parity vs CPU oracle", file=sys.stderr, flush=True)
-        worst, unexcused = parity(Qt, K, V, cfg, keep, plan.keep_idx.cpu())
+        worst, unexcused = parity(Qt, K, V, cfg, plan.keep_idx.cpu())
         out["parity"] = {"min_row_overlap_tie_aware": round(worst, 6), "unexcused_index_diffs": unexcused,
                          "rows": B * Hkv, "keep": keep}
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
-        t_cpu, n, reps = cpu_baseline(Qt, K, V, cfg, keep)
+        t_cpu, n, reps, total = cpu_baseline(Qt, K, V, cfg, min_seconds=args.cpu_seconds)
         out["cpu_baseline"] = {"value": round(bytes_alg / t_cpu / 1e9, 3), "unit": "GB/s", "cores": n,
                                "kind": "port", "ms_per_layer_call": round(1e3 * t_cpu, 2),
-                               "sample": f"the full {args.workload} layer-call (median of {reps} after 1 warm-up), "
-                                         "deployed-path restatement: fallback score, max-pool, protect, top-k, "
-                                         "sort, gather; torch CPU, Q tail only"}
+                               "sample": f"the full {args.workload} layer-call repeated {reps} times "
+                                         f"({total:.1f} s, median reported) after 1 warm-up; deployed-path "
+                                         "restatement (oracle): fallback score, max-pool, protect, top-k, sort, "
+                                         "gather; torch CPU, Q tail only"}
     print(json.dumps(out), flush=True)
 
 

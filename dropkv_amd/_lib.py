@@ -50,6 +50,8 @@ _SIGNATURES = {
     "dropkv_profile_end": (_c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64)]),
     "dropkv_profile_read": (_c_int, [_c_i64, ctypes.POINTER(ctypes.c_double)]),
     "dropkv_profile_disarm": (_c_int, []),
+    "dropkv_timing_enable": (_c_int, [_c_int]),
+    "dropkv_timing_read": (_c_int, [ctypes.POINTER(ctypes.c_double), _c_int]),
     "dropkv_selftest_mfma": (_c_int, [_c_vp, _c_vp]),
 }
 

@@ -102,10 +102,34 @@ int prof_slot_ms(const uint64_t* host_slot, double* stage_ms) {
   return DROPKV_OK;
 }
 
+// Event-based stage timing (dropkv_timing_*), per calling thread: event 0
+// is recorded when a timed API call starts, event i+1 after its i-th kernel.
+constexpr int kMaxTimedKernels = 16;
+struct Timing {
+  bool on = false, created = false;
+  int n = 0;  // events recorded by the most recent call
+  hipEvent_t ev[kMaxTimedKernels + 1];
+};
+thread_local Timing t_timing;
+
+// Called at the start of every API entry that launches kernels.
+void timing_start(hipStream_t st) {
+  Timing& t = t_timing;
+  t.n = 0;
+  if (!t.on) return;
+  if (hipEventRecord(t.ev[0], st) == hipSuccess) t.n = 1;
+}
+
 }  // namespace
 
 namespace dkv {
 uint64_t* prof_slot() { return t_prof_slot; }
+
+void timing_mark(hipStream_t st) {
+  Timing& t = t_timing;
+  if (!t.on || t.n < 1 || t.n > kMaxTimedKernels) return;
+  if (hipEventRecord(t.ev[t.n], st) == hipSuccess) ++t.n;
+}
 }  // namespace dkv
 
 extern "C" {
@@ -137,6 +161,7 @@ int dropkv_scores(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64
   const dkv::ScorePlan p = dkv::make_score_plan(B, Hq, Hkv, Lk, D, W, splits);
   if (!workspace || workspace_bytes < p.total)
     return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", p.total, workspace_bytes);
+  timing_start(static_cast<hipStream_t>(stream));
   return hip_status(dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Hkv,
                                        (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, scores,
                                        static_cast<char*>(workspace), nullptr, 0, static_cast<hipStream_t>(stream)),
@@ -182,6 +207,7 @@ int dropkv_select(const float* scores, int64_t rows, int64_t Lk, int64_t kernel_
   const size_t need = dkv::select_workspace_bytes(rows, Lk);
   if (!workspace || workspace_bytes < need)
     return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+  timing_start(static_cast<hipStream_t>(stream));
   return hip_status(dkv::launch_select(scores, (int)rows, (int)Lk, (int)kernel_size, (int)window, (int)keep, keep_idx,
                                        pooled, static_cast<char*>(workspace), false, nullptr,
                                        static_cast<hipStream_t>(stream)),
@@ -204,6 +230,7 @@ int dropkv_compact(const void* k, const void* v, int64_t s_b, int64_t s_h, int64
   int rc = check_compact_common(idx, elem_bytes, B, H, D, keep, k_out, v_out);
   if (rc) return rc;
   if (!k || !v) return fail(DROPKV_E_ARG, "null k/v pointer");
+  timing_start(static_cast<hipStream_t>(stream));
   return hip_status(dkv::launch_compact(k, v, s_b, s_h, s_l, L, nullptr, nullptr, 0, 0, 0, 0, elem_bytes, B, H, D,
                                         idx, keep, k_out, v_out, static_cast<hipStream_t>(stream)),
                     "dropkv_compact launch");
@@ -218,6 +245,7 @@ int dropkv_compact2(const void* k0, const void* v0, int64_t s0_b, int64_t s0_h, 
   if (rc) return rc;
   if ((L0 > 0 && (!k0 || !v0)) || (L1 > 0 && (!k1 || !v1))) return fail(DROPKV_E_ARG, "null segment pointer");
   if (L0 < 0 || L1 < 0) return fail(DROPKV_E_ARG, "segment lengths must be >= 0");
+  timing_start(static_cast<hipStream_t>(stream));
   return hip_status(dkv::launch_compact(k0, v0, s0_b, s0_h, s0_l, L0, k1, v1, s1_b, s1_h, s1_l, L1, elem_bytes, B, H,
                                         D, idx, keep, k_out, v_out, static_cast<hipStream_t>(stream)),
                     "dropkv_compact2 launch");
@@ -260,6 +288,7 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
     }
     ~SlotGuard() { t_prof_slot = nullptr; }
   } slot_guard(st);
+  timing_start(st);
   char* sel_ws = ws + p.total + s_bytes;
   hipError_t e = dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Hkv,
                                     (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws,
@@ -334,6 +363,40 @@ int dropkv_profile_end(double* stage_ms, int64_t* calls) {
   if (calls) *calls = g_prof.calls;
   prof_release_locked();
   return DROPKV_OK;
+}
+
+int dropkv_timing_enable(int on) {
+  Timing& t = t_timing;
+  (void)hipGetLastError();
+  if (on && !t.created) {
+    for (int i = 0; i <= kMaxTimedKernels; ++i) {
+      hipError_t e = hipEventCreate(&t.ev[i]);
+      if (e != hipSuccess) {
+        for (int j = 0; j < i; ++j) (void)hipEventDestroy(t.ev[j]);
+        return hip_status(e, "hipEventCreate");
+      }
+    }
+    t.created = true;
+  }
+  t.on = on != 0;
+  t.n = 0;
+  return DROPKV_OK;
+}
+
+int dropkv_timing_read(double* stage_ms, int cap) {
+  Timing& t = t_timing;
+  if (!stage_ms || cap < 0) return -fail(DROPKV_E_ARG, "null stage_ms");
+  if (t.n < 2) return 0;
+  hipError_t e = hipEventSynchronize(t.ev[t.n - 1]);
+  if (e != hipSuccess) return -hip_status(e, "hipEventSynchronize");
+  const int kernels = t.n - 1;
+  for (int i = 0; i < kernels && i < cap; ++i) {
+    float ms = 0.f;
+    e = hipEventElapsedTime(&ms, t.ev[i], t.ev[i + 1]);
+    if (e != hipSuccess) return -hip_status(e, "hipEventElapsedTime");
+    stage_ms[i] = ms;
+  }
+  return kernels;
 }
 
 int dropkv_selftest_mfma(float* out, void* stream) {

@@ -101,6 +101,7 @@ hipError_t launch_compact(const void* k0, const void* v0, int64_t s0b, int64_t s
     hipLaunchKernelGGL(compact_kernel<uint8_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)row_bytes, idx,
                        (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo), prof);
   }
+  timing_mark(st);
   return hipGetLastError();
 }
 

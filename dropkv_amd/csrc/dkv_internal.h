@@ -17,6 +17,11 @@ namespace dkv {
 enum Stage { kStPass1 = 0, kStMerge, kStPass2, kStSelZero, kStSelPool, kStSelTopk, kStCompact, kNumStages };
 uint64_t* prof_slot();
 
+// Event-based stage timing (dropkv_timing_*): when enabled on the calling
+// thread, every launch helper calls timing_mark(stream) right after each
+// kernel launch, recording the next HIP event of the current call.
+void timing_mark(hipStream_t st);
+
 // Launch geometry and workspace layout of one scoring call.
 struct ScorePlan {
   int heads, g, M, n_mc, mpad;

@@ -743,8 +743,10 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
     hipLaunchKernelGGL((pass1_kernel<T, D, 4, 2>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
                        Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, prof);
   }
+  timing_mark(st);
   hipLaunchKernelGGL((merge_kernel<T, D>), dim3(p.heads * p.mpad), dim3(kMergeThreads), 0, st, part_ml, part_y,
                      p.n_mc, p.s1, p.M, y_round, yhl, ystat, yf, zero_ptr, zero_words, prof);
+  timing_mark(st);
   const int cg = min(p.n_mc, 2);
   const size_t lds2 = (size_t)cg * 3 * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
   const dim3 g2(p.heads * p.s2);
@@ -757,6 +759,7 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
                        Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, yhl, ystat, scores,
                        prof);
   }
+  timing_mark(st);
   return hipGetLastError();
 }
 

@@ -562,11 +562,15 @@ hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int wind
     const int64_t zn = (int64_t)rows * kRowWords;
     hipLaunchKernelGGL(sel_zero_kernel, dim3((unsigned)std::min<int64_t>((zn + kSelT - 1) / kSelT, 1024)),
                        dim3(kSelT), 0, st, ws.rowws, zn, prof);
+    timing_mark(st);
   }
   const dim3 grid((unsigned)(rows * chunks));
   hipLaunchKernelGGL(sel_pool_kernel, grid, dim3(kSelT), 0, st, scores, Lk, ks, window, chunks, ws, prof);
+  timing_mark(st);
   hipLaunchKernelGGL(sel_cand_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, ws, prof);
+  timing_mark(st);
   hipLaunchKernelGGL(sel_final_kernel, dim3((unsigned)rows), dim3(kSelT), 0, st, chunks, ws, (int64_t)Lk, prof);
+  timing_mark(st);
   CompactArgs ca{};
   if (cp) {
     ca.k = static_cast<const uint8_t*>(cp->k);
@@ -581,6 +585,7 @@ hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int wind
   }
   hipLaunchKernelGGL(sel_emit_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, ws, out_idx, pooled_out,
                      ca, prof);
+  timing_mark(st);
   return hipGetLastError();
 }
 

@@ -156,6 +156,20 @@ int dropkv_profile_read(int64_t slot, double* stage_ms);
 int dropkv_profile_disarm(void);
 int dropkv_profile_end(double* stage_ms, int64_t* calls);
 
+/* Kernel timing with HIP events (no counterpart in the reference, which has
+ * no timers).  dropkv_timing_enable(1) makes every later dropkv_scores /
+ * dropkv_select / dropkv_compact / dropkv_compact2 / dropkv_evict call on the
+ * calling thread record one HIP event on its stream when it starts and one
+ * right after each kernel it launches.  dropkv_timing_read waits for the
+ * last event of the most recent such call, writes the elapsed milliseconds
+ * of each of its kernels, in launch order, into stage_ms (at most cap
+ * values) and returns the number of kernels (0 if none were timed, a
+ * negative status code on error).  The elapsed time of a kernel includes the
+ * dispatch gap before it.  Only the most recent call is kept; not for use
+ * while a stream is being captured into a graph. */
+int dropkv_timing_enable(int on);
+int dropkv_timing_read(double* stage_ms, int cap);
+
 /* Self-test of the matrix-core operand layout the kernels assume: computes a
  * 16x16 fp32 product of fixed bf16 patterns with one MFMA and writes it to
  * `out` (256 floats, device memory), row-major. */
