@@ -35,9 +35,11 @@ import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBPS = 8000.0
-# kernels of one dropkv_evict call, in launch order
-STAGES = ("pass1_partials", "merge", "pass2_scores", "select_pool", "select_cand", "select_final", "emit_compact")
-STREAM_STAGES = ("pass1_partials", "pass2_scores")  # the kernels that stream all of K and V
+# kernels of one dropkv_evict call, in launch order: with the selection fused
+# into the scoring pass's tail, and with the standalone selection kernels
+STAGES_FUSED = ("pass1_partials", "merge", "pass2_scores_pool", "select_cand", "emit_compact")
+STAGES_UNFUSED = ("pass1_partials", "merge", "pass2_scores", "select_pool", "select_cand", "emit_compact")
+STREAM_STAGES = ("pass1_partials", "pass2_scores", "pass2_scores_pool")  # kernels that stream all of K and V
 
 WORKLOADS = {
     "llama8b_layer_32k": dict(B=1, Hq=32, Hkv=8, D=128, Lq=32768, Lk=32768, window=8, kernel=11, ratio=0.1,
@@ -120,7 +122,7 @@ def pmc_summary(fetch_dir, write_dir, calib_fetch_dir, calib_write_dir, calib_mi
     sf, sw = true_kib / copy_f, true_kib / copy_w
     rows = {}
     for name, vals in fetch.items():
-        short = next((s for s in ("pass1", "pass2", "merge", "sel_pool", "sel_cand", "sel_final", "sel_emit",
+        short = next((s for s in ("pass1", "pass2", "merge", "sel_pool", "sel_cand", "sel_emit",
                                   "compact") if s in name), None)
         if short is None:
             continue
@@ -243,7 +245,8 @@ def main():
                 sums[i] += buf[i]
     finally:
         lib.dropkv_timing_enable(0)
-    names = STAGES if nk == len(STAGES) else tuple(f"kernel{i}" for i in range(nk))
+    names = {len(STAGES_FUSED): STAGES_FUSED, len(STAGES_UNFUSED): STAGES_UNFUSED}.get(
+        nk, tuple(f"kernel{i}" for i in range(nk)))
     kernel_us = {names[i]: 1e3 * sums[i] / args.steps for i in range(nk)}
 
     bytes_alg = 2 * B * Hkv * Lk * D * 2

@@ -46,10 +46,6 @@ _SIGNATURES = {
                               _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                               _c_float, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
                               _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
-    "dropkv_profile_begin": (_c_int, [_c_i64]),
-    "dropkv_profile_end": (_c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64)]),
-    "dropkv_profile_read": (_c_int, [_c_i64, ctypes.POINTER(ctypes.c_double)]),
-    "dropkv_profile_disarm": (_c_int, []),
     "dropkv_timing_enable": (_c_int, [_c_int]),
     "dropkv_timing_read": (_c_int, [ctypes.POINTER(ctypes.c_double), _c_int]),
     "dropkv_selftest_mfma": (_c_int, [_c_vp, _c_vp]),

@@ -62,46 +62,6 @@ int check_score_args(const void* q, const void* k, const void* v, int dtype, int
   return DROPKV_OK;
 }
 
-// Timestamp profiler state (dropkv_profile_*): one device slot of
-// 2*kNumStages uint64 per profiled layer-call.
-struct Profiler {
-  std::mutex mu;
-  bool armed = false;
-  int64_t max_calls = 0, calls = 0;
-  uint64_t* dev = nullptr;
-  double tick_ms = 0.0;  // wall-clock tick length in ms
-};
-Profiler g_prof;
-thread_local uint64_t* t_prof_slot = nullptr;
-
-void prof_release_locked() {
-  if (g_prof.dev) (void)hipFree(g_prof.dev);
-  g_prof.dev = nullptr;
-  g_prof.armed = false;
-  g_prof.max_calls = g_prof.calls = 0;
-}
-
-__global__ void prof_reset_kernel(uint64_t* slot) {
-  const int i = threadIdx.x;
-  if (i < 2 * dkv::kNumStages) slot[i] = (i & 1) ? 0ull : ~0ull;
-}
-
-int prof_slot_ms(const uint64_t* host_slot, double* stage_ms) {
-  for (int s = 0; s < dkv::kNumStages; ++s) {
-    const uint64_t t0 = host_slot[2 * s], t1 = host_slot[2 * s + 1];
-    stage_ms[s] = (t1 > 0 && t0 != ~0ull && t1 >= t0) ? (double)(t1 - t0) * g_prof.tick_ms : 0.0;
-  }
-  uint64_t first = ~0ull, last = 0;
-  for (int s = 0; s < dkv::kNumStages; ++s) {
-    if (host_slot[2 * s + 1] > 0 && host_slot[2 * s] != ~0ull) {
-      first = std::min(first, host_slot[2 * s]);
-      last = std::max(last, host_slot[2 * s + 1]);
-    }
-  }
-  stage_ms[dkv::kNumStages] = last > 0 ? (double)(last - first) * g_prof.tick_ms : 0.0;
-  return DROPKV_OK;
-}
-
 // Event-based stage timing (dropkv_timing_*), per calling thread: event 0
 // is recorded when a timed API call starts, event i+1 after its i-th kernel.
 constexpr int kMaxTimedKernels = 16;
@@ -123,8 +83,6 @@ void timing_start(hipStream_t st) {
 }  // namespace
 
 namespace dkv {
-uint64_t* prof_slot() { return t_prof_slot; }
-
 void timing_mark(hipStream_t st) {
   Timing& t = t_timing;
   if (!t.on || t.n < 1 || t.n > kMaxTimedKernels) return;
@@ -164,7 +122,8 @@ int dropkv_scores(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64
   timing_start(static_cast<hipStream_t>(stream));
   return hip_status(dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Hkv,
                                        (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, scores,
-                                       static_cast<char*>(workspace), nullptr, 0, static_cast<hipStream_t>(stream)),
+                                       static_cast<char*>(workspace), nullptr, 0, nullptr,
+                                       static_cast<hipStream_t>(stream)),
                     "dropkv_scores launch");
 }
 
@@ -278,91 +237,32 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
   char* ws = static_cast<char*>(workspace);
   float* sc = scores ? scores : reinterpret_cast<float*>(ws + p.total);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  struct SlotGuard {
-    explicit SlotGuard(hipStream_t st) {
-      std::lock_guard<std::mutex> lk(g_prof.mu);
-      if (g_prof.armed && g_prof.calls < g_prof.max_calls) {
-        t_prof_slot = g_prof.dev + (size_t)(g_prof.calls++) * 2 * dkv::kNumStages;
-        hipLaunchKernelGGL(prof_reset_kernel, dim3(1), dim3(64), 0, st, t_prof_slot);
-      }
-    }
-    ~SlotGuard() { t_prof_slot = nullptr; }
-  } slot_guard(st);
   timing_start(st);
   char* sel_ws = ws + p.total + s_bytes;
-  hipError_t e = dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Hkv,
-                                    (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws,
-                                    reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv), st);
-  if (e != hipSuccess) return hip_status(e, "dropkv_evict scores");
   // The gather runs inside the selection's emit stage when the rows allow
   // 16-byte copies; otherwise as its own kernel.
-  const bool fuse = (D * 2) % 16 == 0 && aligned16(k_out) && aligned16(v_out);
+  const bool vec = (D * 2) % 16 == 0 && aligned16(k_out) && aligned16(v_out);
   const dkv::SelectCompact cp{k, v, Hkv * Lk * D, Lk * D, D, 2, D, (int)Hkv, k_out, v_out};
-  e = dkv::launch_select(sc, (int)(B * Hkv), (int)Lk, (int)kernel_size, (int)protect_window, (int)keep, keep_idx,
-                         nullptr, sel_ws, true, fuse ? &cp : nullptr, st);
+  // Pooling runs in the tail of the scoring pass when the plan allows it;
+  // otherwise as the standalone selection's pool kernel.
+  const bool fused = dkv::select_after_pool_ok(p.s2, p.kps2, Lk, kernel_size);
+  const dkv::FuseSelect fs{sel_ws, (int)kernel_size, (int)protect_window};
+  hipError_t e = dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Hkv,
+                                    (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws,
+                                    reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv),
+                                    fused ? &fs : nullptr, st);
+  if (e != hipSuccess) return hip_status(e, "dropkv_evict scores");
+  if (fused)
+    e = dkv::launch_select_after_pool(sc, (int)(B * Hkv), (int)Lk, (int)kernel_size, (int)protect_window, (int)keep,
+                                      p.s2, p.kps2, keep_idx, nullptr, sel_ws, vec ? &cp : nullptr, st);
+  else
+    e = dkv::launch_select(sc, (int)(B * Hkv), (int)Lk, (int)kernel_size, (int)protect_window, (int)keep, keep_idx,
+                           nullptr, sel_ws, true, vec ? &cp : nullptr, st);
   if (e != hipSuccess) return hip_status(e, "dropkv_evict select");
-  if (fuse) return DROPKV_OK;
+  if (vec) return DROPKV_OK;
   e = dkv::launch_compact(k, v, Hkv * Lk * D, Lk * D, D, Lk, nullptr, nullptr, 0, 0, 0, 0, 2, B, Hkv, D, keep_idx,
                           keep, k_out, v_out, st);
   return hip_status(e, "dropkv_evict compact");
-}
-
-int dropkv_profile_begin(int64_t max_calls) {
-  if (max_calls < 1 || max_calls > 100000) return fail(DROPKV_E_ARG, "max_calls must be in [1, 100000]");
-  (void)hipGetLastError();
-  std::lock_guard<std::mutex> lk(g_prof.mu);
-  prof_release_locked();
-  int dev = 0, khz = 0;
-  hipError_t err = hipGetDevice(&dev);
-  if (err == hipSuccess) err = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
-  if (err != hipSuccess || khz <= 0) return hip_status(err == hipSuccess ? hipErrorInvalidValue : err, "wall clock rate");
-  g_prof.tick_ms = 1.0 / (double)khz;
-  err = hipMalloc(reinterpret_cast<void**>(&g_prof.dev), (size_t)max_calls * 2 * dkv::kNumStages * sizeof(uint64_t));
-  if (err != hipSuccess) {
-    g_prof.dev = nullptr;
-    return hip_status(err, "hipMalloc(profile slots)");
-  }
-  g_prof.max_calls = max_calls;
-  g_prof.calls = 0;
-  g_prof.armed = true;
-  return DROPKV_OK;
-}
-
-int dropkv_profile_read(int64_t slot, double* stage_ms) {
-  std::lock_guard<std::mutex> lk(g_prof.mu);
-  if (!g_prof.dev || slot < 0 || slot >= g_prof.calls)
-    return fail(DROPKV_E_ARG, "no recorded profile slot %lld", (long long)slot);
-  uint64_t host[2 * dkv::kNumStages];
-  hipError_t err = hipDeviceSynchronize();
-  if (err == hipSuccess)
-    err = hipMemcpy(host, g_prof.dev + (size_t)slot * 2 * dkv::kNumStages, sizeof(host), hipMemcpyDeviceToHost);
-  if (err != hipSuccess) return hip_status(err, "profile read");
-  return prof_slot_ms(host, stage_ms);
-}
-
-int dropkv_profile_disarm(void) {
-  std::lock_guard<std::mutex> lk(g_prof.mu);
-  g_prof.armed = false;  // recorded slots stay readable until dropkv_profile_end
-  return DROPKV_OK;
-}
-
-int dropkv_profile_end(double* stage_ms, int64_t* calls) {
-  std::lock_guard<std::mutex> lk(g_prof.mu);
-  if (!g_prof.dev) return fail(DROPKV_E_ARG, "profiler not started");
-  for (int s = 0; s <= dkv::kNumStages; ++s) stage_ms[s] = 0.0;
-  std::vector<uint64_t> host((size_t)g_prof.calls * 2 * dkv::kNumStages);
-  hipError_t err = hipDeviceSynchronize();
-  if (err == hipSuccess && !host.empty())
-    err = hipMemcpy(host.data(), g_prof.dev, host.size() * sizeof(uint64_t), hipMemcpyDeviceToHost);
-  if (err != hipSuccess) return hip_status(err, "profile end");
-  for (int64_t i = 0; i < g_prof.calls; ++i) {
-    double ms[dkv::kNumStages + 1];
-    prof_slot_ms(&host[(size_t)i * 2 * dkv::kNumStages], ms);
-    for (int s = 0; s <= dkv::kNumStages; ++s) stage_ms[s] += ms[s];
-  }
-  if (calls) *calls = g_prof.calls;
-  prof_release_locked();
-  return DROPKV_OK;
 }
 
 int dropkv_timing_enable(int on) {

@@ -65,20 +65,6 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
   return base + slot;
 }
 
-// Timestamp profiler hooks (see prof_slot() in dkv_internal.h).  `prof` is
-// uniform across the grid, so the barrier in prof_end is reached by all.
-__device__ __forceinline__ void prof_begin(uint64_t* prof, int stage) {
-  if (prof && threadIdx.x == 0)
-    atomicMin(reinterpret_cast<unsigned long long*>(prof + 2 * stage), (unsigned long long)wall_clock64());
-}
-__device__ __forceinline__ void prof_end(uint64_t* prof, int stage) {
-  if (prof) {
-    __syncthreads();
-    if (threadIdx.x == 0)
-      atomicMax(reinterpret_cast<unsigned long long*>(prof + 2 * stage + 1), (unsigned long long)wall_clock64());
-  }
-}
-
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);

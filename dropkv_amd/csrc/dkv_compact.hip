@@ -25,9 +25,7 @@ constexpr int kItems = 4;
 template <typename U>
 __global__ void __launch_bounds__(kCopyThreads)
 compact_kernel(Seg s0, Seg s1, int H, int units_per_row, const int64_t* __restrict__ idx, int keep,
-               int blocks_per_head, uint8_t* __restrict__ ko, uint8_t* __restrict__ vo,
-               uint64_t* __restrict__ prof) {
-  prof_begin(prof, kStCompact);
+               int blocks_per_head, uint8_t* __restrict__ ko, uint8_t* __restrict__ vo) {
   const int bh = blockIdx.x / blocks_per_head;
   const int r0 = (blockIdx.x % blocks_per_head) * kRowsPerBlock;
   const int b = bh / H, h = bh % H;
@@ -66,7 +64,6 @@ compact_kernel(Seg s0, Seg s1, int H, int units_per_row, const int64_t* __restri
       }
     }
   }
-  prof_end(prof, kStCompact);
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -87,19 +84,18 @@ hipError_t launch_compact(const void* k0, const void* v0, int64_t s0b, int64_t s
   vec = vec && seg_ok(a, k0, v0) && seg_ok(c, k1, v1);
   const int bph = (int)((keep + kRowsPerBlock - 1) / kRowsPerBlock);
   const dim3 grid((unsigned)(B * H * bph));
-  uint64_t* prof = prof_slot();
   if (vec) {
     hipLaunchKernelGGL(compact_kernel<uint4>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)(row_bytes / 16),
-                       idx, (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo), prof);
+                       idx, (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
   } else if (eb == 2) {
     hipLaunchKernelGGL(compact_kernel<uint16_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)D, idx,
-                       (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo), prof);
+                       (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
   } else if (eb == 4) {
     hipLaunchKernelGGL(compact_kernel<uint32_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)D, idx,
-                       (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo), prof);
+                       (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
   } else {
     hipLaunchKernelGGL(compact_kernel<uint8_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)row_bytes, idx,
-                       (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo), prof);
+                       (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
   }
   timing_mark(st);
   return hipGetLastError();

@@ -7,16 +7,6 @@
 
 namespace dkv {
 
-// Kernels of a layer-call, for the optional timestamp profiler
-// (dropkv_profile_*).  When a call is being profiled, prof_slot() returns a
-// device buffer of 2*kNumStages uint64 (per stage: first-workgroup start,
-// last-workgroup end, in wall-clock ticks) that the kernels update; otherwise
-// nullptr and the kernels skip the bookkeeping.
-// (kStSelZero times both the standalone workspace clear and the per-row
-// threshold stage; only one of them runs in a fused layer-call.)
-enum Stage { kStPass1 = 0, kStMerge, kStPass2, kStSelZero, kStSelPool, kStSelTopk, kStCompact, kNumStages };
-uint64_t* prof_slot();
-
 // Event-based stage timing (dropkv_timing_*): when enabled on the calling
 // thread, every launch helper calls timing_mark(stream) right after each
 // kernel launch, recording the next HIP event of the current call.
@@ -32,10 +22,18 @@ struct ScorePlan {
 };
 
 ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W, int64_t splits);
+// Pooling fused into the scoring pass: the selection workspace (its per-row
+// words are cleared by the merge kernel through zero_ptr) and the pooling
+// parameters.  The selection then continues with launch_select_after_pool
+// using the pass-2 split geometry (ScorePlan::s2, ::kps2).
+struct FuseSelect {
+  char* ws;
+  int ks, window;
+};
 hipError_t launch_scores(const ScorePlan& p, int dtype_bf16, int D, const void* q, int64_t q_sb, int64_t q_sh,
                          int64_t q_ss, int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk, int W,
                          float eps, int p_round, int y_round, float* scores, char* ws, uint32_t* zero_ptr,
-                         int64_t zero_words, hipStream_t st);
+                         int64_t zero_words, const FuseSelect* fuse, hipStream_t st);
 hipError_t launch_debug_state(const ScorePlan& p, const char* ws, int D, float* lse_out, float* y_out,
                               hipStream_t st);
 hipError_t launch_mfma_selftest(float* out, hipStream_t st);
@@ -59,6 +57,13 @@ struct SelectCompact {
 };
 hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int window, int keep, int64_t* out_idx,
                          float* pooled_out, char* ws, bool pre_zeroed, const SelectCompact* cp, hipStream_t st);
+// The cand and emit stages after a pooling stage that pooled every key
+// except those within kernel_size/2 of j = i*kps (1 <= i < n_splits).
+hipError_t launch_select_after_pool(const float* scores, int rows, int Lk, int ks, int window, int keep,
+                                    int n_splits, int kps, int64_t* out_idx, float* pooled_out, char* ws,
+                                    const SelectCompact* cp, hipStream_t st);
+// Whether launch_select_after_pool accepts that geometry.
+bool select_after_pool_ok(int64_t n_splits, int64_t kps, int64_t Lk, int64_t ks);
 
 hipError_t launch_compact(const void* k0, const void* v0, int64_t s0b, int64_t s0h, int64_t s0l, int64_t L0,
                           const void* k1, const void* v1, int64_t s1b, int64_t s1h, int64_t s1l, int64_t L1,

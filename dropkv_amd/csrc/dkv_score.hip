@@ -22,7 +22,9 @@
 //     along D in HBM, but the contraction here runs along keys).
 #include "dkv_common.h"
 #include "dkv_internal.h"
+#include "dkv_select_dev.h"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -121,9 +123,7 @@ __global__ void __launch_bounds__(64 * WAVES, MINW)
 pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
              const T* __restrict__ kp, const T* __restrict__ vp,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int n_splits, int kps,
-             float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y,
-             uint64_t* __restrict__ prof) {
-  prof_begin(prof, kStPass1);
+             float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y) {
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
   constexpr int DT = D / 16;
@@ -330,7 +330,6 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     for (int w = 0; w < WAVES; ++w) y += wbuf[((size_t)w * kRows + row) * kYPitch + d] * sm_f[w * kRows + row];
     py[i] = y;
   }
-  prof_end(prof, kStPass1);
 }
 
 // ---------------------------------------------------------------------------
@@ -360,8 +359,7 @@ template <typename T, int D>
 __global__ void __launch_bounds__(kMergeThreads)
 merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y, int n_mc, int n_splits,
              int M, int y_round, T* __restrict__ yhl, float* __restrict__ ystat, float* __restrict__ yf32,
-             uint32_t* __restrict__ zero_ptr, int64_t zero_words, uint64_t* __restrict__ prof) {
-  prof_begin(prof, kStMerge);
+             uint32_t* __restrict__ zero_ptr, int64_t zero_words) {
   constexpr int G = kMergeThreads / D;
   __shared__ float s_f[kMaxSplits];
   __shared__ float s_red[kMergeThreads / 64];
@@ -443,7 +441,6 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
     ystat[rbase * 2 + 0] = valid ? mx + log2f(fmaxf(l, 1e-40f)) : INFINITY;
     ystat[rbase * 2 + 1] = yn2;
   }
-  prof_end(prof, kStMerge);
 }
 
 // ---------------------------------------------------------------------------
@@ -479,6 +476,26 @@ __device__ __forceinline__ float sumsq8<_Float16>(Elem<_Float16>::v8 x, float ac
   return acc;
 }
 
+
+// ---------------------------------------------------------------------------
+// Pooling epilogue of pass 2 (a layer-call's score -> select).  Every pass-2
+// workgroup owns the key range [k_begin, k_end) of one row and, once its
+// scores are stored, pools the keys whose whole window lies in that range
+// (its interior) into the pooled row, the row maximum and the top-digit
+// histogram (pool_range).  The selection's cand stage pools the keys next to
+// the split boundaries.  The kernel boundary is the only synchronisation: an
+// in-kernel handoff between workgroups would need agent-scope
+// release/acquire, which on gfx950 writes back and invalidates an XCD's whole
+// L2 per workgroup and costs far more than a launch.
+// ---------------------------------------------------------------------------
+struct SelFuse {
+  SelWs ws;    // selection workspace; its per-row words were zeroed by merge
+  int enabled;
+  int ks, window;
+  int sc_lds;  // the workgroup's scores are also kept in LDS (kps <= kScLds)
+};
+constexpr int kScLds = 4096;  // longest split range whose scores pass 2 keeps in LDS
+
 template <typename T, int D, int WAVES, int MINW>
 __global__ void __launch_bounds__(64 * WAVES, MINW)
 pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
@@ -486,14 +503,14 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int cg, int n_splits, int kps,
              float scale_log2, float eps, int p_round,
              const T* __restrict__ yhl, const float* __restrict__ ystat, float* __restrict__ scores,
-             uint64_t* __restrict__ prof) {
-  prof_begin(prof, kStPass2);
+             SelFuse fz) {
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
   constexpr int OPS = 3 * kMB * KK;  // operand slots per row-chunk (Q, Yhi, Ylo)
   constexpr int NT = 64 * WAVES;
   extern __shared__ u32x4 opnd[];    // [cg][OPS][64] then float stats [cg][kMB][2][16]
   float* stat = reinterpret_cast<float*>(opnd + (size_t)cg * OPS * 64);
+  float* sc_row = stat + cg * kMB * 32;  // [kps] this workgroup's scores (fused pooling only)
 
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   const int split = lid % n_splits;
@@ -636,11 +653,25 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
           float* dst = scores + (int64_t)head * Lk + n;
           if (!first) v += *dst;
           *dst = last ? v * inv_g : v;
+          if (last && fz.sc_lds) sc_row[n - k_begin] = v * inv_g;
         }
       }
     }
   }
-  prof_end(prof, kStPass2);
+  if (fz.enabled) {
+    __syncthreads();  // this workgroup's score stores are done; the LDS operands are dead
+    const int h = fz.ks / 2;
+    const int i0 = split == 0 ? 0 : k_begin + h;
+    const int i1 = k_end >= Lk ? Lk : k_end - h;
+    uint32_t* L = reinterpret_cast<uint32_t*>(opnd);  // below sc: the operand region is dead
+    float* prow = fz.ws.pooled + (int64_t)head * Lk;
+    uint32_t* rw = fz.ws.rowws + (int64_t)head * kRowWords;
+    if (fz.sc_lds)
+      pool_range_lds<NT>(sc_row, k_begin, prow, rw, Lk, h, Lk - fz.window, i0, i1, L, L + kBins1);
+    else
+      pool_range<NT>(scores + (int64_t)head * Lk, prow, rw, Lk, h, Lk - fz.window, i0, i1,
+                     reinterpret_cast<float*>(L), L + kSub + 2 * kMaxHalo, L + kSub + 2 * kMaxHalo + kBins1);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -718,7 +749,7 @@ template <typename T, int D>
 static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
                                   int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk, int W,
                                   float eps, int p_round, int y_round, float* scores, char* ws,
-                                  uint32_t* zero_ptr, int64_t zero_words, hipStream_t st) {
+                                  uint32_t* zero_ptr, int64_t zero_words, const FuseSelect* fuse, hipStream_t st) {
   const float scale_log2 = 1.4426950408889634f / sqrtf((float)D);
   float* part_ml = reinterpret_cast<float*>(ws + p.off_ml);
   float* part_y = reinterpret_cast<float*>(ws + p.off_y);
@@ -729,35 +760,42 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   const T* kk = static_cast<const T*>(k);
   const T* vv = static_cast<const T*>(v);
 
-  uint64_t* prof = prof_slot();
   const bool qvec = q_sd == 1 && (q_sb % 8) == 0 && (q_sh % 8) == 0 && (q_ss % 8) == 0 &&
                     (reinterpret_cast<uintptr_t>(q) & 15u) == 0;
   const dim3 g1(p.heads * p.n_mc * p.s1);
   if (p.p1_waves == 8) {
     hipLaunchKernelGGL((pass1_kernel<T, D, 8, 1>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, prof);
+                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y);
   } else if (p.p1_occ == 1) {
     hipLaunchKernelGGL((pass1_kernel<T, D, 4, 1>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, prof);
+                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y);
   } else {
     hipLaunchKernelGGL((pass1_kernel<T, D, 4, 2>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, prof);
+                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y);
   }
   timing_mark(st);
   hipLaunchKernelGGL((merge_kernel<T, D>), dim3(p.heads * p.mpad), dim3(kMergeThreads), 0, st, part_ml, part_y,
-                     p.n_mc, p.s1, p.M, y_round, yhl, ystat, yf, zero_ptr, zero_words, prof);
+                     p.n_mc, p.s1, p.M, y_round, yhl, ystat, yf, zero_ptr, zero_words);
   timing_mark(st);
+  SelFuse fz{};
   const int cg = min(p.n_mc, 2);
-  const size_t lds2 = (size_t)cg * 3 * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
+  size_t lds2 = (size_t)cg * 3 * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
+  if (fuse) {
+    fz.enabled = 1;
+    fz.ws = sel_layout(fuse->ws, p.heads, Lk, nullptr);
+    fz.ks = fuse->ks;
+    fz.window = fuse->window;
+    fz.sc_lds = p.kps2 <= kScLds;
+    if (fz.sc_lds) lds2 += (size_t)p.kps2 * 4;  // sc_row[] after the operands and statistics
+    lds2 = std::max(lds2, (size_t)kPoolLdsWords * 4);
+  }
   const dim3 g2(p.heads * p.s2);
   if (p.p2_waves == 8) {
     hipLaunchKernelGGL((pass2_kernel<T, D, 8, 1>), g2, dim3(512), lds2, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, yhl, ystat, scores,
-                       prof);
+                       Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, yhl, ystat, scores, fz);
   } else {
     hipLaunchKernelGGL((pass2_kernel<T, D, 4, 2>), g2, dim3(256), lds2, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, yhl, ystat, scores,
-                       prof);
+                       Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, yhl, ystat, scores, fz);
   }
   timing_mark(st);
   return hipGetLastError();
@@ -766,10 +804,10 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
 hipError_t launch_scores(const ScorePlan& p, int dtype_bf16, int D, const void* q, int64_t q_sb, int64_t q_sh,
                          int64_t q_ss, int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk,
                          int W, float eps, int p_round, int y_round, float* scores, char* ws, uint32_t* zero_ptr,
-                         int64_t zero_words, hipStream_t st) {
+                         int64_t zero_words, const FuseSelect* fuse, hipStream_t st) {
 #define DKV_CASE(TT, DD)                                                                                     \
   return launch_scores_t<TT, DD>(p, q, q_sb, q_sh, q_ss, q_sd, k, v, Hkv, Lq, Lk, W, eps, p_round, y_round, \
-                                 scores, ws, zero_ptr, zero_words, st)
+                                 scores, ws, zero_ptr, zero_words, fuse, st)
   if (dtype_bf16) {
     if (D == 64) DKV_CASE(__bf16, 64);
     if (D == 128) DKV_CASE(__bf16, 128);

@@ -1,289 +1,154 @@
 // Pool / protect / top-k / ascending sort of the DropKV scores on gfx950 (the
 // selection half of DropKVCache._compute_keep_indices, dropkv_cache.py:464-475),
 // optionally fused with the gather into the compressed cache
-// (DropKVCache._gather_compressed, dropkv_cache.py:479-491).
+// (DropKVCache._gather_compressed, dropkv_cache.py:479-491).  The stages are
+// described in dkv_select_dev.h.
 //
-//   pooled[j] = max(scores[j-h .. j+h]), h = ks/2, out-of-range = -inf
-//   big = max_j pooled[j] + 1.0f ; pooled[Lk-window ..] = big
-//   keep_idx = ascending indices of the `keep` largest pooled values; among
-//              values equal to the threshold the lowest indices win.
-//
-// Floats are mapped to order-preserving uint32 keys and the keep-th largest
-// key T is found by a radix select over 11 + 11 + 10 bits.  Every stage runs
-// over (row, 1024-key chunk) workgroups, so all CUs take part:
-//   pool   sliding max, row maximum (atomicMax on keys), histogram of the top
-//          digit of the unprotected keys;
-//   cand   every chunk finds the boundary bin of the top digit, counts its
-//          keys above it and appends the keys inside it to a per-row
-//          candidate list;
-//   final  one workgroup per row resolves the two lower digits on the
-//          candidates (a few percent of the row) and turns per-chunk counts
-//          into output offsets;
-//   emit   every chunk writes its kept indices at those offsets, in index
-//          order (block prefix sums), and copies the kept K/V rows.
+// Standalone (dropkv_select): zero -> pool -> cand -> emit.
+// After a scoring pass that pooled its interiors (dropkv_evict): cand -> emit.
 #include "dkv_common.h"
 #include "dkv_internal.h"
+#include "dkv_select_dev.h"
 
 #include <algorithm>
 
 namespace dkv {
 
 constexpr int kSelT = 256;            // threads per workgroup, all stages
-constexpr int kChunk = 1024;          // keys per workgroup
 constexpr int kPer = kChunk / kSelT;  // keys per thread
-constexpr int kBins1 = 2048;          // key bits 31..21
-constexpr int kBins2 = 2048;          // key bits 20..10
-constexpr int kBins3 = 1024;          // key bits 9..0
-constexpr int kMaxHalo = 64;          // kernel_size <= 2*kMaxHalo+1
-constexpr int kMaxChunks = 4096;      // Lk <= kMaxChunks * kChunk
-constexpr int kBatch = 8;             // independent loads in flight per thread
-constexpr int kCandLds = 8192;        // candidates staged in LDS by the final stage
-
-// Per-row words that must be zero on entry:
-//   [0] max pooled key, [1 .. kBins1] top-digit histogram of the unprotected
-//   keys, [kBins1+1] candidate count.
-constexpr int kRowWords = kBins1 + 2;
-constexpr int kCandCount = kBins1 + 1;
-
-struct SelWs {
-  uint32_t* rowws;     // [rows][kRowWords], zeroed per call
-  float* pooled;       // [rows][Lk]
-  uint32_t* cand_key;  // [rows][Lk]
-  uint32_t* cand_idx;  // [rows][Lk]
-  uint32_t* above;     // [rows][chunks] keys of a chunk above the boundary bin
-  uint32_t* gt_off;    // [rows][chunks] kept keys > T in earlier chunks
-  uint32_t* eq_off;    // [rows][chunks] keys == T in earlier chunks
-  uint32_t* thr;       // [rows][2] T, number of keys == T kept
-};
-
-static inline size_t al256(size_t b) { return (b + 255) & ~size_t(255); }
-
-static SelWs sel_layout(char* base, int64_t rows, int64_t Lk, size_t* total) {
-  const int64_t chunks = (Lk + kChunk - 1) / kChunk;
-  SelWs w;
-  size_t off = 0;
-  auto take = [&](size_t bytes) {
-    char* p = base ? base + off : nullptr;
-    off += al256(bytes);
-    return p;
-  };
-  w.rowws = reinterpret_cast<uint32_t*>(take((size_t)rows * kRowWords * 4));
-  w.pooled = reinterpret_cast<float*>(take((size_t)rows * Lk * 4));
-  w.cand_key = reinterpret_cast<uint32_t*>(take((size_t)rows * Lk * 4));
-  w.cand_idx = reinterpret_cast<uint32_t*>(take((size_t)rows * Lk * 4));
-  w.above = reinterpret_cast<uint32_t*>(take((size_t)rows * chunks * 4));
-  w.gt_off = reinterpret_cast<uint32_t*>(take((size_t)rows * chunks * 4));
-  w.eq_off = reinterpret_cast<uint32_t*>(take((size_t)rows * chunks * 4));
-  w.thr = reinterpret_cast<uint32_t*>(take((size_t)rows * 2 * 4));
-  if (total) *total = off;
-  return w;
-}
-
-// ---------------------------------------------------------------------------
-// Block-level helpers for kSelT threads.
-// ---------------------------------------------------------------------------
-// Exclusive prefix sums of two counters over the threads of the block, and
-// optionally their block totals.
-__device__ __forceinline__ void block_excl_scan2(uint32_t a, uint32_t b, uint32_t* pa, uint32_t* pb,
-                                                 uint32_t* ta, uint32_t* tb, uint32_t* wsum /*[8]*/) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  uint32_t xa = a, xb = b;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t ya = __shfl_up((int)xa, o), yb = __shfl_up((int)xb, o);
-    if (lane >= o) {
-      xa += ya;
-      xb += yb;
-    }
-  }
-  __syncthreads();
-  if (lane == 63) {
-    wsum[w] = xa;
-    wsum[4 + w] = xb;
-  }
-  __syncthreads();
-  uint32_t oa = 0, ob = 0, sa = 0, sb = 0;
-#pragma unroll
-  for (int i = 0; i < kSelT / 64; ++i) {
-    if (i < w) {
-      oa += wsum[i];
-      ob += wsum[4 + i];
-    }
-    sa += wsum[i];
-    sb += wsum[4 + i];
-  }
-  *pa = oa + xa - a;
-  *pb = ob + xb - b;
-  if (ta) *ta = sa;
-  if (tb) *tb = sb;
-}
-
-// For a histogram of NB bins in LDS and 1 <= k <= total: the bin b with
-// (count of keys in bins > b) < k <= (count in bins >= b), and the count in
-// bins > b.  Results land in *s_bin / *s_above (LDS); ends with a barrier.
-template <int NB>
-__device__ void find_bin(const uint32_t* hist, uint32_t k, int* s_bin, uint32_t* s_above, uint32_t* wsum) {
-  constexpr int per = NB / kSelT;
-  const int tid = threadIdx.x;
-  uint32_t loc[per];
-  uint32_t tsum = 0u;
-#pragma unroll
-  for (int i = 0; i < per; ++i) {
-    loc[i] = hist[NB - 1 - (tid * per + i)];  // thread order = descending bins
-    tsum += loc[i];
-  }
-  uint32_t run, dummy;
-  block_excl_scan2(tsum, 0u, &run, &dummy, nullptr, nullptr, wsum);
-#pragma unroll
-  for (int i = 0; i < per; ++i) {
-    const uint32_t nxt = run + loc[i];
-    if (run < k && nxt >= k) {
-      *s_bin = NB - 1 - (tid * per + i);
-      *s_above = run;
-    }
-    run = nxt;
-  }
-  __syncthreads();
-}
+constexpr int kUnroll = 8;            // candidate loads in flight per thread
 
 __global__ void __launch_bounds__(kSelT)
-sel_zero_kernel(uint32_t* __restrict__ p, int64_t n, uint64_t* __restrict__ prof) {
-  prof_begin(prof, kStSelZero);
+sel_zero_kernel(uint32_t* __restrict__ p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     p[i] = 0u;
-  prof_end(prof, kStSelZero);
 }
 
 // ---------------------------------------------------------------------------
-// Stage "pool": grid = rows * chunks.  The chunk and its halo are staged in
-// LDS with all global loads in flight at once; the sliding max reads LDS.
+// pool (standalone): grid = rows * chunks, every key of the chunk (the
+// complete score row is readable, so windows may cross chunk edges).
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(kSelT)
-sel_pool_kernel(const float* __restrict__ scores, int Lk, int ks, int window, int chunks, SelWs ws,
-                uint64_t* __restrict__ prof) {
-  prof_begin(prof, kStSelPool);
-  __shared__ uint32_t hist[kBins1];
-  __shared__ uint32_t wmax[kSelT / 64];
-  __shared__ float xs[kChunk + 2 * kMaxHalo];
-  const int tid = threadIdx.x;
+sel_pool_kernel(const float* __restrict__ scores, int Lk, int ks, int window, int chunks, SelWs ws) {
+  __shared__ uint32_t lds[kPoolLdsWords];
   const int row = blockIdx.x / chunks;
   const int c0 = (blockIdx.x % chunks) * kChunk;
-  const int h = ks / 2;
-  const float* s = scores + (int64_t)row * Lk;
-
-  float v[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = c0 + tid + i * kSelT;
-    v[i] = j < Lk ? s[j] : -INFINITY;
-  }
-  float hv = -INFINITY;
-  int hslot = -1;
-  if (tid < 2 * h) {
-    const int j = tid < h ? c0 - h + tid : c0 + kChunk + (tid - h);
-    hslot = tid < h ? kMaxHalo - h + tid : kMaxHalo + kChunk + (tid - h);
-    hv = (j >= 0 && j < Lk) ? s[j] : -INFINITY;
-  }
-  for (int i = tid; i < kBins1; i += kSelT) hist[i] = 0u;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) xs[kMaxHalo + tid + i * kSelT] = v[i];
-  if (hslot >= 0) xs[hslot] = hv;
-  __syncthreads();
-
-  uint32_t kmax = 0u;
-  const int prot = Lk - window;
-  float* pooled = ws.pooled + (int64_t)row * Lk;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int jl = tid + i * kSelT;
-    const int j = c0 + jl;
-    if (j < Lk) {
-      const float* w = xs + kMaxHalo + jl - h;
-      float m = -INFINITY;
-#pragma unroll 11
-      for (int t = 0; t <= 2 * h; ++t) m = fmaxf(m, w[t]);
-      pooled[j] = m;
-      const uint32_t key = float_key(m);
-      kmax = max(kmax, key);
-      if (j < prot) atomicAdd(&hist[key >> 21], 1u);
-    }
-  }
-  for (int o = 32; o >= 1; o >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
-  if ((tid & 63) == 0) wmax[tid >> 6] = kmax;
-  __syncthreads();
-  uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
-  if (tid == 0) {
-    uint32_t m = 0u;
-    for (int i = 0; i < kSelT / 64; ++i) m = max(m, wmax[i]);
-    atomicMax(&rw[0], m);
-  }
-  for (int i = tid; i < kBins1; i += kSelT)
-    if (hist[i]) atomicAdd(&rw[1 + i], hist[i]);
-  prof_end(prof, kStSelPool);
+  float* xs = reinterpret_cast<float*>(lds);
+  uint32_t* hist = lds + kSub + 2 * kMaxHalo;
+  uint32_t* red = hist + kBins1;
+  pool_range<kSelT>(scores + (int64_t)row * Lk, ws.pooled + (int64_t)row * Lk, ws.rowws + (int64_t)row * kRowWords,
+                    Lk, ks / 2, Lk - window, c0, min(c0 + kChunk, Lk), xs, hist, red);
 }
 
 // ---------------------------------------------------------------------------
-// Stage "cand": grid = rows * chunks.  Each chunk finds the boundary bin of
-// the top digit (all chunks compute the same one), counts its keys above it
-// and appends the keys inside it to the row's candidate list.
+// cand: grid = rows * chunks.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(kSelT)
-sel_cand_kernel(int Lk, int window, int keep, int chunks, SelWs ws, uint64_t* __restrict__ prof) {
-  prof_begin(prof, kStSelTopk);
+sel_cand_kernel(const float* __restrict__ scores, int Lk, int ks, int window, int keep, int chunks, SplitGeom geom,
+                SelWs ws) {
   __shared__ uint32_t hist[kBins1];
-  __shared__ uint32_t wsum[8];
-  __shared__ int s_bin;
-  __shared__ uint32_t s_above;
+  __shared__ uint32_t hist2[kBins2];
+  __shared__ float bxs[kBndLds];
+  __shared__ float bpool[kBndPoolLds];
+  __shared__ uint32_t small[64];
   const int tid = threadIdx.x;
   const int row = blockIdx.x / chunks;
   const int c = blockIdx.x % chunks;
+  const int h = ks / 2;
+  const int prot = Lk - window;
   uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
-  const float* pooled = ws.pooled + (int64_t)row * Lk;
+  const float* srow = scores + (int64_t)row * Lk;
+  float* prow = ws.pooled + (int64_t)row * Lk;
+  uint32_t* wsum = small;
+  int* s_bin = reinterpret_cast<int*>(small + 16);
+  uint32_t* s_above = small + 17;
+  uint32_t* s_base = small + 18;
+
+  // The chunk's pooled values (complete except the boundary keys) are loaded
+  // first, in the same round trip as everything step (1) reads.
+  float cv[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = c * kChunk + tid + i * kSelT;
+    cv[i] = j < Lk ? prow[j] : 0.f;
+  }
+  // (1) The keys within h of a split boundary b = i*kps (1 <= i < n_splits):
+  //     raw scores [b-2h, b+2h) staged, then each window read from LDS.
+  const int nb = geom.n_splits - 1;
+  const int w4 = 4 * h, w2 = 2 * h;
+  for (int t = tid; t < nb * w4; t += kSelT) {
+    const int u = (t / w4 + 1) * geom.kps - 2 * h + t % w4;
+    bxs[t] = (u >= 0 && u < Lk) ? srow[u] : -INFINITY;
+  }
+  for (int i = tid; i < kBins1; i += kSelT) {
+    hist[i] = rw[kRowHist1 + i];
+    hist2[i] = 0u;
+  }
+  __syncthreads();
+  uint32_t bmax = 0u;
+  for (int t = tid; t < nb * w2; t += kSelT) {
+    const int bi = t / w2, k = t % w2;
+    const int j = (bi + 1) * geom.kps - h + k;
+    float m = -INFINITY;
+    if (j < Lk) {
+      const float* w = bxs + bi * w4 + k;
+      for (int u = 0; u <= 2 * h; ++u) m = fmaxf(m, w[u]);
+      const uint32_t key = float_key(m);
+      bmax = max(bmax, key);
+      if (j < prot) atomicAdd(&hist[key >> 21], 1u);
+    }
+    bpool[t] = m;
+  }
+  const uint32_t gmax = block_max_u32(max(bmax, rw[kRowMax]), small + 32);
+  const uint32_t kbig = float_key(key_float(gmax) + 1.0f);
+  if (tid == 0) {
+    hist[kbig >> 21] += (uint32_t)window;
+    *s_bin = 0;
+    *s_above = 0u;
+  }
+  __syncthreads();
+  find_bin<kBins1, kSelT>(hist, (uint32_t)keep, s_bin, s_above, wsum);
+  const uint32_t b1 = (uint32_t)*s_bin;
+  const uint32_t k1 = (uint32_t)keep - *s_above;
+
+  // (2) This chunk: above-b1 count, candidates (keys in b1) and their digit-2
+  //     histogram.  Boundary keys take their value from bpool and are written
+  //     to the pooled row here (the pooling stage skipped them).
+  uint32_t keys[kPer];
+  uint32_t nab = 0u, ncand = 0u;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = c * kChunk + tid + i * kSelT;
+    keys[i] = 0u;
+    if (j < Lk) {
+      float v = cv[i];
+      const int bi = (j + h) / geom.kps;
+      const int off = j + h - bi * geom.kps;
+      if (bi >= 1 && bi <= nb && off < w2) {
+        v = bpool[(bi - 1) * w2 + off];
+        prow[j] = v;
+      }
+      keys[i] = j >= prot ? kbig : float_key(v);
+      const uint32_t d = keys[i] >> 21;
+      nab += d > b1 ? 1u : 0u;
+      ncand += d == b1 ? 1u : 0u;
+    }
+  }
+  uint32_t pc, dummy, tot_c, tot_ab;
+  block_excl_scan2<kSelT>(ncand, nab, &pc, &dummy, &tot_c, &tot_ab, wsum);
+  if (tid == 0) {
+    *s_base = tot_c ? atomicAdd(&rw[kRowNCand], tot_c) : 0u;
+    ws.above[(int64_t)row * chunks + c] = tot_ab;
+    if (c == 0) {
+      rw[kRowB1 + 0] = b1;
+      rw[kRowB1 + 1] = k1;
+      rw[kRowB1 + 2] = gmax;
+    }
+  }
+  __syncthreads();
+  uint32_t pos = *s_base + pc;
   uint32_t* ckey = ws.cand_key + (int64_t)row * Lk;
   uint32_t* cidx = ws.cand_idx + (int64_t)row * Lk;
-
-  const float big = key_float(rw[0]) + 1.0f;
-  const uint32_t kbig = float_key(big);
-  const int prot = Lk - window;
-  uint32_t keys[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = c * kChunk + tid + i * kSelT;
-    keys[i] = j < Lk ? (j >= prot ? kbig : float_key(pooled[j])) : 0u;
-  }
-  for (int i = tid; i < kBins1; i += kSelT) hist[i] = rw[1 + i] + ((int)(kbig >> 21) == i ? (uint32_t)window : 0u);
-  if (tid == 0) {
-    s_bin = 0;
-    s_above = 0u;
-  }
-  __syncthreads();
-  find_bin<kBins1>(hist, (uint32_t)keep, &s_bin, &s_above, wsum);
-  const uint32_t b1 = (uint32_t)s_bin;
-
-  // Count this thread's keys above / inside the boundary bin, then reserve
-  // the block's candidate slots with a single atomic.
-  uint32_t above = 0u, ncand = 0u;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = c * kChunk + tid + i * kSelT;
-    if (j < Lk) {
-      above += (keys[i] >> 21) > b1 ? 1u : 0u;
-      ncand += (keys[i] >> 21) == b1 ? 1u : 0u;
-    }
-  }
-  uint32_t pa, pc, tot_above, tot_cand;
-  block_excl_scan2(above, ncand, &pa, &pc, &tot_above, &tot_cand, wsum);
-  __shared__ uint32_t s_base;
-  if (tid == 0) {
-    s_base = tot_cand ? atomicAdd(&rw[kCandCount], tot_cand) : 0u;
-    ws.above[(int64_t)row * chunks + c] = tot_above;
-    if (c == 0) {
-      ws.thr[row * 2 + 0] = b1;  // boundary bin and what remains to take in it
-      ws.thr[row * 2 + 1] = (uint32_t)keep - s_above;
-    }
-  }
-  __syncthreads();
-  uint32_t pos = s_base + pc;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int j = c * kChunk + tid + i * kSelT;
@@ -291,154 +156,18 @@ sel_cand_kernel(int Lk, int window, int keep, int chunks, SelWs ws, uint64_t* __
       ckey[pos] = keys[i];
       cidx[pos] = (uint32_t)j;
       ++pos;
+      atomicAdd(&hist2[(keys[i] >> 10) & 2047u], 1u);
     }
   }
-  prof_end(prof, kStSelTopk);
+  __syncthreads();
+  for (int i = tid; i < kBins2; i += kSelT)
+    if (hist2[i]) atomicAdd(&rw[kRowHist2 + i], hist2[i]);
 }
 
 // ---------------------------------------------------------------------------
-// Stage "final": one workgroup per row.  Resolves the two lower digits on the
-// candidates, giving the threshold key T and how many keys equal to T are
-// kept, and turns per-chunk counts into output offsets.
-// ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(kSelT)
-sel_final_kernel(int chunks, SelWs ws, int64_t Lk, uint64_t* __restrict__ prof) {
-  prof_begin(prof, kStSelZero);
-  __shared__ uint32_t hist[kBins2];
-  __shared__ uint32_t cgt[kMaxChunks], ceq[kMaxChunks];
-  __shared__ uint32_t wsum[8];
-  __shared__ int s_bin;
-  __shared__ uint32_t s_above;
-  const int tid = threadIdx.x;
-  const int row = blockIdx.x;
-  const uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
-  const uint32_t nc = rw[kCandCount];
-  const uint32_t b1 = ws.thr[row * 2 + 0];
-  const uint32_t k1 = ws.thr[row * 2 + 1];
-  // The candidates (typically a few percent of the row) are read three
-  // times: stage them in LDS when they fit.
-  __shared__ uint32_t lkey[kCandLds], lidx[kCandLds];
-  const uint32_t* ckey = ws.cand_key + (int64_t)row * Lk;
-  const uint32_t* cidx = ws.cand_idx + (int64_t)row * Lk;
-  if (nc <= (uint32_t)kCandLds) {
-    for (uint32_t base = 0; base < nc; base += kSelT * kBatch) {
-      uint32_t kv[kBatch], iv[kBatch];
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        const uint32_t p = base + tid + i * kSelT;
-        kv[i] = p < nc ? ckey[p] : 0u;
-        iv[i] = p < nc ? cidx[p] : 0u;
-      }
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        const uint32_t p = base + tid + i * kSelT;
-        if (p < nc) {
-          lkey[p] = kv[i];
-          lidx[p] = iv[i];
-        }
-      }
-    }
-    ckey = lkey;
-    cidx = lidx;
-  }
-
-  // Digit 2 over the candidates.
-  for (int i = tid; i < kBins2; i += kSelT) hist[i] = 0u;
-  if (tid == 0) {
-    s_bin = 0;
-    s_above = 0u;
-  }
-  __syncthreads();
-  for (uint32_t base = 0; base < nc; base += kSelT * kBatch) {
-    uint32_t kv[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const uint32_t p = base + tid + i * kSelT;
-      kv[i] = p < nc ? ckey[p] : 0u;
-    }
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i)
-      if (base + tid + i * kSelT < nc) atomicAdd(&hist[(kv[i] >> 10) & 2047u], 1u);
-  }
-  __syncthreads();
-  find_bin<kBins2>(hist, k1, &s_bin, &s_above, wsum);
-  const uint32_t b2 = (uint32_t)s_bin;
-  const uint32_t k2 = k1 - s_above;
-  // Digit 3 over the candidates that match the first two digits.
-  for (int i = tid; i < kBins3; i += kSelT) hist[i] = 0u;
-  __syncthreads();
-  const uint32_t pre = (b1 << 11) | b2;
-  for (uint32_t base = 0; base < nc; base += kSelT * kBatch) {
-    uint32_t kv[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const uint32_t p = base + tid + i * kSelT;
-      kv[i] = p < nc ? ckey[p] : 0u;
-    }
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i)
-      if (base + tid + i * kSelT < nc && (kv[i] >> 10) == pre) atomicAdd(&hist[kv[i] & 1023u], 1u);
-  }
-  __syncthreads();
-  find_bin<kBins3>(hist, k2, &s_bin, &s_above, wsum);
-  const uint32_t T = (pre << 10) | (uint32_t)s_bin;
-  const uint32_t take_eq = k2 - s_above;
-
-  // Per-chunk counts of keys > T and == T, then exclusive offsets over chunks.
-  for (int i = tid; i < chunks; i += kSelT) {
-    cgt[i] = ws.above[(int64_t)row * chunks + i];
-    ceq[i] = 0u;
-  }
-  __syncthreads();
-  for (uint32_t base = 0; base < nc; base += kSelT * kBatch) {
-    uint32_t kv[kBatch], iv[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const uint32_t p = base + tid + i * kSelT;
-      kv[i] = p < nc ? ckey[p] : 0u;
-      iv[i] = p < nc ? cidx[p] : 0u;
-    }
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      if (base + tid + i * kSelT < nc) {
-        if (kv[i] > T) atomicAdd(&cgt[iv[i] / kChunk], 1u);
-        else if (kv[i] == T) atomicAdd(&ceq[iv[i] / kChunk], 1u);
-      }
-    }
-  }
-  __syncthreads();
-  const int cpt = (chunks + kSelT - 1) / kSelT;  // chunks per thread, contiguous
-  uint32_t sg = 0u, se = 0u;
-  for (int i = 0; i < cpt; ++i) {
-    const int cc = tid * cpt + i;
-    if (cc < chunks) {
-      sg += cgt[cc];
-      se += ceq[cc];
-    }
-  }
-  uint32_t og, oe;
-  block_excl_scan2(sg, se, &og, &oe, nullptr, nullptr, wsum);
-  for (int i = 0; i < cpt; ++i) {
-    const int cc = tid * cpt + i;
-    if (cc < chunks) {
-      ws.gt_off[(int64_t)row * chunks + cc] = og;
-      ws.eq_off[(int64_t)row * chunks + cc] = oe;
-      og += cgt[cc];
-      oe += ceq[cc];
-    }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    ws.thr[row * 2 + 0] = T;
-    ws.thr[row * 2 + 1] = take_eq;
-  }
-  prof_end(prof, kStSelZero);
-}
-
-// ---------------------------------------------------------------------------
-// Stage "emit": grid = rows * chunks.  Thread t owns the kPer consecutive keys
-// c*kChunk + kPer*t ..; kept keys are written in index order, then (when
-// ko is given) their K/V rows are copied.
+// emit: grid = rows * chunks.  Resolves T from the candidate list, then
+// thread t owns the kPer consecutive keys c*kChunk + kPer*t ..; kept keys are
+// written in index order, then (when ko is given) their K/V rows are copied.
 // ---------------------------------------------------------------------------
 struct CompactArgs {
   const uint8_t* k;
@@ -450,28 +179,106 @@ struct CompactArgs {
   uint8_t* vo;
 };
 
+constexpr int kEmitCandLds = 4096;  // candidates staged in LDS by emit (more: read from global)
+
 __global__ void __launch_bounds__(kSelT)
 sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __restrict__ out_idx,
-                float* __restrict__ pooled_out, CompactArgs ca, uint64_t* __restrict__ prof) {
-  prof_begin(prof, kStCompact);
-  __shared__ uint32_t wsum[8];
+                float* __restrict__ pooled_out, CompactArgs ca) {
+  __shared__ uint32_t hist[kBins2];  // digit-2, then digit-3 histogram
+  __shared__ uint32_t small[64];
+  __shared__ uint32_t lkey[kEmitCandLds], lidx[kEmitCandLds];
   __shared__ int s_src[kChunk];
   __shared__ int s_dst[kChunk];
   const int tid = threadIdx.x;
   const int row = blockIdx.x / chunks;
   const int c = blockIdx.x % chunks;
+  uint32_t* wsum = small;
+  int* s_bin = reinterpret_cast<int*>(small + 16);
+  uint32_t* s_above = small + 17;
   const uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
   const float* pooled = ws.pooled + (int64_t)row * Lk;
-  const float big = key_float(rw[0]) + 1.0f;
-  const uint32_t kbig = float_key(big);
   const int prot = Lk - window;
-  const uint32_t T = ws.thr[row * 2 + 0], take_eq = ws.thr[row * 2 + 1];
-  const uint32_t gt0 = ws.gt_off[(int64_t)row * chunks + c], eq0 = ws.eq_off[(int64_t)row * chunks + c];
 
+  // Round trip 1: the row words, this chunk's pooled values and the
+  // above-b1 counts of the earlier chunks.
   const int j0 = c * kChunk + kPer * tid;
   float pv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) pv[i] = (j0 + i < Lk) ? pooled[j0 + i] : 0.f;
+  uint32_t hv[kBins2 / kSelT];
+#pragma unroll
+  for (int i = 0; i < kBins2 / kSelT; ++i) hv[i] = rw[kRowHist2 + tid + i * kSelT];
+  const uint32_t b1 = rw[kRowB1 + 0], k1 = rw[kRowB1 + 1];
+  const float big = key_float(rw[kRowB1 + 2]) + 1.0f;
+  const uint32_t kbig = float_key(big);
+  const uint32_t nc = rw[kRowNCand];
+  uint32_t g = 0u, e = 0u;
+  for (int cc = tid; cc < c; cc += kSelT) g += ws.above[(int64_t)row * chunks + cc];
+
+  // Round trip 2: the candidate list (staged in LDS when it fits).
+  const uint32_t* gkey = ws.cand_key + (int64_t)row * Lk;
+  const uint32_t* gidx = ws.cand_idx + (int64_t)row * Lk;
+  const bool in_lds = nc <= (uint32_t)kEmitCandLds;
+  if (in_lds) {
+    for (uint32_t base = 0; base < nc; base += kSelT * kUnroll) {
+      uint32_t kv[kUnroll], iv[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t p = base + tid + u * kSelT;
+        kv[u] = p < nc ? gkey[p] : 0u;
+        iv[u] = p < nc ? gidx[p] : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t p = base + tid + u * kSelT;
+        if (p < nc) {
+          lkey[p] = kv[u];
+          lidx[p] = iv[u];
+        }
+      }
+    }
+  }
+  const uint32_t* ckey = in_lds ? lkey : gkey;
+  const uint32_t* cidx = in_lds ? lidx : gidx;
+
+  // Digit 2.
+#pragma unroll
+  for (int i = 0; i < kBins2 / kSelT; ++i) hist[tid + i * kSelT] = hv[i];
+  if (tid == 0) {
+    *s_bin = 0;
+    *s_above = 0u;
+  }
+  __syncthreads();
+  find_bin<kBins2, kSelT>(hist, k1, s_bin, s_above, wsum);
+  const uint32_t b2 = (uint32_t)*s_bin;
+  const uint32_t k2 = k1 - *s_above;
+  const uint32_t pre = (b1 << 11) | b2;
+  __syncthreads();
+  for (int i = tid; i < kBins3; i += kSelT) hist[i] = 0u;
+  __syncthreads();
+  // Digit 3 over the candidates matching the first two digits.
+  for (uint32_t p = tid; p < nc; p += kSelT) {
+    const uint32_t kv = ckey[p];
+    if ((kv >> 10) == pre) atomicAdd(&hist[kv & 1023u], 1u);
+  }
+  __syncthreads();
+  find_bin<kBins3, kSelT>(hist, k2, s_bin, s_above, wsum);
+  const uint32_t T = (pre << 10) | (uint32_t)*s_bin;
+  const uint32_t take_eq = k2 - *s_above;
+
+  // Output offsets of this chunk: kept keys > T and keys == T in earlier
+  // chunks (above-b1 keys per chunk, plus the candidates before it).
+  const uint32_t lim = (uint32_t)c * kChunk;
+  for (uint32_t p = tid; p < nc; p += kSelT) {
+    if (cidx[p] < lim) {
+      const uint32_t kv = ckey[p];
+      g += kv > T ? 1u : 0u;
+      e += kv == T ? 1u : 0u;
+    }
+  }
+  uint32_t gt0, eq0;
+  block_sum2<kSelT>(g, e, &gt0, &eq0, wsum);
+
   uint32_t keys[kPer];
   uint32_t ng = 0u, ne = 0u;
 #pragma unroll
@@ -485,7 +292,7 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __r
     }
   }
   uint32_t pg, pe, tg, te;
-  block_excl_scan2(ng, ne, &pg, &pe, &tg, &te, wsum);
+  block_excl_scan2<kSelT>(ng, ne, &pg, &pe, &tg, &te, wsum);
   const uint32_t start = gt0 + min(eq0, take_eq);  // first output slot of this chunk
   uint32_t g_before = gt0 + pg, e_before = eq0 + pe;
 #pragma unroll
@@ -514,10 +321,11 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __r
     const int total = nk * ca.units;
     const uint8_t* kb = ca.k + b * ca.sb + h * ca.sh;
     const uint8_t* vb = ca.v + b * ca.sb + h * ca.sh;
-    for (int t0 = tid; t0 < total; t0 += 4 * kSelT) {
-      u32x4 kv[4], vv[4];
+    constexpr int kG = 8;  // 16-byte units of K and of V in flight per thread
+    for (int t0 = tid; t0 < total; t0 += kG * kSelT) {
+      u32x4 kv[kG], vv[kG];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < kG; ++q) {
         const int t = t0 + q * kSelT;
         if (t < total) {
           const int64_t off = (int64_t)s_src[t / ca.units] * ca.sl + 16 * (t % ca.units);
@@ -526,7 +334,7 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __r
         }
       }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < kG; ++q) {
         const int t = t0 + q * kSelT;
         if (t < total) {
           const int64_t o = ((int64_t)row * keep + s_dst[t / ca.units]) * ca.units * 16 + 16 * (t % ca.units);
@@ -536,7 +344,6 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __r
       }
     }
   }
-  prof_end(prof, kStCompact);
 }
 
 // ---------------------------------------------------------------------------
@@ -552,25 +359,7 @@ int64_t select_zero_words(int64_t rows) { return rows * kRowWords; }
 
 int64_t select_max_len() { return (int64_t)kMaxChunks * kChunk; }
 
-hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int window, int keep, int64_t* out_idx,
-                         float* pooled_out, char* ws_base, bool pre_zeroed, const SelectCompact* cp,
-                         hipStream_t st) {
-  const SelWs ws = sel_layout(ws_base, rows, Lk, nullptr);
-  const int chunks = (Lk + kChunk - 1) / kChunk;
-  uint64_t* prof = prof_slot();
-  if (!pre_zeroed) {
-    const int64_t zn = (int64_t)rows * kRowWords;
-    hipLaunchKernelGGL(sel_zero_kernel, dim3((unsigned)std::min<int64_t>((zn + kSelT - 1) / kSelT, 1024)),
-                       dim3(kSelT), 0, st, ws.rowws, zn, prof);
-    timing_mark(st);
-  }
-  const dim3 grid((unsigned)(rows * chunks));
-  hipLaunchKernelGGL(sel_pool_kernel, grid, dim3(kSelT), 0, st, scores, Lk, ks, window, chunks, ws, prof);
-  timing_mark(st);
-  hipLaunchKernelGGL(sel_cand_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, ws, prof);
-  timing_mark(st);
-  hipLaunchKernelGGL(sel_final_kernel, dim3((unsigned)rows), dim3(kSelT), 0, st, chunks, ws, (int64_t)Lk, prof);
-  timing_mark(st);
+static CompactArgs compact_args(const SelectCompact* cp) {
   CompactArgs ca{};
   if (cp) {
     ca.k = static_cast<const uint8_t*>(cp->k);
@@ -583,10 +372,44 @@ hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int wind
     ca.ko = static_cast<uint8_t*>(cp->k_out);
     ca.vo = static_cast<uint8_t*>(cp->v_out);
   }
+  return ca;
+}
+
+hipError_t launch_select_after_pool(const float* scores, int rows, int Lk, int ks, int window, int keep,
+                                    int n_splits, int kps, int64_t* out_idx, float* pooled_out, char* ws_base,
+                                    const SelectCompact* cp, hipStream_t st) {
+  const SelWs ws = sel_layout(ws_base, rows, Lk, nullptr);
+  const int chunks = (Lk + kChunk - 1) / kChunk;
+  const dim3 grid((unsigned)(rows * chunks));
+  hipLaunchKernelGGL(sel_cand_kernel, grid, dim3(kSelT), 0, st, scores, Lk, ks, window, keep, chunks,
+                     SplitGeom{n_splits, kps}, ws);
+  timing_mark(st);
   hipLaunchKernelGGL(sel_emit_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, ws, out_idx, pooled_out,
-                     ca, prof);
+                     compact_args(cp));
   timing_mark(st);
   return hipGetLastError();
+}
+
+hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int window, int keep, int64_t* out_idx,
+                         float* pooled_out, char* ws_base, bool pre_zeroed, const SelectCompact* cp,
+                         hipStream_t st) {
+  const SelWs ws = sel_layout(ws_base, rows, Lk, nullptr);
+  const int chunks = (Lk + kChunk - 1) / kChunk;
+  if (!pre_zeroed) {
+    const int64_t zn = (int64_t)rows * kRowWords;
+    hipLaunchKernelGGL(sel_zero_kernel, dim3((unsigned)std::min<int64_t>((zn + kSelT - 1) / kSelT, 1024)),
+                       dim3(kSelT), 0, st, ws.rowws, zn);
+    timing_mark(st);
+  }
+  hipLaunchKernelGGL(sel_pool_kernel, dim3((unsigned)(rows * chunks)), dim3(kSelT), 0, st, scores, Lk, ks, window,
+                     chunks, ws);
+  timing_mark(st);
+  return launch_select_after_pool(scores, rows, Lk, ks, window, keep, 1, Lk, out_idx, pooled_out, ws_base, cp, st);
+}
+
+bool select_after_pool_ok(int64_t n_splits, int64_t kps, int64_t Lk, int64_t ks) {
+  const int64_t h = ks / 2;
+  return h <= kMaxHalo && kps >= 2 * h && (Lk + kChunk - 1) / kChunk <= kMaxChunks && boundary_fits(n_splits, h);
 }
 
 }  // namespace dkv

@@ -1,0 +1,266 @@
+// Device-side pieces of the selection (pool / protect / top-k threshold /
+// ordered emit) shared by the selection kernels (dkv_select.hip) and the
+// pooling epilogue of the scoring pass (dkv_score.hip).
+//
+// Reference semantics (dropkv_cache.py:464-475):
+//   pooled[j] = max(scores[j-h .. j+h]), h = kernel_size/2, out of range = -inf
+//   big = max_j pooled[j] + 1.0f ; pooled[Lk-window ..] = big
+//   keep the `keep` largest pooled values; among values equal to the
+//   threshold the lowest indices win (torch.topk leaves that order open).
+//
+// Floats are mapped to order-preserving uint32 keys and the keep-th largest
+// key T is found by a radix select over 11 + 11 + 10 bits, spread so that
+// every stage runs on all CUs:
+//   pool   (pass-2 epilogue, or the standalone pool kernel) pooled values of
+//          the keys whose window lies inside one workgroup's range, the row
+//          maximum and the top-digit histogram (device atomics);
+//   cand   (row, 1024-key chunk) workgroups: each first pools the few keys
+//          next to the scoring pass's split boundaries (redundantly), which
+//          completes the histogram and fixes the boundary bin b1; then its
+//          chunk's keys above b1 are counted and those inside b1 appended to
+//          the row's candidate list, with their digit-2 histogram;
+//   emit   (row, chunk) workgroups: each resolves digits 2 and 3 from the
+//          candidate list (a few percent of the row), derives its chunk's
+//          output offsets, writes its kept indices in index order and copies
+//          the K/V rows they name.
+#pragma once
+
+#include "dkv_common.h"
+
+namespace dkv {
+
+constexpr int kChunk = 1024;      // keys per cand/emit workgroup (offset granularity)
+constexpr int kBins1 = 2048;      // key bits 31..21
+constexpr int kBins2 = 2048;      // key bits 20..10
+constexpr int kBins3 = 1024;      // key bits 9..0
+constexpr int kMaxHalo = 64;      // kernel_size <= 2*kMaxHalo+1
+constexpr int kMaxChunks = 4096;  // Lk <= kMaxChunks * kChunk
+constexpr int kBndLds = 4096;     // LDS words for the boundary keys' raw-score neighbourhoods
+constexpr int kBndPoolLds = 2048; // LDS words for the boundary keys' pooled values
+
+// Per-row words that must be zero on entry (the merge kernel or the zero
+// kernel clears them every call), then results of the cand stage:
+constexpr int kRowMax = 0;                     // max pooled key of the interiors
+constexpr int kRowHist1 = 1;                   // top-digit histogram (unprotected interior keys)
+constexpr int kRowHist2 = kRowHist1 + kBins1;  // digit-2 histogram of the candidates
+constexpr int kRowNCand = kRowHist2 + kBins2;  // candidate count
+constexpr int kRowB1 = kRowNCand + 1;          // b1, keep left in b1, max key of the row (cand stage)
+constexpr int kRowWords = kRowB1 + 3;
+
+struct SelWs {
+  uint32_t* rowws;     // [rows][kRowWords]
+  float* pooled;       // [rows][Lk]
+  uint32_t* above;     // [rows][chunks] keys of a chunk above the boundary bin
+  uint32_t* cand_key;  // [rows][Lk]
+  uint32_t* cand_idx;  // [rows][Lk]
+};
+
+inline size_t sel_al256(size_t b) { return (b + 255) & ~size_t(255); }
+
+inline SelWs sel_layout(char* base, int64_t rows, int64_t Lk, size_t* total) {
+  const int64_t chunks = (Lk + kChunk - 1) / kChunk;
+  SelWs w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += sel_al256(bytes);
+    return p;
+  };
+  w.rowws = reinterpret_cast<uint32_t*>(take((size_t)rows * kRowWords * 4));
+  w.pooled = reinterpret_cast<float*>(take((size_t)rows * Lk * 4));
+  w.above = reinterpret_cast<uint32_t*>(take((size_t)rows * chunks * 4));
+  w.cand_key = reinterpret_cast<uint32_t*>(take((size_t)rows * Lk * 4));
+  w.cand_idx = reinterpret_cast<uint32_t*>(take((size_t)rows * Lk * 4));
+  if (total) *total = off;
+  return w;
+}
+
+// Split geometry of the pooling stage: keys within h of j = i*kps
+// (1 <= i < n_splits) were not pooled by it (their window straddles two
+// workgroup ranges).  n_splits = 1 means every key was pooled.
+struct SplitGeom {
+  int n_splits, kps;
+};
+
+// Whether the cand stage can hold the boundary keys of this geometry in LDS.
+__host__ __device__ constexpr bool boundary_fits(int64_t n_splits, int64_t h) {
+  return (n_splits - 1) * 4 * h <= kBndLds && (n_splits - 1) * 2 * h <= kBndPoolLds;
+}
+
+// ---------------------------------------------------------------------------
+// Block-level helpers for NT threads (a multiple of 64).
+// ---------------------------------------------------------------------------
+// Exclusive prefix sums of two counters over the threads of the block, and
+// optionally their block totals.  wsum: 2*NT/64 words of LDS.
+template <int NT>
+__device__ __forceinline__ void block_excl_scan2(uint32_t a, uint32_t b, uint32_t* pa, uint32_t* pb, uint32_t* ta,
+                                                 uint32_t* tb, uint32_t* wsum) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint32_t xa = a, xb = b;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t ya = __shfl_up((int)xa, o), yb = __shfl_up((int)xb, o);
+    if (lane >= o) {
+      xa += ya;
+      xb += yb;
+    }
+  }
+  __syncthreads();
+  if (lane == 63) {
+    wsum[w] = xa;
+    wsum[NW + w] = xb;
+  }
+  __syncthreads();
+  uint32_t oa = 0, ob = 0, sa = 0, sb = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    if (i < w) {
+      oa += wsum[i];
+      ob += wsum[NW + i];
+    }
+    sa += wsum[i];
+    sb += wsum[NW + i];
+  }
+  *pa = oa + xa - a;
+  *pb = ob + xb - b;
+  if (ta) *ta = sa;
+  if (tb) *tb = sb;
+}
+
+// Block sums of two counters (every thread gets them).  wsum: 2*NT/64 words.
+template <int NT>
+__device__ __forceinline__ void block_sum2(uint32_t a, uint32_t b, uint32_t* ta, uint32_t* tb, uint32_t* wsum) {
+  constexpr int NW = NT / 64;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    a += (uint32_t)__shfl_xor((int)a, o);
+    b += (uint32_t)__shfl_xor((int)b, o);
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    wsum[threadIdx.x >> 6] = a;
+    wsum[NW + (threadIdx.x >> 6)] = b;
+  }
+  __syncthreads();
+  uint32_t sa = 0, sb = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    sa += wsum[i];
+    sb += wsum[NW + i];
+  }
+  *ta = sa;
+  *tb = sb;
+}
+
+// For a histogram of NB bins in LDS and 1 <= k <= total: the bin b with
+// (count of keys in bins > b) < k <= (count in bins >= b), and the count in
+// bins > b.  Results land in *s_bin / *s_above (LDS); ends with a barrier.
+template <int NB, int NT>
+__device__ void find_bin(const uint32_t* hist, uint32_t k, int* s_bin, uint32_t* s_above, uint32_t* wsum) {
+  static_assert(NB % NT == 0, "bins must be a multiple of the block size");
+  constexpr int per = NB / NT;
+  const int tid = threadIdx.x;
+  uint32_t loc[per];
+  uint32_t tsum = 0u;
+#pragma unroll
+  for (int i = 0; i < per; ++i) {
+    loc[i] = hist[NB - 1 - (tid * per + i)];  // thread order = descending bins
+    tsum += loc[i];
+  }
+  uint32_t run, dummy;
+  block_excl_scan2<NT>(tsum, 0u, &run, &dummy, nullptr, nullptr, wsum);
+#pragma unroll
+  for (int i = 0; i < per; ++i) {
+    const uint32_t nxt = run + loc[i];
+    if (run < k && nxt >= k) {
+      *s_bin = NB - 1 - (tid * per + i);
+      *s_above = run;
+    }
+    run = nxt;
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t x, uint32_t* red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = max(x, (uint32_t)__shfl_xor((int)x, o));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  uint32_t m = 0u;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) m = max(m, red[i]);
+  return m;
+}
+
+// Lanes below this one in the wave whose bit is set in `mask`.
+__device__ __forceinline__ uint32_t lane_prefix(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// ---------------------------------------------------------------------------
+// Pooling of the keys j in [i0, i1) of one row whose whole window lies in
+// the scores this workgroup may read (the caller guarantees it), adding them
+// to the row's maximum and top-digit histogram.  xs: kSub + 2*kMaxHalo
+// floats, hist: kBins1 words, red: 16 words of LDS.
+// ---------------------------------------------------------------------------
+constexpr int kSub = 2048;  // keys pooled per round
+constexpr int kPoolLdsWords = kSub + 2 * kMaxHalo + kBins1 + 16;
+
+template <int NT>
+__device__ void pool_range(const float* __restrict__ srow, float* __restrict__ prow, uint32_t* rw, int Lk, int h,
+                           int prot, int i0, int i1, float* xs, uint32_t* hist, uint32_t* red) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kBins1; i += NT) hist[i] = 0u;
+  uint32_t kmax = 0u;
+  for (int s0 = i0; s0 < i1; s0 += kSub) {
+    const int s1 = min(s0 + kSub, i1);
+    const int lo = s0 - h, n = s1 + h - lo;
+    __syncthreads();
+    for (int t = tid; t < n; t += NT) {
+      const int j = lo + t;
+      xs[t] = (j >= 0 && j < Lk) ? srow[j] : -INFINITY;
+    }
+    __syncthreads();
+    for (int j = s0 + tid; j < s1; j += NT) {
+      const float* w = xs + (j - s0);
+      float m = -INFINITY;
+      for (int t = 0; t <= 2 * h; ++t) m = fmaxf(m, w[t]);
+      prow[j] = m;
+      const uint32_t key = float_key(m);
+      kmax = max(kmax, key);
+      if (j < prot) atomicAdd(&hist[key >> 21], 1u);
+    }
+  }
+  kmax = block_max_u32(kmax, red);
+  if (tid == 0 && i0 < i1) atomicMax(&rw[kRowMax], kmax);
+  for (int i = tid; i < kBins1; i += NT)
+    if (hist[i]) atomicAdd(&rw[kRowHist1 + i], hist[i]);
+}
+
+// The same, when the workgroup's own scores [k_begin, k_end) are in LDS (sc)
+// and every window of [i0, i1) lies inside them once clipped to [0, Lk).
+// hist: kBins1 words, red: 16 words of LDS; the caller has made sc visible.
+template <int NT>
+__device__ void pool_range_lds(const float* sc, int k_begin, float* __restrict__ prow, uint32_t* rw, int Lk, int h,
+                               int prot, int i0, int i1, uint32_t* hist, uint32_t* red) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kBins1; i += NT) hist[i] = 0u;
+  __syncthreads();
+  uint32_t kmax = 0u;
+  for (int j = i0 + tid; j < i1; j += NT) {
+    const int u0 = max(j - h, 0) - k_begin, u1 = min(j + h, Lk - 1) - k_begin;
+    float m = -INFINITY;
+    for (int u = u0; u <= u1; ++u) m = fmaxf(m, sc[u]);
+    prow[j] = m;
+    const uint32_t key = float_key(m);
+    kmax = max(kmax, key);
+    if (j < prot) atomicAdd(&hist[key >> 21], 1u);
+  }
+  kmax = block_max_u32(kmax, red);
+  if (tid == 0 && i0 < i1) atomicMax(&rw[kRowMax], kmax);
+  for (int i = tid; i < kBins1; i += NT)
+    if (hist[i]) atomicAdd(&rw[kRowHist1 + i], hist[i]);
+}
+
+}  // namespace dkv

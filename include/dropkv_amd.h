@@ -123,8 +123,13 @@ int dropkv_compact2(const void* k0, const void* v0, int64_t s0_b, int64_t s0_h, 
  * One layer-call of prefill eviction: scores -> select -> compact, all
  * enqueued on `stream` by one call.  Equivalent to
  * DropKVCache._compute_keep_indices followed by _gather_compressed
- * (dropkv_cache.py:355-491) on the fast path.  `scores`, `pooled` may be NULL
- * (then they live in the workspace / are not written).
+ * (dropkv_cache.py:355-491) on the fast path.  `protect_window` is the
+ * cache's window_size (the last protect_window keys are always kept, as
+ * dropkv_cache.py:466-467), `W` the scoring window (min(window, Lq) on the
+ * deployed path).  `scores` may be NULL (then it lives in the workspace).
+ * Pooling and the top-k threshold run in the tail of the scoring kernel
+ * whenever the plan allows it (three kernels per call), otherwise as the
+ * standalone selection kernels.
  * ------------------------------------------------------------------------ */
 size_t dropkv_evict_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk,
                                     int64_t D, int64_t W, int64_t splits);
@@ -136,25 +141,6 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
                  int64_t kernel_size, int64_t protect_window, int64_t keep,
                  float* scores, int64_t* keep_idx, void* k_out, void* v_out,
                  void* workspace, size_t workspace_bytes, void* stream);
-
-/* Kernel-time profiler for dropkv_evict (no counterpart in the reference,
- * which has no timers).  dropkv_profile_begin(n) allocates n device slots and
- * arms recording for the next n dropkv_evict calls in this process: each of
- * those calls first clears its slot, then every kernel it launches records its
- * first-workgroup start and last-workgroup end from the GPU wall clock.  A
- * call captured into a HIP graph re-records its slot on every replay.
- * Stage order: pass-1 partials, merge, pass-2 scores, select-final (the
- * per-row threshold; in a standalone dropkv_select it also covers the
- * workspace clear), select-pool, select-candidates, emit+compact; element 7
- * is the span from the first kernel start to the last kernel end.
- *   dropkv_profile_read(slot, ms[8])   waits for the device, reads one slot
- *   dropkv_profile_disarm()            stop recording new slots
- *   dropkv_profile_end(ms[8], calls)   sum over recorded slots, then free
- * Not thread-safe against concurrent dropkv_evict calls. */
-int dropkv_profile_begin(int64_t max_calls);
-int dropkv_profile_read(int64_t slot, double* stage_ms);
-int dropkv_profile_disarm(void);
-int dropkv_profile_end(double* stage_ms, int64_t* calls);
 
 /* Kernel timing with HIP events (no counterpart in the reference, which has
  * no timers).  dropkv_timing_enable(1) makes every later dropkv_scores /

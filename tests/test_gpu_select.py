@@ -122,3 +122,39 @@ def test_evict_fused_matches_ops(gpu, shape):
     # and against the oracle's selection on the same scores
     pooled = R.pool_protect(s.cpu().clone(), 11, 8)
     assert torch.equal(idx.cpu(), R.topk_sorted(pooled, keep))
+
+
+@pytest.mark.parametrize("Lk,ks,window,keep,splits,vzero", [
+    (1000, 11, 8, 100, 0, False),
+    (777, 1, 8, 77, 0, False),        # kernel_size 1: no halo at all
+    (5000, 31, 64, 4999, 0, False),   # keep ~ Lk
+    (4096, 11, 8, 1, 0, False),       # keep 1: only the protected maximum competes
+    (3000, 11, 8, 300, 7, False),     # uneven split ranges
+    (6400, 11, 8, 640, 200, False),   # 32-key split ranges: many boundaries
+    (6400, 81, 8, 640, 200, False),   # ranges shorter than the kernel: standalone selection
+    (2048, 11, 600, 700, 8, False),   # protected window wider than a split range
+    (3000, 11, 8, 300, 0, True),      # V = 0: every score is 0, all ties
+])
+def test_evict_fused_selection_edges(gpu, Lk, ks, window, keep, splits, vzero):
+    """dropkv_evict (selection fused into the scoring tail where the plan
+    allows) against the oracle's pool / protect / rank rule on the same GPU
+    scores, and a bit-exact gather."""
+    from dropkv_amd import ops
+    g = torch.Generator().manual_seed(Lk + ks + keep)
+    B, Hq, Hkv, D = 1, 8, 2, 128
+    Q = torch.randn(B, Hq, 64, D, generator=g).to(torch.bfloat16).to(gpu)
+    K = torch.randn(B, Hkv, Lk, D, generator=g).to(torch.bfloat16).to(gpu)
+    V = torch.randn(B, Hkv, Lk, D, generator=g).to(torch.bfloat16).to(gpu)
+    if vzero:
+        V.zero_()
+    plan = ops.EvictPlan(Q, K, 8, ks, keep, protect_window=window, splits=splits, keep_scores=True)
+    idx, ko, vo = plan(Q, K, V)
+    s = ops.scores(Q, K, V, 8, splits=splits)
+    assert torch.equal(plan.scores, s)
+    pooled = R.pool_protect(s.cpu().clone(), ks, window)
+    assert torch.equal(idx.cpu(), R.topk_sorted(pooled, keep))
+    rk, rv = R.gather_compressed(K.cpu(), V.cpu(), idx.cpu())
+    assert torch.equal(ko.cpu(), rk) and torch.equal(vo.cpu(), rv)
+    # a second call on the same plan (workspace reused) gives the same result
+    idx2, _, _ = plan(Q, K, V)
+    assert torch.equal(idx2, idx)
