@@ -29,6 +29,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
     # Packed fp32 VALU ops stay off (the hardware forms are not trusted here).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs: the score kernels consume every
+    # accumulator with VALU ops, so accumulation registers only add copies.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

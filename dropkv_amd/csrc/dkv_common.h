@@ -37,6 +37,19 @@ __device__ __forceinline__ float round_through(float x) {
   return static_cast<float>(static_cast<T>(x));
 }
 
+// Raw buffer view of `bytes` bytes at `base`.  Loads at byte offsets >= bytes
+// return zeros and issue no memory request, so a tile loop can load past the
+// end of its range without a branch.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  // Word 3: 32-bit data format, no swizzle / stride / thread-id addressing.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+
 template <typename V>
 __device__ __forceinline__ V bitcast_u4(u32x4 x) {
   return __builtin_bit_cast(V, x);

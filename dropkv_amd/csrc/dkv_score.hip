@@ -25,6 +25,7 @@
 #include "dkv_select_dev.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -76,37 +77,40 @@ __device__ __forceinline__ void load_q_ops(typename Elem<T>::v8 (&qop)[D / 32], 
 }
 
 // ---------------------------------------------------------------------------
-// Tile loads shared by the two passes.
+// Tile loads shared by the two passes.  A workgroup reads the rows
+// [k_begin, k_end) of one head through buffer views (make_rsrc) that end at
+// k_end, so rows past the range (a wave's tiles after its last one, the tail
+// past Lk) read as zeros without memory traffic; the callers mask those keys.
+// Offsets are bytes relative to row k_begin; per-lane parts are computed once
+// and the tile offset is one add.
 // ---------------------------------------------------------------------------
-// 32 key rows as an MFMA A operand: lane (li, lg) holds row t0+16kb+li,
-// head-dim columns 32kk+8lg .. +7.  Rows past Lk are clamped (and masked by
-// the caller).
+// 32 key rows as an MFMA A operand: lane (li, lg) holds row t+16kb+li,
+// head-dim columns 32kk+8lg .. +7.  `lane_off` = (li*D + 8*lg) * sizeof(T).
 template <typename T, int D>
-__device__ __forceinline__ void load_rows_op(typename Elem<T>::v8 (&op)[2][D / 32], const T* __restrict__ base,
-                                             int t0, int Lk, int li, int lg) {
+__device__ __forceinline__ void load_rows_op(typename Elem<T>::v8 (&op)[2][D / 32], rsrc_t rs, uint32_t lane_off,
+                                             int t) {
   typedef typename Elem<T>::v8 v8;
+  const uint32_t base = lane_off + (uint32_t)t * (D * sizeof(T));
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    const int n = min(t0 + 16 * kb + li, Lk - 1);
+  for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk) op[kb][kk] = *reinterpret_cast<const v8*>(base + (int64_t)n * D + 32 * kk + 8 * lg);
-  }
+    for (int kk = 0; kk < D / 32; ++kk)
+      op[kb][kk] = bitcast_u4<v8>(buf_load16(rs, base + (16 * kb * D + 32 * kk) * sizeof(T)));
 }
 
 // 32 value rows in coalesced 16-byte chunks, two adjacent keys per lane
-// (pairs p, chunk c) for the transposed LDS tile.
+// (pairs p, chunk c) for the transposed LDS tile.  `lane_off` =
+// (2*(lane/CPR)*D + 8*(lane%CPR)) * sizeof(T).
 template <typename T, int D>
 __device__ __forceinline__ void load_v_pairs(u32x4 (&va)[(kTile / 2) / (64 / (D / 8))],
-                                             u32x4 (&vb)[(kTile / 2) / (64 / (D / 8))], const T* __restrict__ Vh,
-                                             int t0, int Lk, int lane) {
+                                             u32x4 (&vb)[(kTile / 2) / (64 / (D / 8))], rsrc_t rs,
+                                             uint32_t lane_off, int t) {
   constexpr int CPR = D / 8, GRP = 64 / CPR, NIT = (kTile / 2) / GRP;
+  const uint32_t base = lane_off + (uint32_t)t * (D * sizeof(T));
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
-    const int p = it * GRP + lane / CPR;
-    const int c = lane % CPR;
-    const int n0 = min(t0 + 2 * p, Lk - 1), n1 = min(t0 + 2 * p + 1, Lk - 1);
-    va[it] = *reinterpret_cast<const u32x4*>(Vh + (int64_t)n0 * D + 8 * c);
-    vb[it] = *reinterpret_cast<const u32x4*>(Vh + (int64_t)n1 * D + 8 * c);
+    va[it] = buf_load16(rs, base + (2 * it * GRP) * D * sizeof(T));
+    vb[it] = buf_load16(rs, base + (2 * it * GRP + 1) * D * sizeof(T));
   }
 }
 
@@ -159,9 +163,13 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   const bool pad_chunk = mc * kRows + kRows > M;
   const int unmasked_end = Lk - W + 1;
 
-  const int64_t hoff = (int64_t)head * Lk * D;
-  const T* __restrict__ Kh = kp + hoff;
-  const T* __restrict__ Vh = vp + hoff;
+  const int k_begin = split * kps;
+  const int k_end = min(k_begin + kps, Lk);
+  const int64_t roff = ((int64_t)head * Lk + k_begin) * D;
+  const uint32_t range = (uint32_t)(k_end - k_begin) * (D * sizeof(T));
+  const rsrc_t krs = make_rsrc(kp + roff, range), vrs = make_rsrc(vp + roff, range);
+  const uint32_t k_lane = (li * D + 8 * lg) * sizeof(T);
+  const uint32_t v_lane = (2 * (lane / CPR) * D + 8 * (lane % CPR)) * sizeof(T);
   uint32_t* vt = lds + wv * D * kPitch;
 
   float m2[kMB], lsum[kMB];
@@ -174,17 +182,15 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const int k_begin = split * kps;
-  const int k_end = min(k_begin + kps, Lk);
-
   v8 kop[2][KK];
   u32x4 va[NIT], vb[NIT];
-  int t0 = k_begin + wv * kTile;
-  if (t0 < k_end) {
-    load_rows_op<T, D>(kop, Kh, t0, Lk, li, lg);
-    load_v_pairs<T, D>(va, vb, Vh, t0, Lk, lane);
-  }
-  for (; t0 < k_end; t0 += WAVES * kTile) {
+  const int stride = WAVES * kTile;
+
+  // One tile (t0 absolute, tn relative to k_begin): consume the K/V
+  // registers, refill them with tile tn (zeros past the range), then the
+  // softmax and P.V work, which overlaps both tiles' loads.
+  auto tile = [&](v8 (&kop)[2][KK], u32x4 (&va)[NIT], u32x4 (&vb)[NIT], int t0, int tn)
+      __attribute__((always_inline)) {
     // S^T = K Q^T.
     f32x4 s[2][kMB];
 #pragma unroll
@@ -206,20 +212,19 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t a = va[it][j], bb = vb[it][j];
-        const uint32_t lo = (a & 0xffffu) | (bb << 16);
-        const uint32_t hi = (a >> 16) | (bb & 0xffff0000u);
+        const uint32_t lo = __builtin_amdgcn_perm(bb, a, 0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(bb, a, 0x07060302u);
         const int d0 = 8 * c + 2 * j, d1 = d0 + 1;
         vt[d0 * kPitch + (p ^ (4 * ((d0 >> 4) & 3)))] = lo;
         vt[d1 * kPitch + (p ^ (4 * ((d1 >> 4) & 3)))] = hi;
       }
     }
 
-    // The K/V registers are free again: start the next tile's loads now.
-    const int tn = t0 + WAVES * kTile;
-    if (tn < k_end) {
-      load_rows_op<T, D>(kop, Kh, tn, Lk, li, lg);
-      load_v_pairs<T, D>(va, vb, Vh, tn, Lk, lane);
-    }
+    // The K/V registers are free again: start the loads of tile tn.  They
+    // are unconditional (zeros past the range) so that the compiler's wait
+    // counts stay exact.
+    load_rows_op<T, D>(kop, krs, k_lane, tn);
+    load_v_pairs<T, D>(va, vb, vrs, v_lane, tn);
 
     // Online softmax (base 2) for each row block; P hi/lo split for the MFMA.
     const bool masked = pad_chunk || t0 + kTile > unmasked_end;
@@ -275,6 +280,14 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
         yacc[dt][mb] = Elem<T>::mfma(aop, plo[mb], yacc[dt][mb]);
       }
     }
+  };
+
+  const int nrel = k_end - k_begin;
+  int t = wv * kTile;  // relative to k_begin
+  if (t < nrel) {
+    load_rows_op<T, D>(kop, krs, k_lane, t);
+    load_v_pairs<T, D>(va, vb, vrs, v_lane, t);
+    for (; t < nrel; t += stride) tile(kop, va, vb, k_begin + t, t + stride);
   }
 
   // Row sums are per lane-group partials; fold the four groups.
@@ -358,9 +371,13 @@ __device__ __forceinline__ float block_reduce(float x, float* red, bool is_max) 
 template <typename T, int D>
 __global__ void __launch_bounds__(kMergeThreads)
 merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y, int n_mc, int n_splits,
-             int M, int y_round, T* __restrict__ yhl, float* __restrict__ ystat, float* __restrict__ yf32,
-             uint32_t* __restrict__ zero_ptr, int64_t zero_words) {
+             int M, int y_round, const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
+             int Hkv, int g, int W, int Lq, u32x4* __restrict__ opblk, float* __restrict__ stblk,
+             float* __restrict__ ystat, float* __restrict__ yf32, uint32_t* __restrict__ zero_ptr,
+             int64_t zero_words) {
   constexpr int G = kMergeThreads / D;
+  constexpr int KK = D / 32;
+  constexpr int OPS = 3 * kMB * KK;
   __shared__ float s_f[kMaxSplits];
   __shared__ float s_red[kMergeThreads / 64];
   __shared__ float s_acc[G][D];
@@ -371,8 +388,9 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
       zero_ptr[i] = 0u;
 
   const int mpad = n_mc * kRows;
-  const int head = blockIdx.x / mpad;
-  const int gr = blockIdx.x % mpad;
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);  // a head's rows on the XCD that wrote its partials
+  const int head = lid / mpad;
+  const int gr = lid % mpad;
   const int mc = gr / kRows, row = gr % kRows;
   const int64_t slot0 = ((int64_t)head * n_mc + mc) * n_splits;
 
@@ -387,19 +405,33 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
     const int s = grp + i * G;
     yv[i] = s < n_splits ? py[(int64_t)s * kRows * D] : 0.f;
   }
+  // This row of the window queries, for the pass-2 operand block.
+  const bool qrow = gr < M && grp == 0;
+  T qv = static_cast<T>(0.f);
+  if (qrow) {
+    const int b = head / Hkv, hkv = head % Hkv, gi = gr / W, w = gr % W;
+    qv = q[(int64_t)b * q_sb + (int64_t)(hkv * g + gi) * q_sh + (int64_t)(Lq - W + w) * q_ss + (int64_t)d * q_sd];
+  }
+  // Split statistics (max, sum) in one pass: the sums are rescaled after the
+  // block maximum is known.
   float mx = -INFINITY;
-  for (int s = tid; s < n_splits; s += kMergeThreads) {
-    const float m = part_ml[((slot0 + s) * kRows + row) * 2];
-    s_f[s] = m;
-    mx = fmaxf(mx, m);
+  float2 ml_own[(kMaxSplits + kMergeThreads - 1) / kMergeThreads];
+#pragma unroll
+  for (int i = 0; i < (kMaxSplits + kMergeThreads - 1) / kMergeThreads; ++i) {
+    const int s = tid + i * kMergeThreads;
+    ml_own[i] = s < n_splits ? *reinterpret_cast<const float2*>(part_ml + ((slot0 + s) * kRows + row) * 2)
+                             : make_float2(-INFINITY, 0.f);
+    mx = fmaxf(mx, ml_own[i].x);
   }
   mx = block_reduce(mx, s_red, true);
   float lpart = 0.f;
-  for (int s = tid; s < n_splits; s += kMergeThreads) {
-    const float m = s_f[s];
+#pragma unroll
+  for (int i = 0; i < (kMaxSplits + kMergeThreads - 1) / kMergeThreads; ++i) {
+    const int s = tid + i * kMergeThreads;
+    const float m = ml_own[i].x;
     const float f = (m == -INFINITY || mx == -INFINITY) ? 0.f : exp2f(m - mx);
-    s_f[s] = f;
-    lpart += part_ml[((slot0 + s) * kRows + row) * 2 + 1] * f;
+    if (s < n_splits) s_f[s] = f;
+    lpart += ml_own[i].y * f;
   }
   const float l = block_reduce(lpart, s_red, false);  // also orders the s_f writes
 
@@ -431,15 +463,26 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
       lo = static_cast<T>(y - static_cast<float>(hi));
     }
     const int64_t rbase = (int64_t)head * mpad + gr;
-    yhl[(rbase * 2 + 0) * D + d] = hi;
-    yhl[(rbase * 2 + 1) * D + d] = lo;
     yf32[rbase * D + d] = y;
+    // Pass-2 operand block of this head: per row-chunk, the Q, Y-hi and Y-lo
+    // MFMA operands in per-lane order (slot (which, mb, kk), lane li + 16*lg,
+    // element e), so that pass 2 stages them with one contiguous copy.
+    const int mb = row / 16, li = row % 16, kk = d / 32, lg = (d % 32) / 8, e = d % 8;
+    T* ob = reinterpret_cast<T*>(opblk + ((int64_t)head * n_mc + mc) * OPS * 64);
+    const int word = li + 16 * lg;
+    ob[((size_t)((0 * kMB + mb) * KK + kk) * 64 + word) * 8 + e] = qv;
+    ob[((size_t)((1 * kMB + mb) * KK + kk) * 64 + word) * 8 + e] = hi;
+    ob[((size_t)((2 * kMB + mb) * KK + kk) * 64 + word) * 8 + e] = lo;
   }
   const float yn2 = block_reduce(y * y, s_red, false);
   if (tid == 0) {
     const int64_t rbase = (int64_t)head * mpad + gr;
-    ystat[rbase * 2 + 0] = valid ? mx + log2f(fmaxf(l, 1e-40f)) : INFINITY;
+    const float lse2 = valid ? mx + log2f(fmaxf(l, 1e-40f)) : INFINITY;
+    ystat[rbase * 2 + 0] = lse2;
     ystat[rbase * 2 + 1] = yn2;
+    float* sb = stblk + ((int64_t)head * n_mc + mc) * kMB * 32 + (row / 16) * 32 + (row % 16);
+    sb[0] = lse2;
+    sb[16] = yn2;
   }
 }
 
@@ -498,11 +541,10 @@ constexpr int kScLds = 4096;  // longest split range whose scores pass 2 keeps i
 
 template <typename T, int D, int WAVES, int MINW>
 __global__ void __launch_bounds__(64 * WAVES, MINW)
-pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
-             const T* __restrict__ kp, const T* __restrict__ vp,
+pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int cg, int n_splits, int kps,
              float scale_log2, float eps, int p_round,
-             const T* __restrict__ yhl, const float* __restrict__ ystat, float* __restrict__ scores,
+             const u32x4* __restrict__ opblk, const float* __restrict__ stblk, float* __restrict__ scores,
              SelFuse fz) {
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
@@ -515,52 +557,52 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   const int split = lid % n_splits;
   const int head = lid / n_splits;
-  const int b = head / Hkv, hkv = head % Hkv;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int mpad = n_mc * kRows;
 
-  const int64_t hoff = (int64_t)head * Lk * D;
-  const T* __restrict__ Kh = kp + hoff;
-  const T* __restrict__ Vh = vp + hoff;
   const float inv_g = 1.0f / static_cast<float>(g);
   const int k_begin = split * kps;
   const int k_end = min(k_begin + kps, Lk);
+  const int64_t roff = ((int64_t)head * Lk + k_begin) * D;
+  const uint32_t range = (uint32_t)(k_end - k_begin) * (D * sizeof(T));
+  const rsrc_t krs = make_rsrc(kp + roff, range), vrs = make_rsrc(vp + roff, range);
+  const uint32_t k_lane = (li * D + 8 * lg) * sizeof(T);
+  const int stride = WAVES * kTile;
+  const int nrel = k_end - k_begin;
   const bool pad_rows = mpad > M;
   const int unmasked_end = Lk - W + 1;
 
+  v8 kop[2][KK], vop[2][KK];
   for (int c0 = 0; c0 < n_mc; c0 += cg) {
     const int cn = min(cg, n_mc - c0);
     const bool first = c0 == 0, last = c0 + cn >= n_mc;
-    __syncthreads();
-    for (int slot = wv; slot < cn * OPS; slot += WAVES) {
-      const int c = slot / OPS, o = slot % OPS;
-      const int which = o / (kMB * KK), mb = (o / KK) % kMB, kk = o % KK;
-      const int m = (c0 + c) * kRows + mb * 16 + li;
-      v8 val;
-      if (which == 0) {
-        val = load_q_op<T>(q, q_sb, q_sh, q_ss, q_sd, qvec, b, hkv, g, W, Lq, M, m, 32 * kk + 8 * lg);
-      } else {
-        const int64_t rbase = (int64_t)head * mpad + m;
-        val = *reinterpret_cast<const v8*>(yhl + (rbase * 2 + (which - 1)) * D + 32 * kk + 8 * lg);
-      }
-      opnd[(size_t)slot * 64 + lane] = __builtin_bit_cast(u32x4, val);
-    }
-    for (int t = threadIdx.x; t < cn * kMB * 16; t += NT) {
-      const int c = t / (kMB * 16), r = t % (kMB * 16);
-      const int64_t rbase = (int64_t)head * mpad + (c0 + c) * kRows + r;
-      stat[(c * kMB + r / 16) * 32 + (r % 16)] = ystat[rbase * 2 + 0];
-      stat[(c * kMB + r / 16) * 32 + 16 + (r % 16)] = ystat[rbase * 2 + 1];
-    }
+    // Operands of row-chunks c0 .. c0+cn-1 (written by the merge kernel in
+    // LDS order): issue their loads, then the first tile's K/V loads, so both
+    // round trips overlap; the LDS writes wait only for the former.
+    constexpr int SPW = (2 * OPS * 64 + NT - 1) / NT;
+    const int nw = cn * OPS * 64, ns = cn * kMB * 32;
+    const u32x4* gop = opblk + ((size_t)head * n_mc + c0) * OPS * 64;
+    const float* gst = stblk + ((size_t)head * n_mc + c0) * kMB * 32;
+    u32x4 sv[SPW];
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) sv[i] = gop[min((int)threadIdx.x + i * NT, nw - 1)];
+    const float stv = gst[min((int)threadIdx.x, ns - 1)];
+    const int tw = wv * kTile;  // this wave's first tile, relative to k_begin
+    load_rows_op<T, D>(kop, krs, k_lane, tw);
+    load_rows_op<T, D>(vop, vrs, k_lane, tw);
+    __syncthreads();  // the previous group's LDS operands are dead
+#pragma unroll
+    for (int i = 0; i < SPW; ++i)
+      if ((int)threadIdx.x + i * NT < nw) opnd[threadIdx.x + i * NT] = sv[i];
+    if ((int)threadIdx.x < ns) stat[threadIdx.x] = stv;
     __syncthreads();
 
-    v8 kop[2][KK], vop[2][KK];
-    int t0 = k_begin + wv * kTile;
-    if (t0 < k_end) {
-      load_rows_op<T, D>(kop, Kh, t0, Lk, li, lg);
-      load_rows_op<T, D>(vop, Vh, t0, Lk, li, lg);
-    }
-    for (; t0 < k_end; t0 += WAVES * kTile) {
+    // The chunk count NC is a compile-time constant so that the refill loads
+    // are unconditional and the compiler's wait counts stay exact.
+    auto run = [&](auto nc_const) __attribute__((always_inline)) {
+    constexpr int NC = decltype(nc_const)::value;
+    auto tile = [&](v8 (&kop)[2][KK], v8 (&vop)[2][KK], int t0, int tn) __attribute__((always_inline)) {
       // |v|^2 of key t0+16kb+li (fp32 dot of the exact operand values), then
       // redistributed to the result layout (keys 16kb+4lg+r).
       float vn2[2][4];
@@ -575,7 +617,6 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
         for (int r = 0; r < 4; ++r) vn2[kb][r] = __shfl(part, 4 * lg + r);
       }
       const bool masked = pad_rows || t0 + kTile > unmasked_end;
-      const int tn = t0 + WAVES * kTile;
 
       float sc[2][4];
 #pragma unroll
@@ -583,7 +624,8 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 #pragma unroll
         for (int r = 0; r < 4; ++r) sc[kb][r] = 0.f;
 
-      for (int c = 0; c < cn; ++c) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
         f32x4 sacc[2][kMB], gacc[2][kMB];
         const u32x4* ob = opnd + (size_t)(c * OPS) * 64 + lane;
 #pragma unroll
@@ -608,10 +650,10 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
             }
           }
         // After the last row-chunk's MFMAs the K/V registers are free: start
-        // the next tile's loads.
-        if (c == cn - 1 && tn < k_end) {
-          load_rows_op<T, D>(kop, Kh, tn, Lk, li, lg);
-          load_rows_op<T, D>(vop, Vh, tn, Lk, li, lg);
+        // the loads of tile tn (relative; zeros past the range).
+        if (c == NC - 1) {
+          load_rows_op<T, D>(kop, krs, k_lane, tn);
+          load_rows_op<T, D>(vop, vrs, k_lane, tn);
         }
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb) {
@@ -656,7 +698,14 @@ pass2_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
           if (last && fz.sc_lds) sc_row[n - k_begin] = v * inv_g;
         }
       }
-    }
+    };
+
+    for (int t = tw; t < nrel; t += stride) tile(kop, vop, k_begin + t, t + stride);
+    };
+    if (cn == 2)
+      run(std::integral_constant<int, 2>{});
+    else
+      run(std::integral_constant<int, 1>{});
   }
   if (fz.enabled) {
     __syncthreads();  // this workgroup's score stores are done; the LDS operands are dead
@@ -738,7 +787,8 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   const size_t slots = (size_t)p.heads * p.n_mc * p.s1;
   p.off_ml = take(slots * kRows * 2 * sizeof(float));
   p.off_y = take(slots * kRows * D * sizeof(float));
-  p.off_yhl = take((size_t)p.heads * p.mpad * 2 * D * 2);
+  p.off_op = take((size_t)p.heads * p.n_mc * 3 * kMB * (D / 32) * 64 * 16);
+  p.off_stb = take((size_t)p.heads * p.n_mc * kMB * 32 * sizeof(float));
   p.off_stat = take((size_t)p.heads * p.mpad * 2 * sizeof(float));
   p.off_yf = take((size_t)p.heads * p.mpad * D * sizeof(float));
   p.total = off;
@@ -753,7 +803,8 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   const float scale_log2 = 1.4426950408889634f / sqrtf((float)D);
   float* part_ml = reinterpret_cast<float*>(ws + p.off_ml);
   float* part_y = reinterpret_cast<float*>(ws + p.off_y);
-  T* yhl = reinterpret_cast<T*>(ws + p.off_yhl);
+  u32x4* opblk = reinterpret_cast<u32x4*>(ws + p.off_op);
+  float* stblk = reinterpret_cast<float*>(ws + p.off_stb);
   float* ystat = reinterpret_cast<float*>(ws + p.off_stat);
   float* yf = reinterpret_cast<float*>(ws + p.off_yf);
   const T* qq = static_cast<const T*>(q);
@@ -775,7 +826,8 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   }
   timing_mark(st);
   hipLaunchKernelGGL((merge_kernel<T, D>), dim3(p.heads * p.mpad), dim3(kMergeThreads), 0, st, part_ml, part_y,
-                     p.n_mc, p.s1, p.M, y_round, yhl, ystat, yf, zero_ptr, zero_words);
+                     p.n_mc, p.s1, p.M, y_round, qq, q_sb, q_sh, q_ss, q_sd, Hkv, p.g, W, Lq, opblk, stblk,
+                     ystat, yf, zero_ptr, zero_words);
   timing_mark(st);
   SelFuse fz{};
   const int cg = min(p.n_mc, 2);
@@ -791,11 +843,11 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   }
   const dim3 g2(p.heads * p.s2);
   if (p.p2_waves == 8) {
-    hipLaunchKernelGGL((pass2_kernel<T, D, 8, 1>), g2, dim3(512), lds2, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, yhl, ystat, scores, fz);
+    hipLaunchKernelGGL((pass2_kernel<T, D, 8, 1>), g2, dim3(512), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M,
+                       p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, opblk, stblk, scores, fz);
   } else {
-    hipLaunchKernelGGL((pass2_kernel<T, D, 4, 2>), g2, dim3(256), lds2, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, yhl, ystat, scores, fz);
+    hipLaunchKernelGGL((pass2_kernel<T, D, 4, 2>), g2, dim3(256), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M,
+                       p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, opblk, stblk, scores, fz);
   }
   timing_mark(st);
   return hipGetLastError();
