@@ -39,7 +39,8 @@ HBM_PEAK_GBPS = 8000.0
 # into the scoring pass's tail, and with the standalone selection kernels
 STAGES_FUSED = ("pass1_partials", "merge", "pass2_scores_pool", "select_cand", "emit_compact")
 STAGES_UNFUSED = ("pass1_partials", "merge", "pass2_scores", "select_pool", "select_cand", "emit_compact")
-STREAM_STAGES = ("pass1_partials", "pass2_scores", "pass2_scores_pool")  # kernels that stream all of K and V
+# kernels that stream all of K and V
+STREAM_STAGES = ("pass1_partials", "pass2_scores", "pass2_scores_pool")
 
 WORKLOADS = {
     "llama8b_layer_32k": dict(B=1, Hq=32, Hkv=8, D=128, Lq=32768, Lk=32768, window=8, kernel=11, ratio=0.1,
@@ -122,8 +123,8 @@ def pmc_summary(fetch_dir, write_dir, calib_fetch_dir, calib_write_dir, calib_mi
     sf, sw = true_kib / copy_f, true_kib / copy_w
     rows = {}
     for name, vals in fetch.items():
-        short = next((s for s in ("pass1", "pass2", "merge", "sel_pool", "sel_cand", "sel_emit",
-                                  "compact") if s in name), None)
+        short = next((s for s in ("pass1", "pass2", "sel_pool", "sel_cand", "sel_emit", "compact")
+                      if s in name), None)
         if short is None:
             continue
         fk = statistics.mean(vals)

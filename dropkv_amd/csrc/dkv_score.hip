@@ -76,6 +76,15 @@ __device__ __forceinline__ void load_q_ops(typename Elem<T>::v8 (&qop)[D / 32], 
     qop[kk] = load_q_op<T>(q, q_sb, q_sh, q_ss, q_sd, qvec, b, hkv, g, W, Lq, M, m, 32 * kk + 8 * lg);
 }
 
+// Next tile for this wave from the workgroup's LDS counter: waves that get
+// their data sooner take more of the workgroup's tiles, so the waves of a
+// workgroup finish together.  Wave-uniform result.
+__device__ __forceinline__ int grab_tile(uint32_t* ctr) {
+  uint32_t v = 0u;
+  if ((threadIdx.x & 63) == 0) v = atomicAdd(ctr, 1u);
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
 // ---------------------------------------------------------------------------
 // Tile loads shared by the two passes.  A workgroup reads the rows
 // [k_begin, k_end) of one head through buffer views (make_rsrc) that end at
@@ -282,13 +291,13 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     }
   };
 
+  // Static tile order (wave w takes tiles w, w+WAVES, ...): the summation
+  // order, and so every bit of the result, is the same on every call.
   const int nrel = k_end - k_begin;
   int t = wv * kTile;  // relative to k_begin
-  if (t < nrel) {
-    load_rows_op<T, D>(kop, krs, k_lane, t);
-    load_v_pairs<T, D>(va, vb, vrs, v_lane, t);
-    for (; t < nrel; t += stride) tile(kop, va, vb, k_begin + t, t + stride);
-  }
+  load_rows_op<T, D>(kop, krs, k_lane, t);  // zeros if t >= nrel
+  load_v_pairs<T, D>(va, vb, vrs, v_lane, t);
+  for (; t < nrel; t += stride) tile(kop, va, vb, k_begin + t, t + stride);
 
   // Row sums are per lane-group partials; fold the four groups.
 #pragma unroll
@@ -553,6 +562,10 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
   extern __shared__ u32x4 opnd[];    // [cg][OPS][64] then float stats [cg][kMB][2][16]
   float* stat = reinterpret_cast<float*>(opnd + (size_t)cg * OPS * 64);
   float* sc_row = stat + cg * kMB * 32;  // [kps] this workgroup's scores (fused pooling only)
+  // Top-digit histogram of the fused pooling (after sc_row), zeroed now.
+  uint32_t* hist_l = reinterpret_cast<uint32_t*>(sc_row + kps);
+  if (fz.enabled && fz.sc_lds)
+    for (int i = threadIdx.x; i < kBins1; i += NT) hist_l[i] = 0u;
 
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   const int split = lid % n_splits;
@@ -568,8 +581,8 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
   const uint32_t range = (uint32_t)(k_end - k_begin) * (D * sizeof(T));
   const rsrc_t krs = make_rsrc(kp + roff, range), vrs = make_rsrc(vp + roff, range);
   const uint32_t k_lane = (li * D + 8 * lg) * sizeof(T);
-  const int stride = WAVES * kTile;
-  const int nrel = k_end - k_begin;
+  const int ntiles = (k_end - k_begin + kTile - 1) / kTile;
+  __shared__ uint32_t s_next;
   const bool pad_rows = mpad > M;
   const int unmasked_end = Lk - W + 1;
 
@@ -588,10 +601,15 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
 #pragma unroll
     for (int i = 0; i < SPW; ++i) sv[i] = gop[min((int)threadIdx.x + i * NT, nw - 1)];
     const float stv = gst[min((int)threadIdx.x, ns - 1)];
-    const int tw = wv * kTile;  // this wave's first tile, relative to k_begin
-    load_rows_op<T, D>(kop, krs, k_lane, tw);
-    load_rows_op<T, D>(vop, vrs, k_lane, tw);
-    __syncthreads();  // the previous group's LDS operands are dead
+    // Tiles are handed out dynamically: wave w starts with tile w, then
+    // takes the next unclaimed one from s_next (relative to k_begin).  Each
+    // key's score is computed by one wave in a fixed order, so the results do
+    // not depend on the assignment.
+    const int tw = wv;
+    load_rows_op<T, D>(kop, krs, k_lane, tw * kTile);
+    load_rows_op<T, D>(vop, vrs, k_lane, tw * kTile);
+    __syncthreads();  // the previous group's LDS operands and s_next are dead
+    if (threadIdx.x == 0) s_next = WAVES;
 #pragma unroll
     for (int i = 0; i < SPW; ++i)
       if ((int)threadIdx.x + i * NT < nw) opnd[threadIdx.x + i * NT] = sv[i];
@@ -700,7 +718,11 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
       }
     };
 
-    for (int t = tw; t < nrel; t += stride) tile(kop, vop, k_begin + t, t + stride);
+    for (int tc = tw; tc < ntiles;) {
+      const int tn = grab_tile(&s_next);
+      tile(kop, vop, k_begin + tc * kTile, tn * kTile);
+      tc = tn;
+    }
     };
     if (cn == 2)
       run(std::integral_constant<int, 2>{});
@@ -716,7 +738,7 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
     float* prow = fz.ws.pooled + (int64_t)head * Lk;
     uint32_t* rw = fz.ws.rowws + (int64_t)head * kRowWords;
     if (fz.sc_lds)
-      pool_range_lds<NT>(sc_row, k_begin, prow, rw, Lk, h, Lk - fz.window, i0, i1, L, L + kBins1);
+      pool_range_lds<NT>(sc_row, k_begin, prow, rw, Lk, h, Lk - fz.window, i0, i1, hist_l, hist_l + kBins1);
     else
       pool_range<NT>(scores + (int64_t)head * Lk, prow, rw, Lk, h, Lk - fz.window, i0, i1,
                      reinterpret_cast<float*>(L), L + kSub + 2 * kMaxHalo, L + kSub + 2 * kMaxHalo + kBins1);
@@ -838,7 +860,8 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
     fz.ks = fuse->ks;
     fz.window = fuse->window;
     fz.sc_lds = p.kps2 <= kScLds;
-    if (fz.sc_lds) lds2 += (size_t)p.kps2 * 4;  // sc_row[] after the operands and statistics
+    // sc_row[] and the histogram after the operands and statistics.
+    if (fz.sc_lds) lds2 += (size_t)p.kps2 * 4 + (size_t)(kBins1 + 16) * 4;
     lds2 = std::max(lds2, (size_t)kPoolLdsWords * 4);
   }
   const dim3 g2(p.heads * p.s2);

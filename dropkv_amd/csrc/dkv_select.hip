@@ -14,9 +14,8 @@
 
 namespace dkv {
 
-constexpr int kSelT = 256;            // threads per workgroup, all stages
+constexpr int kSelT = 1024;           // threads per workgroup, all stages
 constexpr int kPer = kChunk / kSelT;  // keys per thread
-constexpr int kUnroll = 8;            // candidate loads in flight per thread
 
 __global__ void __launch_bounds__(kSelT)
 sel_zero_kernel(uint32_t* __restrict__ p, int64_t n) {
@@ -43,14 +42,15 @@ sel_pool_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
 // ---------------------------------------------------------------------------
 // cand: grid = rows * chunks.
 // ---------------------------------------------------------------------------
+constexpr int kBndPer = kBndLds / kSelT;  // boundary raw scores per thread (at most)
+
 __global__ void __launch_bounds__(kSelT)
 sel_cand_kernel(const float* __restrict__ scores, int Lk, int ks, int window, int keep, int chunks, SplitGeom geom,
                 SelWs ws) {
-  __shared__ uint32_t hist[kBins1];
-  __shared__ uint32_t hist2[kBins2];
+  __shared__ __attribute__((aligned(16))) uint32_t hist[kBins1];
   __shared__ float bxs[kBndLds];
   __shared__ float bpool[kBndPoolLds];
-  __shared__ uint32_t small[64];
+  __shared__ uint32_t small[128];  // scan partials [0, 32), bin / counts at 64.., max at 96..
   const int tid = threadIdx.x;
   const int row = blockIdx.x / chunks;
   const int c = blockIdx.x % chunks;
@@ -60,31 +60,45 @@ sel_cand_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
   const float* srow = scores + (int64_t)row * Lk;
   float* prow = ws.pooled + (int64_t)row * Lk;
   uint32_t* wsum = small;
-  int* s_bin = reinterpret_cast<int*>(small + 16);
-  uint32_t* s_above = small + 17;
-  uint32_t* s_base = small + 18;
+  int* s_bin = reinterpret_cast<int*>(small + 64);
+  uint32_t* s_above = small + 65;
 
-  // The chunk's pooled values (complete except the boundary keys) are loaded
-  // first, in the same round trip as everything step (1) reads.
+  // One round trip: this chunk's pooled values (complete except the boundary
+  // keys), the row's top-digit histogram and interior maximum, and the raw
+  // scores [b-2h, b+2h) around each split boundary b = i*kps (1 <= i < n_splits).
   float cv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int j = c * kChunk + tid + i * kSelT;
     cv[i] = j < Lk ? prow[j] : 0.f;
   }
-  // (1) The keys within h of a split boundary b = i*kps (1 <= i < n_splits):
-  //     raw scores [b-2h, b+2h) staged, then each window read from LDS.
+  static_assert(kBins1 == 2 * kSelT, "two histogram words per thread");
+  const uint2 hv = reinterpret_cast<const uint2*>(rw + kRowHist1)[tid];
+  const uint32_t rmax = rw[kRowMax];
   const int nb = geom.n_splits - 1;
   const int w4 = 4 * h, w2 = 2 * h;
-  for (int t = tid; t < nb * w4; t += kSelT) {
-    const int u = (t / w4 + 1) * geom.kps - 2 * h + t % w4;
-    bxs[t] = (u >= 0 && u < Lk) ? srow[u] : -INFINITY;
+  const int nbx = nb * w4;
+  float bv[kBndPer];
+#pragma unroll
+  for (int i = 0; i < kBndPer; ++i) {
+    if (i * kSelT >= nbx) break;
+    const int t = tid + i * kSelT;
+    bv[i] = -INFINITY;
+    if (t < nbx) {
+      const int u = (t / w4 + 1) * geom.kps - 2 * h + t % w4;
+      if (u >= 0 && u < Lk) bv[i] = srow[u];
+    }
   }
-  for (int i = tid; i < kBins1; i += kSelT) {
-    hist[i] = rw[kRowHist1 + i];
-    hist2[i] = 0u;
+  reinterpret_cast<uint2*>(hist)[tid] = hv;
+#pragma unroll
+  for (int i = 0; i < kBndPer; ++i) {
+    if (i * kSelT >= nbx) break;
+    const int t = tid + i * kSelT;
+    if (t < nbx) bxs[t] = bv[i];
   }
   __syncthreads();
+
+  // The boundary keys' windows, read from LDS; they complete the histogram.
   uint32_t bmax = 0u;
   for (int t = tid; t < nb * w2; t += kSelT) {
     const int bi = t / w2, k = t % w2;
@@ -95,14 +109,14 @@ sel_cand_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
       for (int u = 0; u <= 2 * h; ++u) m = fmaxf(m, w[u]);
       const uint32_t key = float_key(m);
       bmax = max(bmax, key);
-      if (j < prot) atomicAdd(&hist[key >> 21], 1u);
+      if (j < prot) atomicAdd(&hist[key >> kShift1], 1u);
     }
     bpool[t] = m;
   }
-  const uint32_t gmax = block_max_u32(max(bmax, rw[kRowMax]), small + 32);
+  const uint32_t gmax = block_max_u32(max(bmax, rmax), small + 96);
   const uint32_t kbig = float_key(key_float(gmax) + 1.0f);
   if (tid == 0) {
-    hist[kbig >> 21] += (uint32_t)window;
+    hist[kbig >> kShift1] += (uint32_t)window;
     *s_bin = 0;
     *s_above = 0u;
   }
@@ -111,9 +125,9 @@ sel_cand_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
   const uint32_t b1 = (uint32_t)*s_bin;
   const uint32_t k1 = (uint32_t)keep - *s_above;
 
-  // (2) This chunk: above-b1 count, candidates (keys in b1) and their digit-2
-  //     histogram.  Boundary keys take their value from bpool and are written
-  //     to the pooled row here (the pooling stage skipped them).
+  // This chunk: the count above b1 and the candidates (keys in b1), which go
+  // to the chunk's own region of the candidate arrays.  Boundary keys take
+  // their value from bpool and are written to the pooled row here.
   uint32_t keys[kPer];
   uint32_t nab = 0u, ncand = 0u;
 #pragma unroll
@@ -129,45 +143,38 @@ sel_cand_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
         prow[j] = v;
       }
       keys[i] = j >= prot ? kbig : float_key(v);
-      const uint32_t d = keys[i] >> 21;
+      const uint32_t d = keys[i] >> kShift1;
       nab += d > b1 ? 1u : 0u;
       ncand += d == b1 ? 1u : 0u;
     }
   }
   uint32_t pc, dummy, tot_c, tot_ab;
   block_excl_scan2<kSelT>(ncand, nab, &pc, &dummy, &tot_c, &tot_ab, wsum);
+  uint32_t pos = (uint32_t)c * kChunk + pc;
+  uint32_t* ckey = ws.cand_key + (int64_t)row * Lk;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = c * kChunk + tid + i * kSelT;
+    if (j < Lk && (keys[i] >> kShift1) == b1) {
+      ckey[pos] = keys[i];
+      ++pos;
+    }
+  }
   if (tid == 0) {
-    *s_base = tot_c ? atomicAdd(&rw[kRowNCand], tot_c) : 0u;
-    ws.above[(int64_t)row * chunks + c] = tot_ab;
+    ws.cnt[(int64_t)row * chunks + c] = make_uint2(tot_ab, tot_c);
     if (c == 0) {
       rw[kRowB1 + 0] = b1;
       rw[kRowB1 + 1] = k1;
       rw[kRowB1 + 2] = gmax;
     }
   }
-  __syncthreads();
-  uint32_t pos = *s_base + pc;
-  uint32_t* ckey = ws.cand_key + (int64_t)row * Lk;
-  uint32_t* cidx = ws.cand_idx + (int64_t)row * Lk;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = c * kChunk + tid + i * kSelT;
-    if (j < Lk && (keys[i] >> 21) == b1) {
-      ckey[pos] = keys[i];
-      cidx[pos] = (uint32_t)j;
-      ++pos;
-      atomicAdd(&hist2[(keys[i] >> 10) & 2047u], 1u);
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < kBins2; i += kSelT)
-    if (hist2[i]) atomicAdd(&rw[kRowHist2 + i], hist2[i]);
 }
 
 // ---------------------------------------------------------------------------
-// emit: grid = rows * chunks.  Resolves T from the candidate list, then
-// thread t owns the kPer consecutive keys c*kChunk + kPer*t ..; kept keys are
-// written in index order, then (when ko is given) their K/V rows are copied.
+// emit: grid = rows * chunks.  Gathers the row's candidates into LDS and
+// resolves T from them, then thread t owns the kPer consecutive keys
+// c*kChunk + kPer*t ..; kept keys are written in index order, then (when ko
+// is given) their K/V rows are copied.
 // ---------------------------------------------------------------------------
 struct CompactArgs {
   const uint8_t* k;
@@ -179,102 +186,201 @@ struct CompactArgs {
   uint8_t* vo;
 };
 
-constexpr int kEmitCandLds = 4096;  // candidates staged in LDS by emit (more: read from global)
+constexpr int kEmitCandLds = 4096;                  // candidates held in LDS (more: read from global)
+constexpr int kSpecPer = kEmitCandLds / (4 * kSelT);  // speculative 4-candidate groups per thread
+constexpr int kCntPer = kMaxChunks / kSelT;           // chunk counts per thread (at most)
+constexpr int kSpecMax = 128;                         // speculative candidates per chunk region (at most)
+
+// Candidate p of the row's list (chunk-major) when it is not in LDS: chunk
+// by binary search over the exclusive prefix counts s_pref[0..chunks].
+__device__ __forceinline__ uint32_t cand_global(const uint32_t* s_pref, int chunks, const uint32_t* gkey,
+                                                uint32_t p) {
+  int lo = 0, hi = chunks - 1;  // last chunk with s_pref[cc] <= p
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pref[mid] <= p) lo = mid;
+    else hi = mid - 1;
+  }
+  const int64_t at = (int64_t)lo * kChunk + (p - s_pref[lo]);
+  return gkey[at];
+}
 
 __global__ void __launch_bounds__(kSelT)
-sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __restrict__ out_idx,
+sel_emit_kernel(int Lk, int window, int keep, int chunks, int spec, SelWs ws, int64_t* __restrict__ out_idx,
                 float* __restrict__ pooled_out, CompactArgs ca) {
   __shared__ uint32_t hist[kBins2];  // digit-2, then digit-3 histogram
-  __shared__ uint32_t small[64];
-  __shared__ uint32_t lkey[kEmitCandLds], lidx[kEmitCandLds];
+  __shared__ uint32_t small[128];  // scan partials [0, 32), bin / counts at 64.., max at 96..
+  __shared__ uint32_t lkey[kEmitCandLds];
+  __shared__ uint32_t s_pref[kMaxChunks + 1];
   __shared__ int s_src[kChunk];
   __shared__ int s_dst[kChunk];
   const int tid = threadIdx.x;
   const int row = blockIdx.x / chunks;
   const int c = blockIdx.x % chunks;
   uint32_t* wsum = small;
-  int* s_bin = reinterpret_cast<int*>(small + 16);
-  uint32_t* s_above = small + 17;
+  int* s_bin = reinterpret_cast<int*>(small + 64);
+  uint32_t* s_above = small + 65;
   const uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
   const float* pooled = ws.pooled + (int64_t)row * Lk;
+  const uint32_t* gkey = ws.cand_key + (int64_t)row * Lk;
+  const uint2* cnt = ws.cnt + (int64_t)row * chunks;
   const int prot = Lk - window;
 
-  // Round trip 1: the row words, this chunk's pooled values and the
-  // above-b1 counts of the earlier chunks.
+  // One round trip: the row words, this chunk's pooled values, every chunk's
+  // counts and, speculatively, the first `spec` candidates (a multiple of 4)
+  // of the first ncov = kEmitCandLds / spec chunk regions.
   const int j0 = c * kChunk + kPer * tid;
   float pv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) pv[i] = (j0 + i < Lk) ? pooled[j0 + i] : 0.f;
-  uint32_t hv[kBins2 / kSelT];
-#pragma unroll
-  for (int i = 0; i < kBins2 / kSelT; ++i) hv[i] = rw[kRowHist2 + tid + i * kSelT];
   const uint32_t b1 = rw[kRowB1 + 0], k1 = rw[kRowB1 + 1];
   const float big = key_float(rw[kRowB1 + 2]) + 1.0f;
   const uint32_t kbig = float_key(big);
-  const uint32_t nc = rw[kRowNCand];
-  uint32_t g = 0u, e = 0u;
-  for (int cc = tid; cc < c; cc += kSelT) g += ws.above[(int64_t)row * chunks + cc];
+  const int seg = (chunks + kSelT - 1) / kSelT;  // chunk counts owned by each thread (<= kCntPer)
+  uint2 cv[kCntPer];
+#pragma unroll
+  for (int i = 0; i < kCntPer; ++i) {
+    if (i >= seg) break;
+    const int cc = tid * seg + i;
+    cv[i] = cc < chunks ? cnt[cc] : make_uint2(0u, 0u);
+  }
+  uint4 sk[kSpecPer];
+  const int nspec = min(chunks * spec, kEmitCandLds);
+#pragma unroll
+  for (int i = 0; i < kSpecPer; ++i) {
+    if (4 * i * kSelT >= nspec) break;
+    const int e = 4 * (tid + i * kSelT);
+    const int cc = e / spec, off = e - cc * spec;
+    const int64_t at = (int64_t)cc * kChunk + off;
+    if (cc < chunks && at + 4 <= Lk) {
+      sk[i] = *reinterpret_cast<const uint4*>(gkey + at);
+    } else {
+      sk[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
 
-  // Round trip 2: the candidate list (staged in LDS when it fits).
-  const uint32_t* gkey = ws.cand_key + (int64_t)row * Lk;
-  const uint32_t* gidx = ws.cand_idx + (int64_t)row * Lk;
+  // Candidate counts -> exclusive prefix s_pref (chunk-major list order);
+  // above-b1 keys of the chunks before this one.
+  const int ncov = kEmitCandLds / spec;
+  uint32_t tsum = 0u, g = 0u, e = 0u;
+  bool overflow = false;
+#pragma unroll
+  for (int i = 0; i < kCntPer; ++i) {
+    if (i >= seg) break;
+    const int cc = tid * seg + i;
+    if (cc < chunks) {
+      tsum += cv[i].y;
+      if (cc < c) g += cv[i].x;
+      overflow |= cv[i].y > (cc < ncov ? (uint32_t)spec : 0u);
+    }
+  }
+  uint32_t run, dummy, nc;
+  block_excl_scan2<kSelT>(tsum, 0u, &run, &dummy, &nc, nullptr, wsum);
+#pragma unroll
+  for (int i = 0; i < kCntPer; ++i) {
+    if (i >= seg) break;
+    const int cc = tid * seg + i;
+    if (cc < chunks) {
+      s_pref[cc] = run;
+      run += cv[i].y;
+    }
+  }
+  if (tid == 0) s_pref[chunks] = nc;
+  const bool any_overflow = __syncthreads_or(overflow);
   const bool in_lds = nc <= (uint32_t)kEmitCandLds;
+
+  // Candidates into LDS: the speculative ones, then (rarely) the rest of any
+  // region longer than spec.
   if (in_lds) {
-    for (uint32_t base = 0; base < nc; base += kSelT * kUnroll) {
-      uint32_t kv[kUnroll], iv[kUnroll];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const uint32_t p = base + tid + u * kSelT;
-        kv[u] = p < nc ? gkey[p] : 0u;
-        iv[u] = p < nc ? gidx[p] : 0u;
+    for (int i = 0; i < kSpecPer; ++i) {
+      if (4 * i * kSelT >= nspec) break;
+      const int e4 = 4 * (tid + i * kSelT);
+      const int cc = e4 / spec, off = e4 - cc * spec;
+      if (cc < chunks) {
+        const uint32_t n = s_pref[cc + 1] - s_pref[cc];
+        const uint32_t kk[4] = {sk[i].x, sk[i].y, sk[i].z, sk[i].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if ((uint32_t)(off + q) < n) {
+            lkey[s_pref[cc] + off + q] = kk[q];
+          }
       }
+    }
+    if (any_overflow) {
+      // Every list entry not covered by the speculative loads, 8 loads in
+      // flight per thread.
+      for (uint32_t p0 = tid; p0 < nc; p0 += 8 * kSelT) {
+        uint32_t kv[8];
+        int32_t dst[8];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const uint32_t p = base + tid + u * kSelT;
-        if (p < nc) {
-          lkey[p] = kv[u];
-          lidx[p] = iv[u];
+        for (int q = 0; q < 8; ++q) {
+          const uint32_t p = p0 + q * kSelT;
+          dst[q] = -1;
+          if (p < nc) {
+            int lo = 0, hi = chunks - 1;  // chunk of entry p
+            while (lo < hi) {
+              const int mid = (lo + hi + 1) >> 1;
+              if (s_pref[mid] <= p) lo = mid;
+              else hi = mid - 1;
+            }
+            const uint32_t o = p - s_pref[lo];
+            if (o >= (lo < ncov ? (uint32_t)spec : 0u)) {
+              kv[q] = gkey[(int64_t)lo * kChunk + o];
+              dst[q] = (int32_t)p;
+            }
+          }
         }
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (dst[q] >= 0) lkey[dst[q]] = kv[q];
       }
     }
   }
-  const uint32_t* ckey = in_lds ? lkey : gkey;
-  const uint32_t* cidx = in_lds ? lidx : gidx;
-
-  // Digit 2.
-#pragma unroll
-  for (int i = 0; i < kBins2 / kSelT; ++i) hist[tid + i * kSelT] = hv[i];
+  for (int i = tid; i < kBins2; i += kSelT) hist[i] = 0u;
   if (tid == 0) {
     *s_bin = 0;
     *s_above = 0u;
   }
   __syncthreads();
+
+  // Digit 2 (every candidate is in bin b1).
+  for (uint32_t p = tid; p < nc; p += kSelT) {
+    uint32_t kv;
+    if (in_lds) kv = lkey[p];
+    else kv = cand_global(s_pref, chunks, gkey, p);
+    atomicAdd(&hist[(kv >> kShift2) & (kBins2 - 1)], 1u);
+  }
+  __syncthreads();
   find_bin<kBins2, kSelT>(hist, k1, s_bin, s_above, wsum);
   const uint32_t b2 = (uint32_t)*s_bin;
   const uint32_t k2 = k1 - *s_above;
-  const uint32_t pre = (b1 << 11) | b2;
+  const uint32_t pre = (b1 << kBits2) | b2;
   __syncthreads();
   for (int i = tid; i < kBins3; i += kSelT) hist[i] = 0u;
   __syncthreads();
   // Digit 3 over the candidates matching the first two digits.
   for (uint32_t p = tid; p < nc; p += kSelT) {
-    const uint32_t kv = ckey[p];
-    if ((kv >> 10) == pre) atomicAdd(&hist[kv & 1023u], 1u);
+    uint32_t kv;
+    if (in_lds) kv = lkey[p];
+    else kv = cand_global(s_pref, chunks, gkey, p);
+    if ((kv >> kShift2) == pre) atomicAdd(&hist[kv & (kBins3 - 1)], 1u);
   }
   __syncthreads();
   find_bin<kBins3, kSelT>(hist, k2, s_bin, s_above, wsum);
-  const uint32_t T = (pre << 10) | (uint32_t)*s_bin;
+  const uint32_t T = (pre << kBits3) | (uint32_t)*s_bin;
   const uint32_t take_eq = k2 - *s_above;
 
   // Output offsets of this chunk: kept keys > T and keys == T in earlier
-  // chunks (above-b1 keys per chunk, plus the candidates before it).
-  const uint32_t lim = (uint32_t)c * kChunk;
-  for (uint32_t p = tid; p < nc; p += kSelT) {
-    if (cidx[p] < lim) {
-      const uint32_t kv = ckey[p];
-      g += kv > T ? 1u : 0u;
-      e += kv == T ? 1u : 0u;
-    }
+  // chunks (above-b1 keys per chunk, plus the candidates of those chunks,
+  // which are list entries [0, s_pref[c])).
+  const uint32_t lim = s_pref[c];
+  for (uint32_t p = tid; p < lim; p += kSelT) {
+    uint32_t kv;
+    if (in_lds) kv = lkey[p];
+    else kv = cand_global(s_pref, chunks, gkey, p);
+    g += kv > T ? 1u : 0u;
+    e += kv == T ? 1u : 0u;
   }
   uint32_t gt0, eq0;
   block_sum2<kSelT>(g, e, &gt0, &eq0, wsum);
@@ -384,8 +490,11 @@ hipError_t launch_select_after_pool(const float* scores, int rows, int Lk, int k
   hipLaunchKernelGGL(sel_cand_kernel, grid, dim3(kSelT), 0, st, scores, Lk, ks, window, keep, chunks,
                      SplitGeom{n_splits, kps}, ws);
   timing_mark(st);
-  hipLaunchKernelGGL(sel_emit_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, ws, out_idx, pooled_out,
-                     compact_args(cp));
+  // Speculative candidates per chunk region: a multiple of 4, at least 4,
+  // chunks * spec <= kEmitCandLds.
+  const int spec = std::max(4, std::min(kSpecMax, kEmitCandLds / chunks) & ~3);
+  hipLaunchKernelGGL(sel_emit_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, spec, ws, out_idx,
+                     pooled_out, compact_args(cp));
   timing_mark(st);
   return hipGetLastError();
 }

@@ -17,12 +17,16 @@
 //   cand   (row, 1024-key chunk) workgroups: each first pools the few keys
 //          next to the scoring pass's split boundaries (redundantly), which
 //          completes the histogram and fixes the boundary bin b1; then its
-//          chunk's keys above b1 are counted and those inside b1 appended to
-//          the row's candidate list, with their digit-2 histogram;
-//   emit   (row, chunk) workgroups: each resolves digits 2 and 3 from the
-//          candidate list (a few percent of the row), derives its chunk's
-//          output offsets, writes its kept indices in index order and copies
-//          the K/V rows they name.
+//          chunk's keys above b1 are counted and those inside b1 (the
+//          candidates) written to the chunk's own region of the candidate
+//          arrays, with the two counts;
+//   emit   (row, chunk) workgroups: each gathers the row's candidates (a few
+//          percent of the row) into LDS, resolves digits 2 and 3 from them,
+//          derives its chunk's output offsets, writes its kept indices in
+//          index order and copies the K/V rows they name.
+// Every stage issues all of its global loads in one round trip where the
+// data allow (emit loads the first kSpec candidates of every chunk region
+// before it knows the counts).
 #pragma once
 
 #include "dkv_common.h"
@@ -30,9 +34,12 @@
 namespace dkv {
 
 constexpr int kChunk = 1024;      // keys per cand/emit workgroup (offset granularity)
-constexpr int kBins1 = 2048;      // key bits 31..21
-constexpr int kBins2 = 2048;      // key bits 20..10
-constexpr int kBins3 = 1024;      // key bits 9..0
+constexpr int kBits1 = 11, kBits2 = 11, kBits3 = 10;  // radix digits, most significant first
+constexpr int kShift1 = 32 - kBits1;                // digit 1 = key >> kShift1
+constexpr int kShift2 = kBits3;                     // digit 2 = (key >> kShift2) & (kBins2 - 1)
+constexpr int kBins1 = 1 << kBits1;                 // key bits 31..21
+constexpr int kBins2 = 1 << kBits2;                 // key bits 20..10
+constexpr int kBins3 = 1 << kBits3;                 // key bits 9..0
 constexpr int kMaxHalo = 64;      // kernel_size <= 2*kMaxHalo+1
 constexpr int kMaxChunks = 4096;  // Lk <= kMaxChunks * kChunk
 constexpr int kBndLds = 4096;     // LDS words for the boundary keys' raw-score neighbourhoods
@@ -40,19 +47,16 @@ constexpr int kBndPoolLds = 2048; // LDS words for the boundary keys' pooled val
 
 // Per-row words that must be zero on entry (the merge kernel or the zero
 // kernel clears them every call), then results of the cand stage:
-constexpr int kRowMax = 0;                     // max pooled key of the interiors
-constexpr int kRowHist1 = 1;                   // top-digit histogram (unprotected interior keys)
-constexpr int kRowHist2 = kRowHist1 + kBins1;  // digit-2 histogram of the candidates
-constexpr int kRowNCand = kRowHist2 + kBins2;  // candidate count
-constexpr int kRowB1 = kRowNCand + 1;          // b1, keep left in b1, max key of the row (cand stage)
-constexpr int kRowWords = kRowB1 + 3;
+constexpr int kRowMax = 0;                 // max pooled key of the interiors
+constexpr int kRowB1 = 1;                  // b1, keep left in b1, max key of the row (cand stage)
+constexpr int kRowHist1 = 4;               // top-digit histogram (unprotected interior keys), 16-byte aligned
+constexpr int kRowWords = kRowHist1 + kBins1;
 
 struct SelWs {
   uint32_t* rowws;     // [rows][kRowWords]
   float* pooled;       // [rows][Lk]
-  uint32_t* above;     // [rows][chunks] keys of a chunk above the boundary bin
-  uint32_t* cand_key;  // [rows][Lk]
-  uint32_t* cand_idx;  // [rows][Lk]
+  uint2* cnt;          // [rows][chunks] {keys above b1, candidates} of each chunk
+  uint32_t* cand_key;  // [rows][Lk]: chunk c's candidate keys at c*kChunk ..
 };
 
 inline size_t sel_al256(size_t b) { return (b + 255) & ~size_t(255); }
@@ -68,9 +72,8 @@ inline SelWs sel_layout(char* base, int64_t rows, int64_t Lk, size_t* total) {
   };
   w.rowws = reinterpret_cast<uint32_t*>(take((size_t)rows * kRowWords * 4));
   w.pooled = reinterpret_cast<float*>(take((size_t)rows * Lk * 4));
-  w.above = reinterpret_cast<uint32_t*>(take((size_t)rows * chunks * 4));
+  w.cnt = reinterpret_cast<uint2*>(take((size_t)rows * chunks * 8));
   w.cand_key = reinterpret_cast<uint32_t*>(take((size_t)rows * Lk * 4));
-  w.cand_idx = reinterpret_cast<uint32_t*>(take((size_t)rows * Lk * 4));
   if (total) *total = off;
   return w;
 }
@@ -229,7 +232,7 @@ __device__ void pool_range(const float* __restrict__ srow, float* __restrict__ p
       prow[j] = m;
       const uint32_t key = float_key(m);
       kmax = max(kmax, key);
-      if (j < prot) atomicAdd(&hist[key >> 21], 1u);
+      if (j < prot) atomicAdd(&hist[key >> kShift1], 1u);
     }
   }
   kmax = block_max_u32(kmax, red);
@@ -240,13 +243,12 @@ __device__ void pool_range(const float* __restrict__ srow, float* __restrict__ p
 
 // The same, when the workgroup's own scores [k_begin, k_end) are in LDS (sc)
 // and every window of [i0, i1) lies inside them once clipped to [0, Lk).
-// hist: kBins1 words, red: 16 words of LDS; the caller has made sc visible.
+// hist: kBins1 words of LDS, zeroed by the caller; red: 16 words of LDS; the
+// caller has made sc and the zeroed hist visible.
 template <int NT>
 __device__ void pool_range_lds(const float* sc, int k_begin, float* __restrict__ prow, uint32_t* rw, int Lk, int h,
                                int prot, int i0, int i1, uint32_t* hist, uint32_t* red) {
   const int tid = threadIdx.x;
-  for (int i = tid; i < kBins1; i += NT) hist[i] = 0u;
-  __syncthreads();
   uint32_t kmax = 0u;
   for (int j = i0 + tid; j < i1; j += NT) {
     const int u0 = max(j - h, 0) - k_begin, u1 = min(j + h, Lk - 1) - k_begin;
@@ -255,7 +257,7 @@ __device__ void pool_range_lds(const float* sc, int k_begin, float* __restrict__
     prow[j] = m;
     const uint32_t key = float_key(m);
     kmax = max(kmax, key);
-    if (j < prot) atomicAdd(&hist[key >> 21], 1u);
+    if (j < prot) atomicAdd(&hist[key >> kShift1], 1u);
   }
   kmax = block_max_u32(kmax, red);
   if (tid == 0 && i0 < i1) atomicMax(&rw[kRowMax], kmax);
