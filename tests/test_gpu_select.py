@@ -23,7 +23,8 @@ def _select_case(gpu, scores, ks, window, keep):
 
 
 @pytest.mark.parametrize("rows,Lk,keep", [(8, 32768, 3276), (2, 512, 51), (3, 100, 30), (1, 8, 8),
-                                          (4, 1000, 1), (2, 70000, 7000), (1, 4096, 4096)])
+                                          (4, 1000, 1), (2, 70000, 7000), (1, 4096, 4096),
+                                          (1, 32769, 3277), (2, 32767, 5000), (1, 40000, 1)])
 def test_select_random(gpu, rows, Lk, keep):
     g = torch.Generator().manual_seed(Lk + keep)
     scores = torch.rand(1, rows, Lk, generator=g) * 1e-3
@@ -134,6 +135,9 @@ def test_evict_fused_matches_ops(gpu, shape):
     (6400, 81, 8, 640, 200, False),   # ranges shorter than the kernel: standalone selection
     (2048, 11, 600, 700, 8, False),   # protected window wider than a split range
     (3000, 11, 8, 300, 0, True),      # V = 0: every score is 0, all ties
+    (32768, 11, 8, 3276, 0, False),   # the headline row length
+    (40000, 11, 8, 4000, 0, False),   # 40 chunks: more than one speculative window per region
+    (40000, 11, 8, 4000, 0, True),    # ... with every score tied (overflow of the speculative loads)
 ])
 def test_evict_fused_selection_edges(gpu, Lk, ks, window, keep, splits, vzero):
     """dropkv_evict (selection fused into the scoring tail where the plan
