@@ -123,7 +123,7 @@ def pmc_summary(fetch_dir, write_dir, calib_fetch_dir, calib_write_dir, calib_mi
     sf, sw = true_kib / copy_f, true_kib / copy_w
     rows = {}
     for name, vals in fetch.items():
-        short = next((s for s in ("pass1", "pass2", "sel_pool", "sel_cand", "sel_emit", "compact")
+        short = next((s for s in ("pass1", "pass2", "merge", "sel_pool", "sel_cand", "sel_emit", "compact")
                       if s in name), None)
         if short is None:
             continue
