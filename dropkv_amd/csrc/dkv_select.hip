@@ -60,8 +60,6 @@ sel_cand_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
   const float* srow = scores + (int64_t)row * Lk;
   float* prow = ws.pooled + (int64_t)row * Lk;
   uint32_t* wsum = small;
-  int* s_bin = reinterpret_cast<int*>(small + 64);
-  uint32_t* s_above = small + 65;
 
   // One round trip: this chunk's pooled values (complete except the boundary
   // keys), the row's top-digit histogram and interior maximum, and the raw
@@ -115,15 +113,13 @@ sel_cand_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
   }
   const uint32_t gmax = block_max_u32(max(bmax, rmax), small + 96);
   const uint32_t kbig = float_key(key_float(gmax) + 1.0f);
-  if (tid == 0) {
-    hist[kbig >> kShift1] += (uint32_t)window;
-    *s_bin = 0;
-    *s_above = 0u;
-  }
+  if (tid == 0) hist[kbig >> kShift1] += (uint32_t)window;
   __syncthreads();
-  find_bin<kBins1, kSelT>(hist, (uint32_t)keep, s_bin, s_above, wsum);
-  const uint32_t b1 = (uint32_t)*s_bin;
-  const uint32_t k1 = (uint32_t)keep - *s_above;
+  uint32_t* fb = small + 64;  // wave_find_bin result
+  if (tid < 64) wave_find_bin<kBins1>(hist, nullptr, (uint32_t)keep, fb);
+  __syncthreads();
+  const uint32_t b1 = fb[0];
+  const uint32_t k1 = (uint32_t)keep - fb[1];
 
   // This chunk: the count above b1 and the candidates (keys in b1), which go
   // to the chunk's own region of the candidate arrays.  Boundary keys take
@@ -208,7 +204,7 @@ __device__ __forceinline__ uint32_t cand_global(const uint32_t* s_pref, int chun
 __global__ void __launch_bounds__(kSelT)
 sel_emit_kernel(int Lk, int window, int keep, int chunks, int spec, SelWs ws, int64_t* __restrict__ out_idx,
                 float* __restrict__ pooled_out, CompactArgs ca) {
-  __shared__ uint32_t hist[kBins2];  // digit-2, then digit-3 histogram
+  __shared__ uint32_t hist[kBins2 + kBins3];  // digit-2 and digit-3 histograms
   __shared__ uint32_t small[128];  // scan partials [0, 32), bin / counts at 64.., max at 96..
   __shared__ uint32_t lkey[kEmitCandLds];
   __shared__ uint32_t s_pref[kMaxChunks + 1];
@@ -218,8 +214,6 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, int spec, SelWs ws, in
   const int row = blockIdx.x / chunks;
   const int c = blockIdx.x % chunks;
   uint32_t* wsum = small;
-  int* s_bin = reinterpret_cast<int*>(small + 64);
-  uint32_t* s_above = small + 65;
   const uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
   const float* pooled = ws.pooled + (int64_t)row * Lk;
   const uint32_t* gkey = ws.cand_key + (int64_t)row * Lk;
@@ -337,39 +331,37 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, int spec, SelWs ws, in
       }
     }
   }
-  for (int i = tid; i < kBins2; i += kSelT) hist[i] = 0u;
-  if (tid == 0) {
-    *s_bin = 0;
-    *s_above = 0u;
-  }
+  uint32_t* hist2 = hist;
+  uint32_t* hist3 = hist + kBins2;
+  for (int i = tid; i < kBins2 + kBins3; i += kSelT) hist[i] = 0u;
   __syncthreads();
 
-  // Digit 2 (every candidate is in bin b1).
+  // Digit 2 (every candidate is in bin b1); the bin searches run on one wave.
+  uint32_t* fb = small + 64;
   for (uint32_t p = tid; p < nc; p += kSelT) {
     uint32_t kv;
     if (in_lds) kv = lkey[p];
     else kv = cand_global(s_pref, chunks, gkey, p);
-    atomicAdd(&hist[(kv >> kShift2) & (kBins2 - 1)], 1u);
+    atomicAdd(&hist2[(kv >> kShift2) & (kBins2 - 1)], 1u);
   }
   __syncthreads();
-  find_bin<kBins2, kSelT>(hist, k1, s_bin, s_above, wsum);
-  const uint32_t b2 = (uint32_t)*s_bin;
-  const uint32_t k2 = k1 - *s_above;
+  if (tid < 64) wave_find_bin<kBins2>(hist2, nullptr, k1, fb);
+  __syncthreads();
+  const uint32_t b2 = fb[0];
+  const uint32_t k2 = k1 - fb[1];
   const uint32_t pre = (b1 << kBits2) | b2;
-  __syncthreads();
-  for (int i = tid; i < kBins3; i += kSelT) hist[i] = 0u;
-  __syncthreads();
   // Digit 3 over the candidates matching the first two digits.
   for (uint32_t p = tid; p < nc; p += kSelT) {
     uint32_t kv;
     if (in_lds) kv = lkey[p];
     else kv = cand_global(s_pref, chunks, gkey, p);
-    if ((kv >> kShift2) == pre) atomicAdd(&hist[kv & (kBins3 - 1)], 1u);
+    if ((kv >> kShift2) == pre) atomicAdd(&hist3[kv & (kBins3 - 1)], 1u);
   }
   __syncthreads();
-  find_bin<kBins3, kSelT>(hist, k2, s_bin, s_above, wsum);
-  const uint32_t T = (pre << kBits3) | (uint32_t)*s_bin;
-  const uint32_t take_eq = k2 - *s_above;
+  if (tid < 64) wave_find_bin<kBins3>(hist3, nullptr, k2, fb + 4);
+  __syncthreads();
+  const uint32_t T = (pre << kBits3) | fb[4];
+  const uint32_t take_eq = k2 - fb[5];
 
   // Output offsets of this chunk: kept keys > T and keys == T in earlier
   // chunks (above-b1 keys per chunk, plus the candidates of those chunks,

@@ -185,6 +185,58 @@ __device__ void find_bin(const uint32_t* hist, uint32_t k, int* s_bin, uint32_t*
   __syncthreads();
 }
 
+// The same search done by one whole wave (no block barrier inside; the
+// caller brackets it with barriers).  For a second histogram he over the same
+// bins (optional), also its count in bins > b and in b.  Writes out[0..3] =
+// {b, count in bins > b, he count in bins > b, he[b]}.  Lane l first sums the
+// bins of its segment (NB/64 consecutive bins, lane order = descending bins;
+// the reads are rotated per lane so that a wave's reads hit distinct banks),
+// the lane holding the k-th key is found by a scan over lanes, and its
+// segment is then scanned one bin per lane.
+template <int NB>
+__device__ void wave_find_bin(const uint32_t* hist, const uint32_t* he, uint32_t k, uint32_t* out) {
+  constexpr int per = NB / 64;
+  static_assert(per >= 1 && per <= 64 && (per & (per - 1)) == 0, "NB/64 must be a power of two up to 64");
+  const int lane = threadIdx.x & 63;
+  const int top = NB - 1 - lane * per;
+  uint32_t th = 0u, te = 0u;
+#pragma unroll
+  for (int i = 0; i < per; ++i) {
+    const int b = top - ((i + lane) & (per - 1));
+    th += hist[b];
+    if (he) te += he[b];
+  }
+  uint32_t ih = th, ie = te;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t yh = (uint32_t)__shfl_up((int)ih, o), ye = (uint32_t)__shfl_up((int)ie, o);
+    if (lane >= o) {
+      ih += yh;
+      ie += ye;
+    }
+  }
+  const uint64_t hit = __ballot(ih - th < k && ih >= k);
+  const int lf = __ffsll((unsigned long long)hit) - 1;
+  const uint32_t run0 = (uint32_t)__shfl((int)(ih - th), lf), rune0 = (uint32_t)__shfl((int)(ie - te), lf);
+  const int b = NB - 1 - lf * per - lane;
+  const uint32_t hv = lane < per ? hist[b] : 0u, ev = (lane < per && he) ? he[b] : 0u;
+  uint32_t jh = hv, je = ev;
+#pragma unroll
+  for (int o = 1; o < per; o <<= 1) {
+    const uint32_t yh = (uint32_t)__shfl_up((int)jh, o), ye = (uint32_t)__shfl_up((int)je, o);
+    if (lane >= o) {
+      jh += yh;
+      je += ye;
+    }
+  }
+  if (lane < per && run0 + jh - hv < k && run0 + jh >= k) {
+    out[0] = (uint32_t)b;
+    out[1] = run0 + jh - hv;
+    out[2] = rune0 + je - ev;
+    out[3] = ev;
+  }
+}
+
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t x, uint32_t* red) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x = max(x, (uint32_t)__shfl_xor((int)x, o));
