@@ -355,113 +355,97 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 }
 
 // ---------------------------------------------------------------------------
-// Merge: one workgroup per (head, padded row).  The split weights
-// f_s = 2^(m_s - max_s m_s) go to LDS; thread (group, d) then sums the
-// weighted partial y rows of every G-th split, with many loads in flight.
-// Writes y as (hi, lo) element pairs for the score pass, the row statistics
-// (lse in log2 units, |y|^2) and an fp32 copy of y for inspection.  Optionally
-// clears `zero_words` words at `zero_ptr` (the selection workspace of a fused
-// layer-call), so that needs no launch of its own.
+// Merge: one wave per (head, padded row), kMergeRows rows per workgroup; no
+// workgroup barrier.  Lane l owns head-dim columns l*DPL .. +DPL-1 and split
+// l's statistics; the split weights f_s = 2^(m_s - max_s m_s) are broadcast
+// with lane shuffles and the weighted partial y rows summed with every load
+// in flight.  Writes, for the score pass, the row's Q / Y-hi / Y-lo operands
+// into the head's operand block (in the order pass 2's lanes read them from
+// LDS) and its statistics (lse in log2 units, |y|^2), plus an fp32 copy of y
+// for inspection.  Optionally clears `zero_words` words at `zero_ptr` (the
+// selection workspace of a fused layer-call), so that needs no launch of its
+// own.
 // ---------------------------------------------------------------------------
-constexpr int kMergeThreads = 256;
+constexpr int kMergeRows = 1;  // waves (rows) per workgroup
 constexpr int kMaxSplits = 1024;
 
-__device__ __forceinline__ float block_reduce(float x, float* red, bool is_max) {
-  x = is_max ? wave_max(x) : wave_sum(x);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = x;
-  __syncthreads();
-  float t = red[0];
-  for (int i = 1; i < (int)(blockDim.x >> 6); ++i) t = is_max ? fmaxf(t, red[i]) : t + red[i];
-  return t;
-}
-
 template <typename T, int D>
-__global__ void __launch_bounds__(kMergeThreads)
+__global__ void __launch_bounds__(64 * kMergeRows)
 merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y, int n_mc, int n_splits,
-             int M, int y_round, const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
-             int Hkv, int g, int W, int Lq, u32x4* __restrict__ opblk, float* __restrict__ stblk,
+             int M, int n_rows, int y_round, const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
+             int64_t q_sd, int Hkv, int g, int W, int Lq, u32x4* __restrict__ opblk, float* __restrict__ stblk,
              float* __restrict__ ystat, float* __restrict__ yf32, uint32_t* __restrict__ zero_ptr,
              int64_t zero_words) {
-  constexpr int G = kMergeThreads / D;
+  constexpr int DPL = D / 64;  // columns per lane
   constexpr int KK = D / 32;
   constexpr int OPS = 3 * kMB * KK;
-  __shared__ float s_f[kMaxSplits];
-  __shared__ float s_red[kMergeThreads / 64];
-  __shared__ float s_acc[G][D];
-  const int tid = threadIdx.x;
+  constexpr int kPre = 32;     // splits whose partial y is loaded up front
+  const int lane = threadIdx.x & 63;
   if (zero_ptr)
-    for (int64_t i = (int64_t)blockIdx.x * kMergeThreads + tid; i < zero_words;
-         i += (int64_t)gridDim.x * kMergeThreads)
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_words;
+         i += (int64_t)gridDim.x * blockDim.x)
       zero_ptr[i] = 0u;
 
   const int mpad = n_mc * kRows;
-  const int lid = xcd_remap(blockIdx.x, gridDim.x);  // a head's rows on the XCD that wrote its partials
-  const int head = lid / mpad;
-  const int gr = lid % mpad;
+  // (head, padded row); a head's rows on the XCD whose pass-1 workgroups
+  // wrote its partials (pass 1 maps heads to XCDs the same way).
+  const int rid = xcd_remap(blockIdx.x, gridDim.x) * kMergeRows + (threadIdx.x >> 6);
+  if (rid >= n_rows) return;
+  const int head = rid / mpad;
+  const int gr = rid % mpad;
   const int mc = gr / kRows, row = gr % kRows;
   const int64_t slot0 = ((int64_t)head * n_mc + mc) * n_splits;
+  const int d0 = lane * DPL;
 
-  // Issue every load up front: the partial y values of this thread's splits
-  // (the first kPre of them) and the per-split statistics.
-  const int d = tid % D, grp = tid / D;
-  const float* py = part_y + (slot0 * kRows + row) * D + d;
-  constexpr int kPre = 16;
-  float yv[kPre];
+  // Every load up front: the partial y columns of the first kPre splits, the
+  // query row and the per-split statistics.
+  typedef float fv __attribute__((ext_vector_type(DPL)));
+  const float* py = part_y + (slot0 * kRows + row) * D + d0;
+  fv yv[kPre];
 #pragma unroll
-  for (int i = 0; i < kPre; ++i) {
-    const int s = grp + i * G;
-    yv[i] = s < n_splits ? py[(int64_t)s * kRows * D] : 0.f;
-  }
-  // This row of the window queries, for the pass-2 operand block.
-  const bool qrow = gr < M && grp == 0;
-  T qv = static_cast<T>(0.f);
-  if (qrow) {
-    const int b = head / Hkv, hkv = head % Hkv, gi = gr / W, w = gr % W;
-    qv = q[(int64_t)b * q_sb + (int64_t)(hkv * g + gi) * q_sh + (int64_t)(Lq - W + w) * q_ss + (int64_t)d * q_sd];
-  }
-  // Split statistics (max, sum) in one pass: the sums are rescaled after the
-  // block maximum is known.
-  float mx = -INFINITY;
-  float2 ml_own[(kMaxSplits + kMergeThreads - 1) / kMergeThreads];
+  for (int s = 0; s < kPre; ++s)
+    yv[s] = s < n_splits ? *reinterpret_cast<const fv*>(py + (int64_t)s * kRows * D) : fv{};
+  T qv[DPL];
+  {
+    const bool valid = gr < M;
+    const int b = head / Hkv, hkv = head % Hkv, gi = valid ? gr / W : 0, w = valid ? gr % W : 0;
+    const T* qrow = q + (int64_t)b * q_sb + (int64_t)(hkv * g + gi) * q_sh + (int64_t)(Lq - W + w) * q_ss;
 #pragma unroll
-  for (int i = 0; i < (kMaxSplits + kMergeThreads - 1) / kMergeThreads; ++i) {
-    const int s = tid + i * kMergeThreads;
-    ml_own[i] = s < n_splits ? *reinterpret_cast<const float2*>(part_ml + ((slot0 + s) * kRows + row) * 2)
-                             : make_float2(-INFINITY, 0.f);
-    mx = fmaxf(mx, ml_own[i].x);
+    for (int e = 0; e < DPL; ++e) qv[e] = valid ? qrow[(int64_t)(d0 + e) * q_sd] : static_cast<T>(0.f);
   }
-  mx = block_reduce(mx, s_red, true);
-  float lpart = 0.f;
-#pragma unroll
-  for (int i = 0; i < (kMaxSplits + kMergeThreads - 1) / kMergeThreads; ++i) {
-    const int s = tid + i * kMergeThreads;
-    const float m = ml_own[i].x;
-    const float f = (m == -INFINITY || mx == -INFINITY) ? 0.f : exp2f(m - mx);
-    if (s < n_splits) s_f[s] = f;
-    lpart += ml_own[i].y * f;
-  }
-  const float l = block_reduce(lpart, s_red, false);  // also orders the s_f writes
+  // Split statistics: lane s holds (m, l) of split s (the first 64 in
+  // registers, any further ones re-read in the rare loops below).
+  const float2 ml = lane < n_splits ? *reinterpret_cast<const float2*>(part_ml + ((slot0 + lane) * kRows + row) * 2)
+                                    : make_float2(-INFINITY, 0.f);
+  float mx = ml.x;
+  for (int s = 64 + lane; s < n_splits; s += 64) mx = fmaxf(mx, part_ml[((slot0 + s) * kRows + row) * 2]);
+  mx = wave_max(mx);
+  auto weight = [&](float m) { return (m == -INFINITY || mx == -INFINITY) ? 0.f : exp2f(m - mx); };
+  const float f_lane = weight(ml.x);
+  float lpart = ml.y * f_lane;
+  for (int s = 64 + lane; s < n_splits; s += 64)
+    lpart += part_ml[((slot0 + s) * kRows + row) * 2 + 1] * weight(part_ml[((slot0 + s) * kRows + row) * 2]);
+  const float l = wave_sum(lpart);
 
-  float acc = 0.f;
+  // acc = sum_s f_s * y_s; lane s holds f_s of the first 64 splits.
+  fv acc = {};
 #pragma unroll
-  for (int i = 0; i < kPre; ++i) {
-    const int s = grp + i * G;
-    if (s < n_splits) acc += yv[i] * s_f[s];
+  for (int s = 0; s < kPre; ++s)
+    if (s < n_splits) acc += __shfl(f_lane, s) * yv[s];
+  for (int s = kPre; s < n_splits; ++s) {
+    const float fs = s < 64 ? __shfl(f_lane, s) : weight(part_ml[((slot0 + s) * kRows + row) * 2]);
+    acc += fs * *reinterpret_cast<const fv*>(py + (int64_t)s * kRows * D);
   }
-#pragma unroll 8
-  for (int s = grp + kPre * G; s < n_splits; s += G) acc += py[(int64_t)s * kRows * D] * s_f[s];
-  s_acc[grp][d] = acc;
-  __syncthreads();
 
   const bool valid = gr < M && mx != -INFINITY;
-  float y = 0.f;
-  if (grp == 0) {
-    float t = 0.f;
+  float ysq = 0.f;
+  const int64_t rbase = (int64_t)head * mpad + gr;
+  T* ob = reinterpret_cast<T*>(opblk + ((int64_t)head * n_mc + mc) * OPS * 64);
+  const int mb = row / 16, li = row % 16;
 #pragma unroll
-    for (int i = 0; i < G; ++i) t += s_acc[i][d];
-    y = valid ? t / l : 0.f;
+  for (int e = 0; e < DPL; ++e) {
+    const int d = d0 + e;
+    float y = valid ? acc[e] / l : 0.f;
     T hi, lo;
     if (y_round) {
       hi = static_cast<T>(y);
@@ -471,21 +455,19 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
       hi = static_cast<T>(y);
       lo = static_cast<T>(y - static_cast<float>(hi));
     }
-    const int64_t rbase = (int64_t)head * mpad + gr;
+    ysq += y * y;
     yf32[rbase * D + d] = y;
-    // Pass-2 operand block of this head: per row-chunk, the Q, Y-hi and Y-lo
-    // MFMA operands in per-lane order (slot (which, mb, kk), lane li + 16*lg,
-    // element e), so that pass 2 stages them with one contiguous copy.
-    const int mb = row / 16, li = row % 16, kk = d / 32, lg = (d % 32) / 8, e = d % 8;
-    T* ob = reinterpret_cast<T*>(opblk + ((int64_t)head * n_mc + mc) * OPS * 64);
+    // Operand block of this head: per row-chunk, the Q, Y-hi and Y-lo MFMA
+    // operands in per-lane order (slot (which, mb, kk), lane li + 16*lg,
+    // element e8), so that pass 2 stages them with one contiguous copy.
+    const int kk = d / 32, lg = (d % 32) / 8, e8 = d % 8;
     const int word = li + 16 * lg;
-    ob[((size_t)((0 * kMB + mb) * KK + kk) * 64 + word) * 8 + e] = qv;
-    ob[((size_t)((1 * kMB + mb) * KK + kk) * 64 + word) * 8 + e] = hi;
-    ob[((size_t)((2 * kMB + mb) * KK + kk) * 64 + word) * 8 + e] = lo;
+    ob[((size_t)((0 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = qv[e];
+    ob[((size_t)((1 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = hi;
+    ob[((size_t)((2 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = lo;
   }
-  const float yn2 = block_reduce(y * y, s_red, false);
-  if (tid == 0) {
-    const int64_t rbase = (int64_t)head * mpad + gr;
+  const float yn2 = wave_sum(ysq);
+  if (lane == 0) {
     const float lse2 = valid ? mx + log2f(fmaxf(l, 1e-40f)) : INFINITY;
     ystat[rbase * 2 + 0] = lse2;
     ystat[rbase * 2 + 1] = yn2;
@@ -847,9 +829,10 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
                        Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y);
   }
   timing_mark(st);
-  hipLaunchKernelGGL((merge_kernel<T, D>), dim3(p.heads * p.mpad), dim3(kMergeThreads), 0, st, part_ml, part_y,
-                     p.n_mc, p.s1, p.M, y_round, qq, q_sb, q_sh, q_ss, q_sd, Hkv, p.g, W, Lq, opblk, stblk,
-                     ystat, yf, zero_ptr, zero_words);
+  const int n_rows = p.heads * p.mpad;
+  hipLaunchKernelGGL((merge_kernel<T, D>), dim3((n_rows + kMergeRows - 1) / kMergeRows), dim3(64 * kMergeRows), 0, st,
+                     part_ml, part_y, p.n_mc, p.s1, p.M, n_rows, y_round, qq, q_sb, q_sh, q_ss, q_sd, Hkv, p.g, W, Lq,
+                     opblk, stblk, ystat, yf, zero_ptr, zero_words);
   timing_mark(st);
   SelFuse fz{};
   const int cg = min(p.n_mc, 2);
