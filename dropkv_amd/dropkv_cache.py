@@ -26,6 +26,7 @@ from typing import Any, Iterable, Optional
 import torch
 
 from . import ops
+from .hf_query import take_captured_query
 
 logger = logging.getLogger(__name__)
 
@@ -168,19 +169,33 @@ class DropKVCache(_LayerCache):
         return ops.compact(key_states, value_states, keep_idx)
 
     def update(self, query_states: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,
-               layer_idx: int, cache_kwargs: Optional[dict[str, Any]] = None):
-        """Same control flow as dropkv_cache.py:493-622."""
-        # HF 4-argument form: update(key, value, layer_idx, cache_kwargs).
-        if isinstance(value_states, int) and isinstance(layer_idx, dict):
-            cache_kwargs = layer_idx
+               layer_idx: Optional[int] = None, cache_kwargs: Optional[dict[str, Any]] = None):
+        """Same control flow as dropkv_cache.py:493-622.
+
+        Besides the native ``update(query, key, value, layer_idx)`` form, the
+        calls a Transformers model makes are recognised:
+        ``update(key, value, layer_idx, cache_kwargs)`` (4.x, the reference's
+        detection, dropkv_cache.py:505-516) and ``update(key, value,
+        layer_idx)`` (5.x).  In both the query comes from
+        ``cache_kwargs["query_states"]`` or, failing that, from the rotary
+        call recorded by :func:`dropkv_amd.hf_query.query_capture`."""
+        hf_call = isinstance(value_states, int) and (layer_idx is None or isinstance(layer_idx, dict))
+        if hf_call:
+            cache_kwargs = layer_idx if isinstance(layer_idx, dict) else cache_kwargs
             layer_idx = value_states
             value_states = key_states
             key_states = query_states
             query_states = cache_kwargs.get("query_states") if cache_kwargs else None
+            captured = take_captured_query()
+            if query_states is None:
+                query_states = captured
             if query_states is None:
                 logger.warning(
                     "DropKVCache.update() called without query_states — eviction disabled for this layer. "
-                    "Patch your transformers to pass query_states in cache_kwargs.")
+                    "Patch your transformers to pass query_states in cache_kwargs, or run the model inside "
+                    "dropkv_amd.hf_query.query_capture().")
+        elif layer_idx is None:
+            raise TypeError("update() missing required argument: 'layer_idx'")
 
         if layer_idx == 0:
             self._seen_tokens += key_states.shape[-2]
@@ -246,14 +261,30 @@ class DropKVCache(_LayerCache):
             return 0
         return self._seen_tokens
 
-    def get_mask_sizes(self, cache_position: torch.Tensor, layer_idx: int = 0) -> tuple[int, int]:
-        """(stored length + query length, 0) for the attention mask
-        (dropkv_cache.py:635-648)."""
-        query_length = cache_position.shape[0]
+    def _stored_length(self, layer_idx: int) -> int:
         empty = (len(self.key_cache) == 0 or len(self.key_cache) <= layer_idx
                  or not self.key_cache[layer_idx].numel())
-        stored = 0 if empty else self.key_cache[layer_idx].shape[-2]
-        return stored + query_length, 0
+        return 0 if empty else self.key_cache[layer_idx].shape[-2]
+
+    def get_mask_sizes(self, cache_position, layer_idx: int = 0) -> tuple[int, int]:
+        """(stored length + query length, 0) for the attention mask
+        (dropkv_cache.py:635-648).  The query length comes from a
+        ``cache_position`` tensor (Transformers 4.x, the reference's
+        convention) or as an int (5.x)."""
+        query_length = cache_position.shape[0] if isinstance(cache_position, torch.Tensor) else int(cache_position)
+        return self._stored_length(layer_idx) + query_length, 0
+
+    def get_query_offset(self, layer_idx: int = 0) -> int:
+        """Index of the step's first query in the stored-K/V frame of the mask
+        (Transformers 5.x asks for it separately from the RoPE length).
+
+        It is the stored length: the mask pairs query ``i`` with key column
+        ``kv`` iff ``kv <= offset + i``, so with the logical length (what the
+        reference's pinned Transformers used, through ``cache_position``) a
+        chunk that follows an eviction (``budget``, ``every_chunk``) would let
+        query ``i`` see up to ``_seen_tokens - stored`` later keys of its own
+        chunk."""
+        return self._stored_length(layer_idx)
 
 
 def prefill_chunked(model, input_ids, cache, chunk_size=4096, evict_strategy="last_chunk",

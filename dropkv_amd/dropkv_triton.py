@@ -40,32 +40,13 @@ def _compute_num_splits(B: int, Hkv: int, L: int, BLOCK_N: int, device) -> int:
     return max(1, min(wanted, max(1, total_tiles // 4), 64))
 
 
-def dropkv_scores_triton(
-    Q: torch.Tensor,
-    K: torch.Tensor,
-    V: torch.Tensor,
-    window_size: int = 8,
-    eps: float = 1e-6,
-    allow_tf32: bool = True,
-    match_pytorch_precision: bool = True,
-) -> torch.Tensor:
-    """DropKV eviction scores [B, Hkv, Lk] fp32 computed by the HIP kernels.
-
-    Q [B,Hq,Lq,D] (bf16/fp16, any strides; only the last ``window_size`` rows
-    are read), K/V [B,Hkv,Lk,D] contiguous, Lq <= Lk, the query being the
-    tail-aligned suffix of the keys.
-
-    ``match_pytorch_precision=True`` rounds the softmax probabilities to the
-    input dtype before ``w = (p/(1-p+eps))^2`` (dropkv_triton.py:584-587).
-    ``allow_tf32`` is accepted for compatibility and has no effect: gfx950 has
-    no TF32 matrix path; P.V and Y.V^T run as bf16/fp16 MFMAs with the fp32
-    operand split into two bf16/fp16 terms, which is at least as accurate.
-    """
+def check_scoring_inputs(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, window_size: int) -> None:
+    """The input contract of the fast scoring path, message for message as
+    dropkv_triton.py:680-716; raises ``AssertionError``."""
     B, Hq, Lq, D = Q.shape
     Hkv = K.shape[1]
     Lk = K.shape[2]
 
-    # Guards, message for message as dropkv_triton.py:680-716.
     assert isinstance(window_size, int) and window_size > 0, (
         f"window_size must be a positive int, got {window_size}"
     )
@@ -90,4 +71,27 @@ def dropkv_scores_triton(
     assert D & (D - 1) == 0, f"D ({D}) must be a power of 2"
     assert D in supported_head_dims(), f"D ({D}) is not compiled into the MI355X kernels"
 
+
+def dropkv_scores_triton(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    window_size: int = 8,
+    eps: float = 1e-6,
+    allow_tf32: bool = True,
+    match_pytorch_precision: bool = True,
+) -> torch.Tensor:
+    """DropKV eviction scores [B, Hkv, Lk] fp32 computed by the HIP kernels.
+
+    Q [B,Hq,Lq,D] (bf16/fp16, any strides; only the last ``window_size`` rows
+    are read), K/V [B,Hkv,Lk,D] contiguous, Lq <= Lk, the query being the
+    tail-aligned suffix of the keys.
+
+    ``match_pytorch_precision=True`` rounds the softmax probabilities to the
+    input dtype before ``w = (p/(1-p+eps))^2`` (dropkv_triton.py:584-587).
+    ``allow_tf32`` is accepted for compatibility and has no effect: gfx950 has
+    no TF32 matrix path; P.V and Y.V^T run as bf16/fp16 MFMAs with the fp32
+    operand split into two bf16/fp16 terms, which is at least as accurate.
+    """
+    check_scoring_inputs(Q, K, V, window_size)
     return ops.scores(Q, K, V, window_size, eps=eps, p_round=match_pytorch_precision, y_round=False)
