@@ -35,6 +35,7 @@ import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBPS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
 # kernels of one dropkv_evict call, in launch order: with the selection fused
 # into the scoring pass's tail, and with the standalone selection kernels
 STAGES_FUSED = ("pass1_partials", "merge", "pass2_scores_pool", "select_cand", "emit_compact")
@@ -50,7 +51,32 @@ WORKLOADS = {
                               k_scale=None),
     "chunk_4k_of_64k": dict(B=1, Hq=32, Hkv=8, D=128, Lq=4096, Lk=65536, window=8, kernel=11, ratio=0.1,
                             k_scale=None),
+    # BASELINE configs[4], long-context large-GQA stress: inputs drawn on the
+    # device (4.3 G query elements); parity and the CPU baseline use sampled
+    # (b, hkv) rows
+    "stress_b4_128k": dict(B=4, Hq=64, Hkv=8, D=128, Lq=131072, Lk=131072, window=32, kernel=11, ratio=0.05,
+                           k_scale="student_t3", gen="device"),
 }
+# (b, hkv) rows checked against / timed on the CPU oracle when a workload has
+# more rows than that is affordable for
+SAMPLE_ROWS = ((0, 0), (1, 3), (2, 5), (3, 7))
+
+
+def make_device_inputs(cfg, dev, seed=0):
+    """Q/K/V drawn with a seeded device generator: Q's last ``window`` rows
+    ~ N(0,1) (the only rows the path reads), the rest filled with zeros; V ~
+    N(0,1); K ~ Student-t(3) = Z / sqrt(chi2_3 / 3)."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    B, Hq, Hkv, D, Lq, Lk, W = (cfg[k] for k in ("B", "Hq", "Hkv", "D", "Lq", "Lk", "window"))
+    Q = torch.zeros(B, Hq, Lq, D, dtype=torch.bfloat16, device=dev)
+    Q[:, :, -W:] = torch.randn(B, Hq, W, D, generator=g, device=dev).to(torch.bfloat16)
+    z = torch.randn(B, Hkv, Lk, D, generator=g, device=dev)
+    chi2 = sum(torch.randn(B, Hkv, Lk, D, generator=g, device=dev) ** 2 for _ in range(3))
+    K = (z / torch.sqrt(chi2 / 3)).to(torch.bfloat16)
+    del z, chi2
+    V = torch.randn(B, Hkv, Lk, D, generator=g, device=dev).to(torch.bfloat16)
+    return Q, K, V
 
 
 def make_inputs(cfg, seed=0):
@@ -89,15 +115,25 @@ def cpu_baseline(Qt, K, V, cfg, min_seconds=10.0, max_reps=400):
     return statistics.median(times), n, len(times), sum(times)
 
 
-def parity(Qt, K, V, cfg, gpu_idx):
+def parity(Qt, K, V, cfg, gpu_idx, fp64=False):
     """Tie-aware overlap of the GPU selection with the oracle's (scores from
     dropkv_scores_reference(match_pytorch_precision=True), pool, protect,
-    top-k)."""
+    top-k); with ``fp64``, with the float64 arbiter's (the same formula in
+    float64 with the direct distance), which decides where the float32
+    reference is rounding noise (attention sinks)."""
     from oracle import dropkv_ref as R
-    ref_scores = R.dropkv_scores_reference(Qt, K, V, cfg["window"], match_pytorch_precision=True)
+    if fp64:
+        ref_scores = R.dropkv_scores_fp64(Qt, K, V, cfg["window"], p_round=torch_bf16())
+    else:
+        ref_scores = R.dropkv_scores_reference(Qt, K, V, cfg["window"], match_pytorch_precision=True)
     ref_idx, pooled = R.compute_keep_indices(Qt, K, V, cfg["ratio"], cfg["window"], cfg["kernel"],
                                              scores=ref_scores)
     return R.index_overlap(gpu_idx, ref_idx, pooled)
+
+
+def torch_bf16():
+    import torch
+    return torch.bfloat16
 
 
 def _read_counter_csvs(d):
@@ -195,8 +231,11 @@ def main():
     keep = min(Lk, max(int(cfg["ratio"] * Lk), W, 1))
     dev = torch.device("cuda:0")
     print(f"[bench] workload={args.workload} building inputs", file=sys.stderr, flush=True)
-    Q, K, V = make_inputs(cfg)
-    Qg, Kg, Vg = Q.to(dev), K.to(dev), V.to(dev)
+    if cfg.get("gen") == "device":
+        Qg, Kg, Vg = make_device_inputs(cfg, dev)
+    else:
+        Q, K, V = make_inputs(cfg)
+        Qg, Kg, Vg = Q.to(dev), K.to(dev), V.to(dev)
     plan = ops.EvictPlan(Qg, Kg, W, cfg["kernel"], keep, splits=args.splits)
 
     for _ in range(args.warmup):
@@ -254,6 +293,12 @@ def main():
     value = bytes_alg / (ms_per_step * 1e-3) / 1e9
     dom = max((s for s in STREAM_STAGES if s in kernel_us), key=lambda s: kernel_us[s])
     achieved = bytes_alg / (kernel_us[dom] * 1e-6) / 1e9
+    # Each stream kernel does two GEMM-equivalents of 2*M*D flop per key and
+    # head (QK^T and P.V in pass 1; QK^T and Y.V^T in pass 2): arithmetic
+    # intensity 2*M flop per K/V byte against the ridge peak_mfma / peak_hbm.
+    M = (Hq // Hkv) * W
+    flops_kernel = 4 * B * Hkv * M * D * Lk
+    mfma_bound = 2 * M > MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBPS * 1e9)
 
     traffic = None
     tfile = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
@@ -275,7 +320,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) Q/V, LogNormal-scaled K)",
+        "data": {"lognormal": "synthetic (seeded N(0,1) Q/V, LogNormal-scaled K)",
+                 "student_t3": "synthetic (seeded device N(0,1) Q tail/V, Student-t(3) K)"}.get(
+                     cfg["k_scale"], "synthetic (seeded N(0,1) Q/K/V)"),
         "config": {"workload": args.workload, "B": B, "Hq": Hq, "Hkv": Hkv, "D": D, "Lq": Lq, "Lk": Lk,
                    "window": W, "kernel_size": cfg["kernel"], "keep_ratio": cfg["ratio"], "keep": keep,
                    "parallelism": "single GPU"},
@@ -291,21 +338,53 @@ def main():
                      "bytes_per_launch": bytes_alg},
     }
 
-    Qt = Q[:, :, -W:, :].contiguous()  # only the tail is ever read
+    # Parity and CPU-baseline samples: the whole workload, or sampled (b, hkv)
+    # rows (each with its g query heads) where the workload is too large for
+    # the CPU oracle.
+    if cfg.get("gen") == "device":
+        g_h = Hq // Hkv
+        Qt_all = Qg[:, :, -W:].cpu()
+        samples = [(Qt_all[b:b + 1, h * g_h:(h + 1) * g_h].contiguous(), Kg[b:b + 1, h:h + 1].cpu(),
+                     Vg[b:b + 1, h:h + 1].cpu(), plan.keep_idx[b:b + 1, h:h + 1].cpu()) for b, h in SAMPLE_ROWS]
+        sample_desc = f"{len(samples)} sampled (b, hkv) rows {list(SAMPLE_ROWS)}"
+    else:
+        samples = [(Q[:, :, -W:, :].contiguous(), K, V, plan.keep_idx.cpu())]  # only the tail is ever read
+        sample_desc = f"all {B * Hkv} rows"
     if not args.no_parity:
         print("[bench] parity vs CPU oracle", file=sys.stderr, flush=True)
-        worst, unexcused = parity(Qt, K, V, cfg, plan.keep_idx.cpu())
+        worst, unexcused = 1.0, 0
+        for Qt, Ks, Vs, idx in samples:
+            w_, u_ = parity(Qt, Ks, Vs, cfg, idx)
+            worst, unexcused = min(worst, w_), unexcused + u_
         out["parity"] = {"min_row_overlap_tie_aware": round(worst, 6), "unexcused_index_diffs": unexcused,
-                         "rows": B * Hkv, "keep": keep}
+                         "rows": sample_desc, "keep": keep, "oracle": "dropkv_scores_reference (float32)"}
+        if cfg.get("gen") == "device":
+            worst, unexcused = 1.0, 0
+            for Qt, Ks, Vs, idx in samples:
+                w_, u_ = parity(Qt, Ks, Vs, cfg, idx, fp64=True)
+                worst, unexcused = min(worst, w_), unexcused + u_
+            out["parity"]["vs_fp64_arbiter"] = {"min_row_overlap_tie_aware": round(worst, 6),
+                                                "unexcused_index_diffs": unexcused}
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
-        t_cpu, n, reps, total = cpu_baseline(Qt, K, V, cfg, min_seconds=args.cpu_seconds)
-        out["cpu_baseline"] = {"value": round(bytes_alg / t_cpu / 1e9, 3), "unit": "GB/s", "cores": n,
-                               "kind": "port", "ms_per_layer_call": round(1e3 * t_cpu, 2),
-                               "sample": f"the full {args.workload} layer-call repeated {reps} times "
+        Qt, Ks, Vs, _ = samples[0]
+        t_cpu, n, reps, total = cpu_baseline(Qt, Ks, Vs, cfg, min_seconds=args.cpu_seconds)
+        sample_bytes = 2 * Ks.numel() * 2
+        what = (f"the full {args.workload} layer-call" if len(samples) == 1 and cfg.get("gen") != "device"
+                else f"one (b, hkv) row {SAMPLE_ROWS[0]} of {args.workload} ({sample_bytes} B of K/V)")
+        out["cpu_baseline"] = {"value": round(sample_bytes / t_cpu / 1e9, 3), "unit": "GB/s", "cores": n,
+                               "kind": "port", "ms_per_sample": round(1e3 * t_cpu, 2),
+                               "sample": f"{what} repeated {reps} times "
                                          f"({total:.1f} s, median reported) after 1 warm-up; deployed-path "
                                          "restatement (oracle): fallback score, max-pool, protect, top-k, sort, "
                                          "gather; torch CPU, Q tail only"}
+    if mfma_bound:
+        tflops = flops_kernel / (kernel_us[dom] * 1e-6) / 1e12
+        out["roofline"] = {"kernel": dom, "bound": "mfma", "achieved": round(tflops, 1),
+                           "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                           "traffic": traffic, "flops_per_launch": flops_kernel,
+                           "hbm": {"achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                                   "frac": round(achieved / HBM_PEAK_GBPS, 4), "bytes_per_launch": bytes_alg}}
     print(json.dumps(out), flush=True)
 
 

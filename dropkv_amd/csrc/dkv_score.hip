@@ -25,6 +25,7 @@
 #include "dkv_select_dev.h"
 
 #include <algorithm>
+#include <climits>
 #include <type_traits>
 #include <cstdio>
 #include <cstdlib>
@@ -35,6 +36,13 @@ namespace dkv {
 constexpr int kTile = 32;           // keys per wave tile
 constexpr int kRows = 32;           // query rows per row-chunk (2 MFMA row blocks)
 constexpr int kMB = kRows / 16;
+// The fp32 attention output y enters pass 2's G^T = V Y^T as three bf16/fp16
+// MFMA operands y = hi + mid + lo (each the rounded remainder of the one
+// before), which carry its 24 significant bits: dist2 = |v|^2 - 2<v,y> + |y|^2
+// cancels heavily where one key takes almost all of a row's attention, so
+// <v,y> needs the precision of the fp32 y it approximates.
+constexpr int kYParts = 3;
+constexpr int kOpSlots = 1 + kYParts;  // Q and the parts of Y, per row block and k-step
 constexpr int kPitch = 18;          // dwords per row of the transposed V tile
 
 
@@ -136,7 +144,8 @@ __global__ void __launch_bounds__(64 * WAVES, MINW)
 pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
              const T* __restrict__ kp, const T* __restrict__ vp,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int n_splits, int kps,
-             float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y) {
+             float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y,
+             int* __restrict__ part_arg) {
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
   constexpr int DT = D / 16;
@@ -147,7 +156,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 
   constexpr int kYPitch = D + 4;  // fp32 row pitch of the merge buffer
   constexpr int kLdsTiles = WAVES * D * kPitch;
-  constexpr int kLdsMerge = 3 * WAVES * kRows + WAVES * kRows * kYPitch;
+  constexpr int kLdsMerge = 4 * WAVES * kRows + WAVES * kRows * kYPitch;
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsTiles > kLdsMerge ? kLdsTiles : kLdsMerge];
 
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -182,11 +191,15 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   uint32_t* vt = lds + wv * D * kPitch;
 
   float m2[kMB], lsum[kMB];
+  // Per lane: the lowest of its keys that holds the row's running maximum
+  // (INT_MAX if none of this lane's keys does).
+  int acand[kMB];
   f32x4 yacc[DT][kMB];
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
     m2[mb] = -INFINITY;
     lsum[mb] = 0.f;
+    acand[mb] = INT_MAX;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -268,10 +281,21 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
         }
       lsum[mb] = lsum[mb] * alpha + psum;
       m2[mb] = mnew;
-      // Rescale only when some row's maximum moved (rare after a few tiles).
+      // Rescale only when some row's maximum moved (rare after a few tiles);
+      // then the lanes of a row whose maximum moved note which of their keys
+      // hold it.
       if (__any(alpha != 1.f)) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= alpha;
+        if (alpha != 1.f && !empty) {
+          int c = INT_MAX;
+#pragma unroll
+          for (int kb = 1; kb >= 0; --kb)
+#pragma unroll
+            for (int r = 3; r >= 0; --r)
+              c = s[kb][mb][r] == mnew ? t0 + 16 * kb + 4 * lg + r : c;
+          acand[mb] = c;
+        }
       }
     }
 
@@ -313,12 +337,20 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   float* sm_m = reinterpret_cast<float*>(lds);
   float* sm_l = sm_m + WAVES * kRows;
   float* sm_f = sm_l + WAVES * kRows;
-  float* wbuf = sm_f + WAVES * kRows;  // [WAVES][kRows][kYPitch]
+  int* sm_a = reinterpret_cast<int*>(sm_f + WAVES * kRows);
+  float* wbuf = sm_f + 2 * WAVES * kRows;  // [WAVES][kRows][kYPitch]
+  // Key of each row's maximum: the lowest candidate over the lane groups.
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    acand[mb] = min(acand[mb], __shfl_xor(acand[mb], 16));
+    acand[mb] = min(acand[mb], __shfl_xor(acand[mb], 32));
+  }
   if (lg == 0) {
 #pragma unroll
     for (int mb = 0; mb < kMB; ++mb) {
       sm_m[wv * kRows + 16 * mb + li] = m2[mb];
       sm_l[wv * kRows + 16 * mb + li] = lsum[mb];
+      sm_a[wv * kRows + 16 * mb + li] = acand[mb] == INT_MAX ? -1 : acand[mb];
     }
   }
 #pragma unroll
@@ -332,7 +364,15 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   if (threadIdx.x < kRows) {
     const int row = threadIdx.x;
     float mx = -INFINITY;
-    for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, sm_m[w * kRows + row]);
+    int arg = -1;
+    for (int w = 0; w < WAVES; ++w) {
+      const float mw = sm_m[w * kRows + row];
+      if (mw > mx) {
+        mx = mw;
+        arg = sm_a[w * kRows + row];
+      }
+    }
+    part_arg[slot * kRows + row] = arg;
     float l = 0.f;
     for (int w = 0; w < WAVES; ++w) {
       const float mw = sm_m[w * kRows + row];
@@ -359,7 +399,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 // workgroup barrier.  Lane l owns head-dim columns l*DPL .. +DPL-1 and split
 // l's statistics; the split weights f_s = 2^(m_s - max_s m_s) are broadcast
 // with lane shuffles and the weighted partial y rows summed with every load
-// in flight.  Writes, for the score pass, the row's Q / Y-hi / Y-lo operands
+// in flight.  Writes, for the score pass, the row's Q / Y-hi / Y-mid / Y-lo operands
 // into the head's operand block (in the order pass 2's lanes read them from
 // LDS) and its statistics (lse in log2 units, |y|^2), plus an fp32 copy of y
 // for inspection.  Optionally clears `zero_words` words at `zero_ptr` (the
@@ -371,14 +411,15 @@ constexpr int kMaxSplits = 1024;
 
 template <typename T, int D>
 __global__ void __launch_bounds__(64 * kMergeRows)
-merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y, int n_mc, int n_splits,
-             int M, int n_rows, int y_round, const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
-             int64_t q_sd, int Hkv, int g, int W, int Lq, u32x4* __restrict__ opblk, float* __restrict__ stblk,
+merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y, const int* __restrict__ part_arg,
+             int n_mc, int n_splits, int M, int n_rows, int p_round, int y_round, const T* __restrict__ q,
+             int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const T* __restrict__ vp, int Lk,
+             int Hkv, int g, int W, int Lq, u32x4* __restrict__ opblk, float* __restrict__ stblk,
              float* __restrict__ ystat, float* __restrict__ yf32, uint32_t* __restrict__ zero_ptr,
              int64_t zero_words) {
   constexpr int DPL = D / 64;  // columns per lane
   constexpr int KK = D / 32;
-  constexpr int OPS = 3 * kMB * KK;
+  constexpr int OPS = kOpSlots * kMB * KK;
   constexpr int kPre = 32;     // splits whose partial y is loaded up front
   const int lane = threadIdx.x & 63;
   if (zero_ptr)
@@ -417,15 +458,54 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   // registers, any further ones re-read in the rare loops below).
   const float2 ml = lane < n_splits ? *reinterpret_cast<const float2*>(part_ml + ((slot0 + lane) * kRows + row) * 2)
                                     : make_float2(-INFINITY, 0.f);
+  const int arg_lane = (p_round && lane < n_splits) ? part_arg[(slot0 + lane) * kRows + row] : -1;
   float mx = ml.x;
   for (int s = 64 + lane; s < n_splits; s += 64) mx = fmaxf(mx, part_ml[((slot0 + s) * kRows + row) * 2]);
   mx = wave_max(mx);
+  const bool valid = gr < M && mx != -INFINITY;
+
   auto weight = [&](float m) { return (m == -INFINITY || mx == -INFINITY) ? 0.f : exp2f(m - mx); };
   const float f_lane = weight(ml.x);
   float lpart = ml.y * f_lane;
   for (int s = 64 + lane; s < n_splits; s += 64)
     lpart += part_ml[((slot0 + s) * kRows + row) * 2 + 1] * weight(part_ml[((slot0 + s) * kRows + row) * 2]);
   const float l = wave_sum(lpart);
+  const float lse2 = mx + log2f(fmaxf(l, 1e-40f));
+
+  // y from the probabilities rounded to the input dtype (the reference's
+  // semantics with p rounding, dropkv_triton.py:88-93).  Pass 1 summed the
+  // unrounded p; adding (round(p_k) - p_k) v_k for the row's top key k makes
+  // up the part that matters.  Every key's rounding error is at most 2^-9 of
+  // its p, so the others move y by at most 2^-9 (1 - p_k) |v|, a relative
+  // error below 1e-3 in every distance.  The top key's own term matters
+  // because |v_k - y| shrinks with 1 - p_k: without it, dist2 at that key is
+  // wrong by up to tens of percent once p_k approaches 1.  Below p_k = 1/2
+  // the term changes no distance by more than 0.5%, and the row skips the
+  // dependent load of v_k.
+  int k_top = -1;
+  float dk = 0.f;
+  fv vk = {};
+  if (p_round && valid) {
+    const float pk = fminf(__builtin_amdgcn_exp2f(mx - lse2), 1.f);
+    if (pk >= 0.5f) {
+      const uint64_t hit = __ballot(lane < n_splits && ml.x == mx);
+      if (hit) {
+        k_top = __shfl(arg_lane, __builtin_ctzll(hit));
+      } else {
+        for (int s = 64; s < n_splits; ++s)
+          if (part_ml[((slot0 + s) * kRows + row) * 2] == mx) {
+            k_top = part_arg[(slot0 + s) * kRows + row];
+            break;
+          }
+      }
+      if (k_top >= 0 && k_top < Lk) {
+        dk = round_through<T>(pk) - pk;
+        const T* vrow = vp + ((int64_t)head * Lk + k_top) * D + d0;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) vk[e] = static_cast<float>(vrow[e]);
+      }
+    }
+  }
 
   // acc = sum_s f_s * y_s; lane s holds f_s of the first 64 splits.
   fv acc = {};
@@ -437,7 +517,6 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
     acc += fs * *reinterpret_cast<const fv*>(py + (int64_t)s * kRows * D);
   }
 
-  const bool valid = gr < M && mx != -INFINITY;
   float ysq = 0.f;
   const int64_t rbase = (int64_t)head * mpad + gr;
   T* ob = reinterpret_cast<T*>(opblk + ((int64_t)head * n_mc + mc) * OPS * 64);
@@ -445,34 +524,38 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
 #pragma unroll
   for (int e = 0; e < DPL; ++e) {
     const int d = d0 + e;
-    float y = valid ? acc[e] / l : 0.f;
-    T hi, lo;
+    float y = valid ? acc[e] / l + dk * vk[e] : 0.f;
+    T hi, mid, lo;
     if (y_round) {
       hi = static_cast<T>(y);
       y = static_cast<float>(hi);
+      mid = static_cast<T>(0.f);
       lo = static_cast<T>(0.f);
     } else {
       hi = static_cast<T>(y);
-      lo = static_cast<T>(y - static_cast<float>(hi));
+      const float r1 = y - static_cast<float>(hi);
+      mid = static_cast<T>(r1);
+      lo = static_cast<T>(r1 - static_cast<float>(mid));
     }
     ysq += y * y;
     yf32[rbase * D + d] = y;
-    // Operand block of this head: per row-chunk, the Q, Y-hi and Y-lo MFMA
-    // operands in per-lane order (slot (which, mb, kk), lane li + 16*lg,
+    // Operand block of this head: per row-chunk, the Q, Y-hi, Y-mid and Y-lo
+    // MFMA operands in per-lane order (slot (which, mb, kk), lane li + 16*lg,
     // element e8), so that pass 2 stages them with one contiguous copy.
     const int kk = d / 32, lg = (d % 32) / 8, e8 = d % 8;
     const int word = li + 16 * lg;
     ob[((size_t)((0 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = qv[e];
     ob[((size_t)((1 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = hi;
-    ob[((size_t)((2 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = lo;
+    ob[((size_t)((2 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = mid;
+    ob[((size_t)((3 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = lo;
   }
   const float yn2 = wave_sum(ysq);
   if (lane == 0) {
-    const float lse2 = valid ? mx + log2f(fmaxf(l, 1e-40f)) : INFINITY;
-    ystat[rbase * 2 + 0] = lse2;
+    const float lse_row = valid ? lse2 : INFINITY;
+    ystat[rbase * 2 + 0] = lse_row;
     ystat[rbase * 2 + 1] = yn2;
     float* sb = stblk + ((int64_t)head * n_mc + mc) * kMB * 32 + (row / 16) * 32 + (row % 16);
-    sb[0] = lse2;
+    sb[0] = lse_row;
     sb[16] = yn2;
   }
 }
@@ -480,7 +563,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
 // ---------------------------------------------------------------------------
 // Pass 2: per-key score.  Workgroup = (head, key split); each of its WAVES
 // waves streams 32-key tiles, recomputes S^T = K Q^T and G^T = V Y^T (Y as
-// hi+lo) and folds w * dist2 over all query rows.  The next tile's loads are
+// hi+mid+lo) and folds w * dist2 over all query rows.  The next tile's loads are
 // issued right after the last MFMA of the current tile, overlapping the
 // per-element work.  The Q^T / Y^T operands of up to `cg` row-chunks are
 // staged in LDS in per-lane order (one conflict-free 16-byte read per
@@ -539,7 +622,7 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
              SelFuse fz) {
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
-  constexpr int OPS = 3 * kMB * KK;  // operand slots per row-chunk (Q, Yhi, Ylo)
+  constexpr int OPS = kOpSlots * kMB * KK;  // operand slots per row-chunk (Q, Yhi, Ymid, Ylo)
   constexpr int NT = 64 * WAVES;
   extern __shared__ u32x4 opnd[];    // [cg][OPS][64] then float stats [cg][kMB][2][16]
   float* stat = reinterpret_cast<float*>(opnd + (size_t)cg * OPS * 64);
@@ -641,11 +724,13 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
           for (int kk = 0; kk < KK; ++kk) {
             const v8 qo = __builtin_bit_cast(v8, ob[(size_t)((0 * kMB + mb) * KK + kk) * 64]);
             const v8 yh = __builtin_bit_cast(v8, ob[(size_t)((1 * kMB + mb) * KK + kk) * 64]);
-            const v8 yl = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
+            const v8 ym = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
+            const v8 yl = __builtin_bit_cast(v8, ob[(size_t)((3 * kMB + mb) * KK + kk) * 64]);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
               sacc[kb][mb] = Elem<T>::mfma(kop[kb][kk], qo, sacc[kb][mb]);
               gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], yh, gacc[kb][mb]);
+              gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], ym, gacc[kb][mb]);
               gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], yl, gacc[kb][mb]);
             }
           }
@@ -791,7 +876,8 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   const size_t slots = (size_t)p.heads * p.n_mc * p.s1;
   p.off_ml = take(slots * kRows * 2 * sizeof(float));
   p.off_y = take(slots * kRows * D * sizeof(float));
-  p.off_op = take((size_t)p.heads * p.n_mc * 3 * kMB * (D / 32) * 64 * 16);
+  p.off_arg = take(slots * kRows * sizeof(int));
+  p.off_op = take((size_t)p.heads * p.n_mc * kOpSlots * kMB * (D / 32) * 64 * 16);
   p.off_stb = take((size_t)p.heads * p.n_mc * kMB * 32 * sizeof(float));
   p.off_stat = take((size_t)p.heads * p.mpad * 2 * sizeof(float));
   p.off_yf = take((size_t)p.heads * p.mpad * D * sizeof(float));
@@ -811,6 +897,7 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   float* stblk = reinterpret_cast<float*>(ws + p.off_stb);
   float* ystat = reinterpret_cast<float*>(ws + p.off_stat);
   float* yf = reinterpret_cast<float*>(ws + p.off_yf);
+  int* part_arg = reinterpret_cast<int*>(ws + p.off_arg);
   const T* qq = static_cast<const T*>(q);
   const T* kk = static_cast<const T*>(k);
   const T* vv = static_cast<const T*>(v);
@@ -820,23 +907,23 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   const dim3 g1(p.heads * p.n_mc * p.s1);
   if (p.p1_waves == 8) {
     hipLaunchKernelGGL((pass1_kernel<T, D, 8, 1>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y);
+                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
   } else if (p.p1_occ == 1) {
     hipLaunchKernelGGL((pass1_kernel<T, D, 4, 1>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y);
+                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
   } else {
     hipLaunchKernelGGL((pass1_kernel<T, D, 4, 2>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y);
+                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
   }
   timing_mark(st);
   const int n_rows = p.heads * p.mpad;
   hipLaunchKernelGGL((merge_kernel<T, D>), dim3((n_rows + kMergeRows - 1) / kMergeRows), dim3(64 * kMergeRows), 0, st,
-                     part_ml, part_y, p.n_mc, p.s1, p.M, n_rows, y_round, qq, q_sb, q_sh, q_ss, q_sd, Hkv, p.g, W, Lq,
-                     opblk, stblk, ystat, yf, zero_ptr, zero_words);
+                     part_ml, part_y, part_arg, p.n_mc, p.s1, p.M, n_rows, p_round, y_round, qq, q_sb, q_sh, q_ss,
+                     q_sd, vv, Lk, Hkv, p.g, W, Lq, opblk, stblk, ystat, yf, zero_ptr, zero_words);
   timing_mark(st);
   SelFuse fz{};
   const int cg = min(p.n_mc, 2);
-  size_t lds2 = (size_t)cg * 3 * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
+  size_t lds2 = (size_t)cg * kOpSlots * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
   if (fuse) {
     fz.enabled = 1;
     fz.ws = sel_layout(fuse->ws, p.heads, Lk, nullptr);

@@ -22,6 +22,9 @@ live in ``tests/test_oracle.py``, the fixtures in ``tests/golden/``):
   tail is read, scores >= 0.  ``eps`` is pinned only by presence: the Lk == W
   case (p = 1) stays finite; its value is below the float32 resolution of the
   reference's own expansion wherever that expansion is accurate.
+* ``dropkv_scores_fp64`` (float64 arbiter of selections) -- the per-(b, hkv,
+  gi, w) float64 brute force of ``tests/test_oracle.py``, with and without
+  the bf16 rounding of p, to float64 rounding.
 * ``fallback_scores`` (deployed ``use_triton=False`` path) -- float64 brute
   force with round-to-nearest-even of p and y to bf16; golden fixtures
   (including a final chunk shorter than the window); the reference tests'
@@ -112,6 +115,74 @@ def dropkv_scores_reference(
             scores[:, hkv:hkv + 1] += termA - termB + termC
     scores /= g
     return scores
+
+
+def dropkv_scores_fp64(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    window_size: int = 8,
+    eps: float = 1e-6,
+    p_round: Optional[torch.dtype] = None,
+    p_scale: float = 1.0,
+    keys: Optional[torch.Tensor] = None,
+    return_bound: bool = False,
+):
+    """The score of ``dropkv_scores_reference`` evaluated in float64 with the
+    direct distance ``||v_j - y_m||^2`` instead of the float32 expansion
+    termA - termB + termC (dropkv_triton.py:96-106); ``p_round`` rounds p to
+    that dtype before the weight and before y (the
+    ``match_pytorch_precision`` semantics, :88-93).  Returns float64
+    [B, Hkv, Lk], or [B, Hkv, len(keys)] for the key indices ``keys`` only.
+
+    Used as the arbiter of selections where the float32 reference is not
+    decisive: with p rounded to bf16, a last-bit difference in a logit can
+    move p to the neighbouring bf16 value (w changes by about 2^-7, and by far
+    more where p is close to 1), so two float32 evaluations of the same
+    formula can rank keys near the keep threshold differently.  The float64
+    evaluation rounds p from a p that is exact to float32 precision.
+    ``p_scale`` multiplies p before that rounding: a probe of how far a score
+    moves when p is off by a few float32 ulps.
+
+    ``return_bound`` also returns, per key, the scale of the rounding error
+    of any float32 evaluation through the expansion:
+    ``sum_m w * (|v|^2 + 2|<v,y>| + |y|^2) * 2^-24 / g``.  Where one key takes
+    almost all of a row's attention, w reaches 1e12 and this bound exceeds
+    the score itself: no float32 expansion determines such a score."""
+    B, Hq, Lq, D = Q.shape
+    Hkv, Lk = K.shape[1], K.shape[2]
+    g = Hq // Hkv
+    W = window_size
+    Qt = Q[:, :, -W:, :].double()
+    Kd, Vd = K.double(), V.double()
+    sel = torch.arange(Lk) if keys is None else keys.to(torch.int64)
+    out = torch.zeros(B, Hkv, sel.numel(), dtype=torch.float64)
+    bound = torch.zeros_like(out)
+    mask = torch.triu(torch.full((W, Lk), float("-inf"), dtype=torch.float64), diagonal=Lk - W + 1)
+    for hkv in range(Hkv):
+        Kh, Vh = Kd[:, hkv], Vd[:, hkv]                      # [B, Lk, D]
+        Vs = Vh[:, sel]                                      # [B, n, D]
+        vn2 = (Vs ** 2).sum(-1)                              # [B, n]
+        for gi in range(g):
+            q = Qt[:, hkv * g + gi]                          # [B, W, D]
+            p = torch.softmax(q @ Kh.transpose(-1, -2) / math.sqrt(D) + mask, dim=-1)   # [B, W, Lk]
+            if p_scale != 1.0:
+                p = p * p_scale
+            if p_round is not None:
+                p = p.to(p_round).double()
+            y = p @ Vh                                       # [B, W, D]
+            ps = p[:, :, sel]
+            wt = (ps / (1.0 - ps + eps)) ** 2
+            for w in range(W):
+                d2 = ((Vs - y[:, w:w + 1]) ** 2).sum(-1)     # [B, n]
+                out[:, hkv] += wt[:, w] * d2
+                if return_bound:
+                    yw = y[:, w]                             # [B, D]
+                    mag = vn2 + 2.0 * (Vs @ yw.unsqueeze(-1)).squeeze(-1).abs() + (yw ** 2).sum(-1, keepdim=True)
+                    bound[:, hkv] += wt[:, w] * mag
+    if return_bound:
+        return out / g, bound * 2.0 ** -24 / g
+    return out / g
 
 
 # ---------------------------------------------------------------------------

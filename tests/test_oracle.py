@@ -101,6 +101,35 @@ def test_reference_bf16_mode_vs_bruteforce(shape):
     assert (rel > 1e-4).double().mean() < 0.03
 
 
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("p_round", [None, torch.bfloat16])
+def test_fp64_arbiter_vs_bruteforce(shape, p_round):
+    """The vectorised float64 evaluation equals the per-(b, hkv, gi, w)
+    brute force to float64 rounding."""
+    B, Hq, Hkv, D, Lq, Lk, W = shape
+    cfg = dict(B=B, Hq=Hq, Hkv=Hkv, D=D)
+    Q, K, V = make_qkv(cfg, Lq, Lk, dtype=torch.bfloat16, seed=7 + sum(shape))
+    got = R.dropkv_scores_fp64(Q, K, V, W, p_round=p_round)
+    ref = brute_fp64(Q, K, V, W, p_round=p_round)
+    assert got.dtype == torch.float64
+    assert_rel(got, ref, 1e-12)
+    keys = torch.tensor([0, Lk // 2, Lk - 1])
+    assert torch.equal(R.dropkv_scores_fp64(Q, K, V, W, p_round=p_round, keys=keys), got[..., keys])
+
+
+def test_fp64_arbiter_rounding_bound():
+    """The float32-expansion rounding bound is negligible for diffuse
+    attention and exceeds the score at an attention sink (p rounds to 1)."""
+    cfg = dict(B=1, Hq=2, Hkv=1, D=32)
+    Q, K, V = make_qkv(cfg, 64, 64, dtype=torch.bfloat16, seed=3)
+    s, bnd = R.dropkv_scores_fp64(Q, K, V, 8, p_round=torch.bfloat16, return_bound=True)
+    assert (bnd >= 0).all() and (bnd / s).max() < 1e-4
+    K = K.clone()
+    K[0, 0, 20] = (Q[0, 0, -1].float() * 4).to(torch.bfloat16)   # key 20 takes the last row's attention
+    s, bnd = R.dropkv_scores_fp64(Q, K, V, 8, p_round=torch.bfloat16, return_bound=True)
+    assert bnd[0, 0, 20] > s[0, 0, 20]
+
+
 @pytest.mark.parametrize("shape", SHAPES[:3] + [(1, 4, 2, 32, 3, 40, 8)])
 def test_fallback_vs_bruteforce(shape):
     """Deployed path: W = min(window, Lq), p and y rounded to the input dtype
