@@ -139,7 +139,7 @@ __device__ __forceinline__ void load_v_pairs(u32x4 (&va)[(kTile / 2) / (64 / (D 
 // end.  Output per (head, chunk, split, row): running max (log2 domain),
 // running sum, and the unnormalised fp32 y row.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int WAVES, int MINW>
+template <typename T, int D, int WAVES, int MINW, int PS>
 __global__ void __launch_bounds__(64 * WAVES, MINW)
 pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
              const T* __restrict__ kp, const T* __restrict__ vp,
@@ -248,7 +248,10 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     load_rows_op<T, D>(kop, krs, k_lane, tn);
     load_v_pairs<T, D>(va, vb, vrs, v_lane, tn);
 
-    // Online softmax (base 2) for each row block; P hi/lo split for the MFMA.
+    // Online softmax (base 2) for each row block.  P enters the MFMA as PS
+    // parts: one when the scores use p rounded to the input dtype (y is then
+    // only needed to that precision, see the merge kernel), hi + lo for the
+    // fp32 semantics.
     const bool masked = pad_chunk || t0 + kTile > unmasked_end;
     v8 phi[kMB], plo[kMB];
 #pragma unroll
@@ -277,7 +280,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
           psum += pv;
           const T h = static_cast<T>(pv);
           phi[mb][4 * kb + r] = h;
-          plo[mb][4 * kb + r] = static_cast<T>(pv - static_cast<float>(h));
+          if constexpr (PS == 2) plo[mb][4 * kb + r] = static_cast<T>(pv - static_cast<float>(h));
         }
       lsum[mb] = lsum[mb] * alpha + psum;
       m2[mb] = mnew;
@@ -310,7 +313,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 #pragma unroll
       for (int mb = 0; mb < kMB; ++mb) {
         yacc[dt][mb] = Elem<T>::mfma(aop, phi[mb], yacc[dt][mb]);
-        yacc[dt][mb] = Elem<T>::mfma(aop, plo[mb], yacc[dt][mb]);
+        if constexpr (PS == 2) yacc[dt][mb] = Elem<T>::mfma(aop, plo[mb], yacc[dt][mb]);
       }
     }
   };
@@ -391,6 +394,239 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) y += wbuf[((size_t)w * kRows + row) * kYPitch + d] * sm_f[w * kRows + row];
     py[i] = y;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1 for several row-chunks (n_mc >= 2: large GQA groups or windows).
+// Workgroup = (head, key split) with 8 waves; wave w owns row-chunk w (waves
+// past n_mc only load).  Each 32-key K/V tile is loaded once per workgroup,
+// cooperatively, into LDS (K rows padded, V transposed), and every wave
+// applies it to its own rows.  With one workgroup per row-chunk instead,
+// every tile would be streamed n_mc times.  Tiles move in groups of kWideG:
+// the loads of the next group are in flight (in registers) while the waves
+// work on the current one, double-buffered in LDS with one barrier per group,
+// so that ~64 KB per CU are on their way at any time (one tile in flight
+// does not cover the memory latency).
+// Writes the same per-(head, chunk, split, row) partials as pass1_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kWideWaves = 8;
+
+template <typename T, int D, int PS, int kWideG>
+__global__ void __launch_bounds__(64 * kWideWaves, 1)
+pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
+              const T* __restrict__ kp, const T* __restrict__ vp,
+              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int n_splits, int kps,
+              float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y,
+              int* __restrict__ part_arg) {
+  typedef typename Elem<T>::v8 v8;
+  constexpr int KK = D / 32;
+  constexpr int DT = D / 16;
+  constexpr int NT = 64 * kWideWaves;
+  constexpr int CPR = D / 8;                 // 16-byte chunks per key row
+  constexpr int KCH = kTile * CPR;           // K chunks per tile
+  constexpr int VPR = (kTile / 2) * CPR;     // (key pair, chunk) items of V per tile
+  static_assert(KCH <= NT && VPR <= NT, "one K chunk and one V pair per thread");
+  constexpr int kKPitch = D + 8;             // elements per padded K row in LDS
+  constexpr int kKWords = kTile * kKPitch / 2;
+  constexpr int kVWords = D * kPitch;
+  constexpr int kTileWords = kKWords + kVWords;
+  constexpr int kStage = kWideG * kTileWords;  // dwords per buffer stage
+  __shared__ __attribute__((aligned(16))) uint32_t lds[2 * kStage];
+
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int split = lid % n_splits;
+  const int head = lid / n_splits;
+  const int b = head / Hkv, hkv = head % Hkv;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wv = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int mc = wv;
+  const bool active = mc < n_mc;
+
+  v8 qop[kMB][KK];
+  int bound[kMB];
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    const int m = mc * kRows + mb * 16 + li;
+    load_q_ops<T, D>(qop[mb], q, q_sb, q_sh, q_ss, q_sd, qvec, b, hkv, g, W, Lq, M, m, lg);
+    bound[mb] = row_bound(m, M, W, Lk);
+  }
+  const bool pad_chunk = mc * kRows + kRows > M;
+  const int unmasked_end = Lk - W + 1;
+
+  const int k_begin = split * kps;
+  const int k_end = min(k_begin + kps, Lk);
+  const int64_t roff = ((int64_t)head * Lk + k_begin) * D;
+  const uint32_t range = (uint32_t)(k_end - k_begin) * (D * sizeof(T));
+  const rsrc_t krs = make_rsrc(kp + roff, range), vrs = make_rsrc(vp + roff, range);
+  // This thread's share of a tile: K chunk tid (row tid / CPR, chunk tid % CPR)
+  // and V pair item tid (keys 2p, 2p+1, chunk c).
+  const int kr = tid / CPR, kc = tid % CPR;
+  const int vpi = tid / CPR, vc = tid % CPR;
+  const uint32_t k_off = (uint32_t)(kr * D + 8 * kc) * sizeof(T);
+  const uint32_t v_off = (uint32_t)(2 * vpi * D + 8 * vc) * sizeof(T);
+  u32x4 kreg[kWideG], va[kWideG], vb[kWideG];
+  // Loads of tile group grp (rows past the range read as zeros).
+  auto issue = [&](int grp) __attribute__((always_inline)) {
+#pragma unroll
+    for (int gt = 0; gt < kWideG; ++gt) {
+      const uint32_t base = (uint32_t)((grp * kWideG + gt) * kTile) * (D * sizeof(T));
+      if (tid < KCH) kreg[gt] = buf_load16(krs, base + k_off);
+      if (tid < VPR) {
+        va[gt] = buf_load16(vrs, base + v_off);
+        vb[gt] = buf_load16(vrs, base + v_off + D * sizeof(T));
+      }
+    }
+  };
+  auto stage = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int gt = 0; gt < kWideG; ++gt) {
+      uint32_t* kl = lds + buf * kStage + gt * kTileWords;
+      uint32_t* vt = kl + kKWords;
+      if (tid < KCH) *reinterpret_cast<u32x4*>(kl + (kr * kKPitch + 8 * kc) / 2) = kreg[gt];
+      if (tid < VPR) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t lo = __builtin_amdgcn_perm(vb[gt][j], va[gt][j], 0x05040100u);
+          const uint32_t hi = __builtin_amdgcn_perm(vb[gt][j], va[gt][j], 0x07060302u);
+          const int d0 = 8 * vc + 2 * j, d1 = d0 + 1;
+          vt[d0 * kPitch + (vpi ^ (4 * ((d0 >> 4) & 3)))] = lo;
+          vt[d1 * kPitch + (vpi ^ (4 * ((d1 >> 4) & 3)))] = hi;
+        }
+      }
+    }
+  };
+
+  float m2[kMB], lsum[kMB];
+  int acand[kMB];
+  f32x4 yacc[DT][kMB];
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    m2[mb] = -INFINITY;
+    lsum[mb] = 0.f;
+    acand[mb] = INT_MAX;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int nrel = k_end - k_begin;
+  const int ntiles = (nrel + kTile - 1) / kTile;
+  const int ngroups = (ntiles + kWideG - 1) / kWideG;
+  issue(0);
+  stage(0);
+  __syncthreads();
+  for (int grp = 0; grp < ngroups; ++grp) {
+    if (grp + 1 < ngroups) issue(grp + 1);
+    for (int gt = 0; gt < kWideG && active; ++gt) {
+      const int it = grp * kWideG + gt;
+      if (it >= ntiles) break;
+      const int t0 = k_begin + it * kTile;
+      const uint32_t* kl = lds + (grp & 1) * kStage + gt * kTileWords;
+      const uint32_t* vt = kl + kKWords;
+      // S^T = K Q^T with K from LDS.
+      f32x4 s[2][kMB];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        v8 kop[KK];
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+          kop[kk] = bitcast_u4<v8>(
+              *reinterpret_cast<const u32x4*>(kl + ((16 * kb + li) * kKPitch + 32 * kk + 8 * lg) / 2));
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) acc = Elem<T>::mfma(kop[kk], qop[mb][kk], acc);
+          s[kb][mb] = acc;
+        }
+      }
+      const bool masked = pad_chunk || t0 + kTile > unmasked_end;
+      v8 phi[kMB], plo[kMB];
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb) {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float x = s[kb][mb][r] * scale_log2;
+            if (masked) x = (t0 + 16 * kb + 4 * lg + r) <= bound[mb] ? x : -INFINITY;
+            s[kb][mb][r] = x;
+            tmax = fmaxf(tmax, x);
+          }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float mnew = fmaxf(m2[mb], tmax);
+        const bool empty = mnew == -INFINITY;
+        const float alpha = empty ? 1.f : __builtin_amdgcn_exp2f(m2[mb] - mnew);
+        float psum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pv = empty ? 0.f : __builtin_amdgcn_exp2f(s[kb][mb][r] - mnew);
+            psum += pv;
+            const T h = static_cast<T>(pv);
+            phi[mb][4 * kb + r] = h;
+            if constexpr (PS == 2) plo[mb][4 * kb + r] = static_cast<T>(pv - static_cast<float>(h));
+          }
+        lsum[mb] = lsum[mb] * alpha + psum;
+        m2[mb] = mnew;
+        if (__any(alpha != 1.f)) {
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= alpha;
+          if (alpha != 1.f && !empty) {
+            int c = INT_MAX;
+#pragma unroll
+            for (int kb = 1; kb >= 0; --kb)
+#pragma unroll
+              for (int r = 3; r >= 0; --r)
+                c = s[kb][mb][r] == mnew ? t0 + 16 * kb + 4 * lg + r : c;
+            acand[mb] = c;
+          }
+        }
+      }
+      // Y^T += V^T P^T with V^T from LDS.
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = 16 * dt + li;
+        const int sw = 4 * (dt & 3);
+        const u32x2 x0 = *reinterpret_cast<const u32x2*>(vt + d * kPitch + ((2 * lg) ^ sw));
+        const u32x2 x1 = *reinterpret_cast<const u32x2*>(vt + d * kPitch + ((8 + 2 * lg) ^ sw));
+        const v8 aop = bitcast_u4<v8>(u32x4{x0[0], x0[1], x1[0], x1[1]});
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb) {
+          yacc[dt][mb] = Elem<T>::mfma(aop, phi[mb], yacc[dt][mb]);
+          if constexpr (PS == 2) yacc[dt][mb] = Elem<T>::mfma(aop, plo[mb], yacc[dt][mb]);
+        }
+      }
+    }
+    if (grp + 1 < ngroups) stage((grp + 1) & 1);
+    __syncthreads();
+  }
+  if (!active) return;
+
+  // This wave's rows are complete for the split: write the partials.
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    lsum[mb] += __shfl_xor(lsum[mb], 16);
+    lsum[mb] += __shfl_xor(lsum[mb], 32);
+    acand[mb] = min(acand[mb], __shfl_xor(acand[mb], 16));
+    acand[mb] = min(acand[mb], __shfl_xor(acand[mb], 32));
+  }
+  const int64_t slot = ((int64_t)head * n_mc + mc) * n_splits + split;
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    const int row = 16 * mb + li;
+    if (lg == 0) {
+      part_ml[(slot * kRows + row) * 2 + 0] = m2[mb];
+      part_ml[(slot * kRows + row) * 2 + 1] = lsum[mb];
+      part_arg[slot * kRows + row] = acand[mb] == INT_MAX ? -1 : acand[mb];
+    }
+    float* py = part_y + (slot * kRows + row) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(py + 16 * dt + 4 * lg) = yacc[dt][mb];
   }
 }
 
@@ -823,7 +1059,7 @@ static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b)
 // DROPKV_TUNE environment variable ("p1w=8,p1occ=1,p2w=4,s1=32,s2=32",
 // any subset) overrides them for experiments.
 struct Tune {
-  int p1w = 4, p1occ = 1, p2w = 8, s1 = 0, s2 = 0, target = 256;
+  int p1w = 4, p1occ = 1, p2w = 8, s1 = 0, s2 = 0, target = 256, p1wide = 3, p1g = 1;
 };
 static Tune read_tune() {
   Tune t;
@@ -838,6 +1074,8 @@ static Tune read_tune() {
     else if (!strcmp(key, "s1")) t.s1 = val;
     else if (!strcmp(key, "s2")) t.s2 = val;
     else if (!strcmp(key, "target")) t.target = val;
+    else if (!strcmp(key, "p1wide")) t.p1wide = val;
+    else if (!strcmp(key, "p1g")) t.p1g = val;
     e += n;
     if (*e == ',') ++e;
     n = 0;
@@ -859,7 +1097,13 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   p.p2_waves = tune.p2w == 8 ? 8 : 4;
   const int target = max(1, tune.target);  // workgroups per pass (one per CU)
   const int max_by_work = max(1, (int)(Lk / 256));
-  int s1 = splits > 0 ? (int)splits : (tune.s1 > 0 ? tune.s1 : ceil_div(target, (int64_t)p.heads * p.n_mc));
+  // Several row-chunks share each K/V tile in one workgroup (pass1w) from
+  // n_mc >= p1wide (0: never) up to one chunk per wave.
+  // p1_wide is 0 or the pass1w tile group (1, 2 or 4 tiles per LDS stage).
+  p.p1_wide = (tune.p1wide > 0 && p.n_mc >= tune.p1wide && p.n_mc <= kWideWaves)
+                  ? (tune.p1g == 4 ? 4 : tune.p1g == 2 ? 2 : 1) : 0;
+  const int64_t p1_groups = p.p1_wide ? (int64_t)p.heads : (int64_t)p.heads * p.n_mc;
+  int s1 = splits > 0 ? (int)splits : (tune.s1 > 0 ? tune.s1 : ceil_div(target, p1_groups));
   s1 = max(1, min(min(s1, max_by_work), kMaxSplits));
   p.kps1 = ceil_div(ceil_div(Lk, s1), kTile) * kTile;
   p.s1 = ceil_div(Lk, p.kps1);
@@ -905,16 +1149,36 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   const bool qvec = q_sd == 1 && (q_sb % 8) == 0 && (q_sh % 8) == 0 && (q_ss % 8) == 0 &&
                     (reinterpret_cast<uintptr_t>(q) & 15u) == 0;
   const dim3 g1(p.heads * p.n_mc * p.s1);
-  if (p.p1_waves == 8) {
-    hipLaunchKernelGGL((pass1_kernel<T, D, 8, 1>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
-  } else if (p.p1_occ == 1) {
-    hipLaunchKernelGGL((pass1_kernel<T, D, 4, 1>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
-  } else {
-    hipLaunchKernelGGL((pass1_kernel<T, D, 4, 2>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv,
-                       Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
-  }
+  auto launch1 = [&](auto ps) {
+    constexpr int PS = decltype(ps)::value;
+    if (p.p1_wide) {
+      auto wide = [&](auto grp) {
+        constexpr int G = decltype(grp)::value;
+        hipLaunchKernelGGL((pass1w_kernel<T, D, PS, G>), dim3(p.heads * p.s1), dim3(64 * kWideWaves), 0, st, qq,
+                           q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1,
+                           scale_log2, part_ml, part_y, part_arg);
+      };
+      if (p.p1_wide == 4)
+        wide(std::integral_constant<int, 4>{});
+      else if (p.p1_wide == 2)
+        wide(std::integral_constant<int, 2>{});
+      else
+        wide(std::integral_constant<int, 1>{});
+    } else if (p.p1_waves == 8) {
+      hipLaunchKernelGGL((pass1_kernel<T, D, 8, 1, PS>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
+                         vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
+    } else if (p.p1_occ == 1) {
+      hipLaunchKernelGGL((pass1_kernel<T, D, 4, 1, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
+                         vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
+    } else {
+      hipLaunchKernelGGL((pass1_kernel<T, D, 4, 2, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
+                         vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
+    }
+  };
+  if (p_round)
+    launch1(std::integral_constant<int, 1>{});
+  else
+    launch1(std::integral_constant<int, 2>{});
   timing_mark(st);
   const int n_rows = p.heads * p.mpad;
   hipLaunchKernelGGL((merge_kernel<T, D>), dim3((n_rows + kMergeRows - 1) / kMergeRows), dim3(64 * kMergeRows), 0, st,
@@ -922,6 +1186,9 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
                      q_sd, vv, Lk, Hkv, p.g, W, Lq, opblk, stblk, ystat, yf, zero_ptr, zero_words);
   timing_mark(st);
   SelFuse fz{};
+  // Row-chunks whose operands share LDS in one sweep over the keys (every
+  // further group streams the workgroup's K/V range again).  Two at most:
+  // instantiating the tile loop for more pushes pass 2 into register spills.
   const int cg = min(p.n_mc, 2);
   size_t lds2 = (size_t)cg * kOpSlots * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
   if (fuse) {
