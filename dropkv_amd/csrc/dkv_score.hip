@@ -914,12 +914,15 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
 #pragma unroll
     for (int i = 0; i < SPW; ++i)
       if ((int)threadIdx.x + i * NT < nw) opnd[threadIdx.x + i * NT] = sv[i];
+    // Groups of four row-chunks copy the second pair directly.
+    for (int i = SPW * NT + (int)threadIdx.x; i < nw; i += NT) opnd[i] = gop[i];
     if ((int)threadIdx.x < ns) stat[threadIdx.x] = stv;
     __syncthreads();
 
-    // The chunk count NC is a compile-time constant so that the refill loads
-    // are unconditional and the compiler's wait counts stay exact.
-    auto run = [&](auto nc_const) __attribute__((always_inline)) {
+    // The chunk count NC of the unrolled body is a compile-time constant so
+    // that the refill loads stay unconditional; groups of four row-chunks run
+    // that body for two pairs (`npairs`) on the same K/V registers.
+    auto run = [&](auto nc_const, int npairs) __attribute__((always_inline)) {
     constexpr int NC = decltype(nc_const)::value;
     auto tile = [&](v8 (&kop)[2][KK], v8 (&vop)[2][KK], int t0, int tn) __attribute__((always_inline)) {
       // |v|^2 of key t0+16kb+li (fp32 dot of the exact operand values), then
@@ -943,8 +946,11 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
 #pragma unroll
         for (int r = 0; r < 4; ++r) sc[kb][r] = 0.f;
 
+#pragma unroll 1
+      for (int cp = 0; cp < npairs; ++cp)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
+      for (int c1 = 0; c1 < NC; ++c1) {
+        const int c = cp * NC + c1;
         f32x4 sacc[2][kMB], gacc[2][kMB];
         const u32x4* ob = opnd + (size_t)(c * OPS) * 64 + lane;
 #pragma unroll
@@ -972,7 +978,7 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
           }
         // After the last row-chunk's MFMAs the K/V registers are free: start
         // the loads of tile tn (relative; zeros past the range).
-        if (c == NC - 1) {
+        if (c1 == NC - 1 && cp == npairs - 1) {
           load_rows_op<T, D>(kop, krs, k_lane, tn);
           load_rows_op<T, D>(vop, vrs, k_lane, tn);
         }
@@ -1027,10 +1033,10 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
       tc = tn;
     }
     };
-    if (cn == 2)
-      run(std::integral_constant<int, 2>{});
+    if (cn % 2 == 0)
+      run(std::integral_constant<int, 2>{}, cn / 2);
     else
-      run(std::integral_constant<int, 1>{});
+      run(std::integral_constant<int, 1>{}, 1);
   }
   if (fz.enabled) {
     __syncthreads();  // this workgroup's score stores are done; the LDS operands are dead
@@ -1187,9 +1193,10 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   timing_mark(st);
   SelFuse fz{};
   // Row-chunks whose operands share LDS in one sweep over the keys (every
-  // further group streams the workgroup's K/V range again).  Two at most:
-  // instantiating the tile loop for more pushes pass 2 into register spills.
-  const int cg = min(p.n_mc, 2);
+  // further group streams the workgroup's K/V range again): four when they
+  // divide n_mc (as pairs of the two-chunk body: unrolling four chunks pushes
+  // pass 2 into register spills), else up to two.
+  const int cg = (p.n_mc % 4 == 0) ? 4 : min(p.n_mc, 2);
   size_t lds2 = (size_t)cg * kOpSlots * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
   if (fuse) {
     fz.enabled = 1;
