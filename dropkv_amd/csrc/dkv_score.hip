@@ -656,7 +656,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   constexpr int DPL = D / 64;  // columns per lane
   constexpr int KK = D / 32;
   constexpr int OPS = kOpSlots * kMB * KK;
-  constexpr int kPre = 32;     // splits whose partial y is loaded up front
+  constexpr int kPre = 4096 / D;  // splits whose partial y is loaded up front (64 registers)
   const int lane = threadIdx.x & 63;
   if (zero_ptr)
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_words;
@@ -748,9 +748,20 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
 #pragma unroll
   for (int s = 0; s < kPre; ++s)
     if (s < n_splits) acc += __shfl(f_lane, s) * yv[s];
-  for (int s = kPre; s < n_splits; ++s) {
-    const float fs = s < 64 ? __shfl(f_lane, s) : weight(part_ml[((slot0 + s) * kRows + row) * 2]);
-    acc += fs * *reinterpret_cast<const fv*>(py + (int64_t)s * kRows * D);
+  // Further splits in batches of 8 whose loads are all issued before use.
+  for (int s0 = kPre; s0 < n_splits; s0 += 8) {
+    fv yb[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      yb[u] = s0 + u < n_splits ? *reinterpret_cast<const fv*>(py + (int64_t)(s0 + u) * kRows * D) : fv{};
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + u;
+      if (s < n_splits) {
+        const float fs = s < 64 ? __shfl(f_lane, s) : weight(part_ml[((slot0 + s) * kRows + row) * 2]);
+        acc += fs * yb[u];
+      }
+    }
   }
 
   float ysq = 0.f;
