@@ -49,6 +49,10 @@ _SIGNATURES = {
     "dropkv_timing_enable": (_c_int, [_c_int]),
     "dropkv_timing_read": (_c_int, [ctypes.POINTER(ctypes.c_double), _c_int]),
     "dropkv_selftest_mfma": (_c_int, [_c_vp, _c_vp]),
+    "dropkv_decode_workspace_bytes": (_c_size, [_c_i64] * 5),
+    "dropkv_decode_attention": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                         _c_vp, _c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                         _c_float, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_size, _c_vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

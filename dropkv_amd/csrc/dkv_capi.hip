@@ -299,6 +299,55 @@ int dropkv_timing_read(double* stage_ms, int cap) {
   return kernels;
 }
 
+size_t dropkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t capacity) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || capacity < 1 || !head_dim_supported(D)) return 0;
+  return dkv::decode_workspace_bytes((int)B, (int)Hq, (int)Hkv, (int)D, (int)capacity);
+}
+
+int dropkv_decode_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sd, const void* k_new,
+                            const void* v_new, int64_t n_sb, int64_t n_sh, int64_t n_sd, void* k_cache,
+                            void* v_cache, const int32_t* n_rows, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                            int64_t D, int64_t capacity, float scale, void* out, int64_t o_sb, int64_t o_sh,
+                            int64_t o_sd, void* workspace, size_t workspace_bytes, void* stream) {
+  (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
+  if (!q || !k_new || !v_new || !k_cache || !v_cache || !n_rows || !out || !workspace)
+    return fail(DROPKV_E_ARG, "null pointer argument");
+  if (dtype != DROPKV_BF16 && dtype != DROPKV_FP16) return fail(DROPKV_E_ARG, "dtype must be bf16 or fp16");
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv) return fail(DROPKV_E_ARG, "B, Hq, Hkv must be positive, Hkv | Hq");
+  if (Hq / Hkv > 16) return fail(DROPKV_E_UNSUPPORTED, "more than 16 query heads per KV head");
+  if (!head_dim_supported(D)) return fail(DROPKV_E_UNSUPPORTED, "head dim %lld not supported", (long long)D);
+  if (capacity < 1 || capacity * D * 2 > ((int64_t)1 << 31)) return fail(DROPKV_E_ARG, "capacity out of range");
+  if (!aligned16(k_cache) || !aligned16(v_cache)) return fail(DROPKV_E_ARG, "cache buffers must be 16-byte aligned");
+  if (workspace_bytes < dkv::decode_workspace_bytes((int)B, (int)Hq, (int)Hkv, (int)D, (int)capacity))
+    return fail(DROPKV_E_ARG, "workspace too small");
+  dkv::DecodeParams p{};
+  p.q = q;
+  p.q_sb = q_sb;
+  p.q_sh = q_sh;
+  p.q_sd = q_sd;
+  p.kn = k_new;
+  p.vn = v_new;
+  p.n_sb = n_sb;
+  p.n_sh = n_sh;
+  p.n_sd = n_sd;
+  p.kbuf = k_cache;
+  p.vbuf = v_cache;
+  p.n_rows = n_rows;
+  p.B = (int)B;
+  p.Hq = (int)Hq;
+  p.Hkv = (int)Hkv;
+  p.D = (int)D;
+  p.C = (int)capacity;
+  p.dtype_bf16 = dtype == DROPKV_BF16;
+  p.scale = scale;
+  p.out = out;
+  p.o_sb = o_sb;
+  p.o_sh = o_sh;
+  p.o_sd = o_sd;
+  p.workspace = workspace;
+  return hip_status(dkv::launch_decode_attention(p, static_cast<hipStream_t>(stream)), "decode launch");
+}
+
 int dropkv_selftest_mfma(float* out, void* stream) {
   (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
   if (!out) return fail(DROPKV_E_ARG, "null out");

@@ -39,6 +39,27 @@ hipError_t launch_debug_state(const ScorePlan& p, const char* ws, int D, float* 
                               hipStream_t st);
 hipError_t launch_mfma_selftest(float* out, hipStream_t st);
 
+// Decode step on the compressed cache (dkv_decode.hip).
+struct DecodeParams {
+  const void* q;  // [B, Hq, 1, D] element strides
+  int64_t q_sb, q_sh, q_sd;
+  const void* kn;  // the new token's K and V rows [B, Hkv, 1, D] (same strides)
+  const void* vn;
+  int64_t n_sb, n_sh, n_sd;
+  void* kbuf;  // [B, Hkv, C, D] contiguous cache buffers
+  void* vbuf;
+  const int* n_rows;  // device int: rows already stored
+  int B, Hq, Hkv, D, C;
+  int dtype_bf16;
+  float scale;
+  void* out;  // [B, 1, Hq, D] element strides
+  int64_t o_sb, o_sh, o_sd;
+  void* workspace;
+};
+int decode_splits(int C);
+size_t decode_workspace_bytes(int B, int Hq, int Hkv, int D, int C);
+hipError_t launch_decode_attention(const DecodeParams& p, hipStream_t st);
+
 size_t select_workspace_bytes(int64_t rows, int64_t Lk);
 // Words at the start of the selection workspace that must be zero on entry
 // (cleared by launch_select itself unless the caller already did it).

@@ -11,8 +11,10 @@ from a seed.  The model is the installed Transformers' ``Qwen2ForCausalLM``
 which evicts each layer's K/V with the HIP layer-call during prefill.
 
 Run ``python -m dropkv_amd.e2e_qwen2`` on a GPU; it prints one JSON line with
-the prefill time, the decode rate on the compressed cache and, for
-comparison, the same two figures with the uncompressed ``DynamicCache``.
+the prefill time and the decode rate on the compressed cache -- decoded by
+:class:`dropkv_amd.decode.CompressedDecoder` (preallocated buffers, one HIP
+graph per step) and, for comparison, eagerly through Transformers -- and the
+same figures with the uncompressed ``DynamicCache``.
 """
 
 from __future__ import annotations
@@ -26,6 +28,7 @@ import time
 import torch
 
 from . import hf_cache
+from .decode import CompressedDecoder
 
 # Qwen2-0.5B architecture (public model configuration).
 QWEN2_05B = dict(
@@ -115,24 +118,38 @@ def run(args) -> dict:
         return DynamicCache(config=cfg)
 
     res = {}
-    for kind in ("dropkv", "dynamic") if args.compare else ("dropkv",):
-        pre_ms, dec_ms = [], []
+    kinds = ("dropkv", "dropkv_eager", "dynamic") if args.compare else ("dropkv",)
+    for kind in kinds:
+        pre_ms, dec_ms, setup_ms = [], [], []
         for rep in range(args.warmup + args.reps):
-            cache = make_cache(kind)
+            cache = make_cache("dynamic" if kind == "dynamic" else "dropkv")
             tok, t_pre = _timed(lambda: prefill(model, ids, cache))
-            _, t_dec = _timed(lambda: greedy_decode(model, cache, tok, args.decode))
+            if kind == "dropkv":
+                dec, t_setup = _timed(lambda: CompressedDecoder(model, cache, args.decode))
+                out, t_dec = _timed(lambda: dec.generate(tok, args.decode))
+                stored, logical = int(dec.n_rows[0]), int(dec.pos[0, 0])
+                del dec
+            else:
+                t_setup = 0.0
+                out, t_dec = _timed(lambda: greedy_decode(model, cache, tok, args.decode))
+                stored, logical = cache.layers[0].keys.shape[-2], cache.get_seq_length()
             if rep >= args.warmup:
                 pre_ms.append(t_pre)
                 dec_ms.append(t_dec)
-            print(f"[e2e] {kind} rep {rep}: prefill {t_pre:.1f} ms, decode {args.decode} steps {t_dec:.1f} ms",
-                  file=sys.stderr, flush=True)
-        stored = cache.layers[0].keys.shape[-2]
+                setup_ms.append(t_setup)
+            print(f"[e2e] {kind} rep {rep}: prefill {t_pre:.1f} ms, decode setup {t_setup:.1f} ms, "
+                  f"decode {args.decode} steps {t_dec:.1f} ms", file=sys.stderr, flush=True)
         res[kind] = {
             "prefill_ms": statistics.median(pre_ms),
             "decode_tok_s": args.decode / (statistics.median(dec_ms) / 1e3),
             "stored_kv_rows_layer0": stored,
-            "logical_length": cache.get_seq_length(),
+            "logical_length": logical,
         }
+        if kind == "dropkv":
+            res[kind]["decode"] = "CompressedDecoder: HIP graph per step, dropkv_decode_attention"
+            res[kind]["decode_setup_ms"] = statistics.median(setup_ms)
+        else:
+            res[kind]["decode"] = "eager Transformers forward per step (SDPA, torch.cat append)"
         del cache
         torch.cuda.empty_cache()
     return {

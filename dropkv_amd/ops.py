@@ -192,6 +192,46 @@ class EvictPlan:
         return self.keep_idx, self.k_out, self.v_out
 
 
+def decode_workspace(B: int, Hq: int, Hkv: int, D: int, capacity: int, device) -> torch.Tensor:
+    """Workspace of ``decode_attention`` for one cache geometry (reusable
+    across steps and layers of that geometry)."""
+    nbytes = _lib.load().dropkv_decode_workspace_bytes(B, Hq, Hkv, D, capacity)
+    if nbytes == 0:
+        raise RuntimeError("unsupported decode geometry")
+    return _workspace(nbytes, torch.device(device))
+
+
+def decode_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                     v_cache: torch.Tensor, n_rows: torch.Tensor, scale: float, out: torch.Tensor,
+                     workspace: torch.Tensor) -> torch.Tensor:
+    """One decode step on preallocated cache buffers (``dropkv_decode_attention``):
+    stores k_new / v_new at row ``n_rows`` and writes the attention of q over
+    rows 0 .. n_rows into ``out`` [B, 1, Hq, D].  ``n_rows`` (int32, device)
+    is not advanced.  Launches only kernels: capturable in a HIP graph."""
+    dev = _check_device(q, k_new, v_new, k_cache, v_cache, n_rows, out, workspace)
+    if q.dtype not in _DTYPE_CODE or {k_new.dtype, v_new.dtype, k_cache.dtype, v_cache.dtype, out.dtype} != {q.dtype}:
+        raise RuntimeError("decode_attention: all tensors must share a bf16/fp16 dtype")
+    if n_rows.dtype != torch.int32:
+        raise RuntimeError("decode_attention: n_rows must be int32")
+    B, Hq, Lq, D = q.shape
+    _, Hkv, C, Dk = k_cache.shape
+    if Lq != 1 or Dk != D or tuple(k_new.shape) != (B, Hkv, 1, D) or v_new.shape != k_new.shape:
+        raise RuntimeError("decode_attention: shape mismatch")
+    if k_cache.shape != v_cache.shape or not k_cache.is_contiguous() or not v_cache.is_contiguous():
+        raise RuntimeError("decode_attention: cache buffers must be contiguous and alike")
+    if k_new.stride() != v_new.stride():
+        k_new, v_new = k_new.contiguous(), v_new.contiguous()
+    if tuple(out.shape) != (B, 1, Hq, D):
+        raise RuntimeError("decode_attention: out must be [B, 1, Hq, D]")
+    rc = _lib.load().dropkv_decode_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(3), k_new.data_ptr(), v_new.data_ptr(),
+        k_new.stride(0), k_new.stride(1), k_new.stride(3), k_cache.data_ptr(), v_cache.data_ptr(),
+        n_rows.data_ptr(), _DTYPE_CODE[q.dtype], B, Hq, Hkv, D, C, float(scale), out.data_ptr(),
+        out.stride(0), out.stride(2), out.stride(3), workspace.data_ptr(), workspace.numel(), _stream(dev))
+    _lib.check(rc, "dropkv_decode_attention")
+    return out
+
+
 def mfma_selftest(device="cuda") -> torch.Tensor:
     out = torch.empty(16, 16, dtype=torch.float32, device=device)
     rc = _lib.load().dropkv_selftest_mfma(out.data_ptr(), _stream(out.device))

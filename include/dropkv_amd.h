@@ -161,6 +161,32 @@ int dropkv_timing_read(double* stage_ms, int cap);
  * `out` (256 floats, device memory), row-major. */
 int dropkv_selftest_mfma(float* out, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Decode on the compressed cache.  Replaces the decode branch of
+ * DropKVCache.update (dropkv_cache.py:609-617: torch.cat of the new row onto
+ * the stored K/V) together with the attention the model then runs over the
+ * concatenation (torch SDPA in the reference's Transformers integration,
+ * patches/dropkv_transformers.patch:206-213).
+ *
+ * k_cache / v_cache: [B, Hkv, capacity, D] contiguous buffers whose first
+ * *n_rows rows (device int32) are filled.  One call stores the new token's
+ * rows k_new / v_new ([B, Hkv, 1, D], element strides n_*) at row *n_rows
+ * and writes softmax(q K^T * scale) V over rows 0 .. *n_rows into out
+ * ([B, 1, Hq, D], element strides o_*) for the query q ([B, Hq, 1, D],
+ * element strides q_*), the GQA group of query head h being KV head
+ * h / (Hq / Hkv).  *n_rows is read on the device and not advanced: the
+ * caller adds 1 after the step (so a captured graph replays every step).
+ * Requires *n_rows < capacity; larger values are clamped to capacity - 1 and
+ * overwrite the last row.  Hq / Hkv <= 16, D in dropkv_supported_head_dims.
+ * The workspace (dropkv_decode_workspace_bytes) holds the split partials.
+ * ------------------------------------------------------------------------ */
+size_t dropkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t capacity);
+int dropkv_decode_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sd, const void* k_new,
+                            const void* v_new, int64_t n_sb, int64_t n_sh, int64_t n_sd, void* k_cache,
+                            void* v_cache, const int32_t* n_rows, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                            int64_t D, int64_t capacity, float scale, void* out, int64_t o_sb, int64_t o_sh,
+                            int64_t o_sd, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
