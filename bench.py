@@ -10,9 +10,9 @@ cache, i.e. one ``dropkv_evict`` call on inputs already resident in HBM.
 Prints one JSON line.  ``value`` is the K/V bytes read once per layer-call
 (2*B*Hkv*Lk*D*2 = 134,217,728 B) divided by the measured time per step, in
 GB/s.  ``roofline`` describes the longest kernel of the call: its duration is
-measured with HIP events that the library records on its own launch stream
-right before and after each kernel (``dropkv_timing_*``), averaged over the
-timed steps.  ``cpu_baseline`` times the CPU oracle of the deployed path
+measured with the HIP events that ``hipExtLaunchKernel`` sets to each
+dispatch's own begin and end time stamps (``dropkv_timing_*``; the same
+source as the rocprofv3 kernel trace), averaged over the timed steps.  ``cpu_baseline`` times the CPU oracle of the deployed path
 (score -> pool -> top-k -> sort -> gather) on the same inputs.
 
 Other modes: ``--kernels-only`` (warm-up + steps, no extras; for profiler
@@ -268,8 +268,8 @@ def main():
     graph.replay()
     graph_ms, _ = timed(graph.replay, args.steps)
 
-    # Per-kernel durations with HIP events recorded by the library on its
-    # launch stream around each kernel (eager calls, one read per call).
+    # Per-kernel durations from the dispatches' own time stamps (events that
+    # hipExtLaunchKernel fills; eager calls, one read per call).
     lib = _lib.load()
     buf = (ctypes.c_double * 16)()
     sums, nk = None, 0
@@ -331,8 +331,8 @@ def main():
         "wall_ms_per_step": round(wall_ms, 5),
         "graph_ms_per_step": round(graph_ms, 5),
         "kernel_us": {k: round(v, 3) for k, v in kernel_us.items()},
-        "kernel_timing": "HIP events recorded by the library on its launch stream before/after each kernel "
-                         "(includes the dispatch gap), mean over the steps",
+        "kernel_timing": "per-dispatch begin/end time stamps (hipExtLaunchKernel start/stop events set by the "
+                         "runtime), mean over the steps",
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "bytes_per_launch": bytes_alg},

@@ -62,31 +62,30 @@ int check_score_args(const void* q, const void* k, const void* v, int dtype, int
   return DROPKV_OK;
 }
 
-// Event-based stage timing (dropkv_timing_*), per calling thread: event 0
-// is recorded when a timed API call starts, event i+1 after its i-th kernel.
+// Kernel timing (dropkv_timing_*), per calling thread: the i-th kernel of
+// the most recent timed call gets events ev[2i] (start) and ev[2i+1] (stop),
+// filled by hipExtLaunchKernel with the dispatch's begin and end time stamps.
 constexpr int kMaxTimedKernels = 16;
 struct Timing {
   bool on = false, created = false;
-  int n = 0;  // events recorded by the most recent call
-  hipEvent_t ev[kMaxTimedKernels + 1];
+  int n = 0;  // kernels of the most recent call that got an event pair
+  hipEvent_t ev[2 * kMaxTimedKernels];
 };
 thread_local Timing t_timing;
 
 // Called at the start of every API entry that launches kernels.
-void timing_start(hipStream_t st) {
-  Timing& t = t_timing;
-  t.n = 0;
-  if (!t.on) return;
-  if (hipEventRecord(t.ev[0], st) == hipSuccess) t.n = 1;
-}
+void timing_start(hipStream_t) { t_timing.n = 0; }
 
 }  // namespace
 
 namespace dkv {
-void timing_mark(hipStream_t st) {
+bool timing_pair(hipEvent_t* start, hipEvent_t* stop) {
   Timing& t = t_timing;
-  if (!t.on || t.n < 1 || t.n > kMaxTimedKernels) return;
-  if (hipEventRecord(t.ev[t.n], st) == hipSuccess) ++t.n;
+  if (!t.on || t.n >= kMaxTimedKernels) return false;
+  *start = t.ev[2 * t.n];
+  *stop = t.ev[2 * t.n + 1];
+  ++t.n;
+  return true;
 }
 }  // namespace dkv
 
@@ -269,7 +268,7 @@ int dropkv_timing_enable(int on) {
   Timing& t = t_timing;
   (void)hipGetLastError();
   if (on && !t.created) {
-    for (int i = 0; i <= kMaxTimedKernels; ++i) {
+    for (int i = 0; i < 2 * kMaxTimedKernels; ++i) {
       hipError_t e = hipEventCreate(&t.ev[i]);
       if (e != hipSuccess) {
         for (int j = 0; j < i; ++j) (void)hipEventDestroy(t.ev[j]);
@@ -286,17 +285,16 @@ int dropkv_timing_enable(int on) {
 int dropkv_timing_read(double* stage_ms, int cap) {
   Timing& t = t_timing;
   if (!stage_ms || cap < 0) return -fail(DROPKV_E_ARG, "null stage_ms");
-  if (t.n < 2) return 0;
-  hipError_t e = hipEventSynchronize(t.ev[t.n - 1]);
+  if (t.n < 1) return 0;
+  hipError_t e = hipEventSynchronize(t.ev[2 * t.n - 1]);
   if (e != hipSuccess) return -hip_status(e, "hipEventSynchronize");
-  const int kernels = t.n - 1;
-  for (int i = 0; i < kernels && i < cap; ++i) {
+  for (int i = 0; i < t.n && i < cap; ++i) {
     float ms = 0.f;
-    e = hipEventElapsedTime(&ms, t.ev[i], t.ev[i + 1]);
+    e = hipEventElapsedTime(&ms, t.ev[2 * i], t.ev[2 * i + 1]);
     if (e != hipSuccess) return -hip_status(e, "hipEventElapsedTime");
     stage_ms[i] = ms;
   }
-  return kernels;
+  return t.n;
 }
 
 size_t dropkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t capacity) {
@@ -345,6 +343,7 @@ int dropkv_decode_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q
   p.o_sh = o_sh;
   p.o_sd = o_sd;
   p.workspace = workspace;
+  timing_start(static_cast<hipStream_t>(stream));
   return hip_status(dkv::launch_decode_attention(p, static_cast<hipStream_t>(stream)), "decode launch");
 }
 

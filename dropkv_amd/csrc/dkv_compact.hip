@@ -85,19 +85,18 @@ hipError_t launch_compact(const void* k0, const void* v0, int64_t s0b, int64_t s
   const int bph = (int)((keep + kRowsPerBlock - 1) / kRowsPerBlock);
   const dim3 grid((unsigned)(B * H * bph));
   if (vec) {
-    hipLaunchKernelGGL(compact_kernel<uint4>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)(row_bytes / 16),
+    launch(compact_kernel<uint4>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)(row_bytes / 16),
                        idx, (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
   } else if (eb == 2) {
-    hipLaunchKernelGGL(compact_kernel<uint16_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)D, idx,
+    launch(compact_kernel<uint16_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)D, idx,
                        (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
   } else if (eb == 4) {
-    hipLaunchKernelGGL(compact_kernel<uint32_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)D, idx,
+    launch(compact_kernel<uint32_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)D, idx,
                        (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
   } else {
-    hipLaunchKernelGGL(compact_kernel<uint8_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)row_bytes, idx,
+    launch(compact_kernel<uint8_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)row_bytes, idx,
                        (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
   }
-  timing_mark(st);
   return hipGetLastError();
 }
 

@@ -289,20 +289,19 @@ size_t decode_workspace_bytes(int B, int Hq, int Hkv, int D, int C) {
 template <typename T, int D>
 static hipError_t launch_decode_t(DecodeArgs a, hipStream_t st) {
   const int g = a.Hq / a.Hkv;
+  if (g < 1 || g > kDecMaxG) return hipErrorInvalidValue;
   const dim3 grid(a.B * a.Hkv * a.S);
   if (g <= 1)
-    hipLaunchKernelGGL((decode_partial_kernel<T, D, 1>), grid, dim3(64), 0, st, a);
+    launch((decode_partial_kernel<T, D, 1>), grid, dim3(64), 0, st, a);
   else if (g <= 2)
-    hipLaunchKernelGGL((decode_partial_kernel<T, D, 2>), grid, dim3(64), 0, st, a);
+    launch((decode_partial_kernel<T, D, 2>), grid, dim3(64), 0, st, a);
   else if (g <= 4)
-    hipLaunchKernelGGL((decode_partial_kernel<T, D, 4>), grid, dim3(64), 0, st, a);
+    launch((decode_partial_kernel<T, D, 4>), grid, dim3(64), 0, st, a);
   else if (g <= 8)
-    hipLaunchKernelGGL((decode_partial_kernel<T, D, 8>), grid, dim3(64), 0, st, a);
+    launch((decode_partial_kernel<T, D, 8>), grid, dim3(64), 0, st, a);
   else
-    hipLaunchKernelGGL((decode_partial_kernel<T, D, 16>), grid, dim3(64), 0, st, a);
-  timing_mark(st);
-  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(a.B * a.Hq), dim3(64), 0, st, a);
-  timing_mark(st);
+    launch((decode_partial_kernel<T, D, 16>), grid, dim3(64), 0, st, a);
+  launch((decode_merge_kernel<T, D>), dim3(a.B * a.Hq), dim3(64), 0, st, a);
   return hipGetLastError();
 }
 

@@ -1,16 +1,30 @@
 // Host-side interfaces between the kernel translation units and the C ABI.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
 namespace dkv {
 
-// Event-based stage timing (dropkv_timing_*): when enabled on the calling
-// thread, every launch helper calls timing_mark(stream) right after each
-// kernel launch, recording the next HIP event of the current call.
-void timing_mark(hipStream_t st);
+// Kernel timing (dropkv_timing_*): when enabled on the calling thread,
+// timing_pair hands out the (start, stop) events of the current call's next
+// kernel and returns true.  hipExtLaunchKernel sets them to that dispatch's
+// own begin and end time stamps, so the elapsed time is the kernel's
+// execution alone, without the dispatch gap before it.
+bool timing_pair(hipEvent_t* start, hipEvent_t* stop);
+
+// Every kernel of the API calls is launched through here.
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shmem, hipStream_t st,
+                   Args... args) {
+  hipEvent_t a, b;
+  if (timing_pair(&a, &b))
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, st, a, b, 0u, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, shmem, st, args...);
+}
 
 // Launch geometry and workspace layout of one scoring call.
 struct ScorePlan {

@@ -1171,7 +1171,7 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
     if (p.p1_wide) {
       auto wide = [&](auto grp) {
         constexpr int G = decltype(grp)::value;
-        hipLaunchKernelGGL((pass1w_kernel<T, D, PS, G>), dim3(p.heads * p.s1), dim3(64 * kWideWaves), 0, st, qq,
+        launch((pass1w_kernel<T, D, PS, G>), dim3(p.heads * p.s1), dim3(64 * kWideWaves), 0, st, qq,
                            q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1,
                            scale_log2, part_ml, part_y, part_arg);
       };
@@ -1182,13 +1182,13 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
       else
         wide(std::integral_constant<int, 1>{});
     } else if (p.p1_waves == 8) {
-      hipLaunchKernelGGL((pass1_kernel<T, D, 8, 1, PS>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
+      launch((pass1_kernel<T, D, 8, 1, PS>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
                          vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
     } else if (p.p1_occ == 1) {
-      hipLaunchKernelGGL((pass1_kernel<T, D, 4, 1, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
+      launch((pass1_kernel<T, D, 4, 1, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
                          vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
     } else {
-      hipLaunchKernelGGL((pass1_kernel<T, D, 4, 2, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
+      launch((pass1_kernel<T, D, 4, 2, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
                          vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
     }
   };
@@ -1196,12 +1196,10 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
     launch1(std::integral_constant<int, 1>{});
   else
     launch1(std::integral_constant<int, 2>{});
-  timing_mark(st);
   const int n_rows = p.heads * p.mpad;
-  hipLaunchKernelGGL((merge_kernel<T, D>), dim3((n_rows + kMergeRows - 1) / kMergeRows), dim3(64 * kMergeRows), 0, st,
+  launch((merge_kernel<T, D>), dim3((n_rows + kMergeRows - 1) / kMergeRows), dim3(64 * kMergeRows), 0, st,
                      part_ml, part_y, part_arg, p.n_mc, p.s1, p.M, n_rows, p_round, y_round, qq, q_sb, q_sh, q_ss,
                      q_sd, vv, Lk, Hkv, p.g, W, Lq, opblk, stblk, ystat, yf, zero_ptr, zero_words);
-  timing_mark(st);
   SelFuse fz{};
   // Row-chunks whose operands share LDS in one sweep over the keys (every
   // further group streams the workgroup's K/V range again): four when they
@@ -1221,13 +1219,12 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   }
   const dim3 g2(p.heads * p.s2);
   if (p.p2_waves == 8) {
-    hipLaunchKernelGGL((pass2_kernel<T, D, 8, 1>), g2, dim3(512), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M,
+    launch((pass2_kernel<T, D, 8, 1>), g2, dim3(512), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M,
                        p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, opblk, stblk, scores, fz);
   } else {
-    hipLaunchKernelGGL((pass2_kernel<T, D, 4, 2>), g2, dim3(256), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M,
+    launch((pass2_kernel<T, D, 4, 2>), g2, dim3(256), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M,
                        p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, opblk, stblk, scores, fz);
   }
-  timing_mark(st);
   return hipGetLastError();
 }
 

@@ -479,15 +479,13 @@ hipError_t launch_select_after_pool(const float* scores, int rows, int Lk, int k
   const SelWs ws = sel_layout(ws_base, rows, Lk, nullptr);
   const int chunks = (Lk + kChunk - 1) / kChunk;
   const dim3 grid((unsigned)(rows * chunks));
-  hipLaunchKernelGGL(sel_cand_kernel, grid, dim3(kSelT), 0, st, scores, Lk, ks, window, keep, chunks,
+  launch(sel_cand_kernel, grid, dim3(kSelT), 0, st, scores, Lk, ks, window, keep, chunks,
                      SplitGeom{n_splits, kps}, ws);
-  timing_mark(st);
   // Speculative candidates per chunk region: a multiple of 4, at least 4,
   // chunks * spec <= kEmitCandLds.
   const int spec = std::max(4, std::min(kSpecMax, kEmitCandLds / chunks) & ~3);
-  hipLaunchKernelGGL(sel_emit_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, spec, ws, out_idx,
+  launch(sel_emit_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, spec, ws, out_idx,
                      pooled_out, compact_args(cp));
-  timing_mark(st);
   return hipGetLastError();
 }
 
@@ -498,13 +496,11 @@ hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int wind
   const int chunks = (Lk + kChunk - 1) / kChunk;
   if (!pre_zeroed) {
     const int64_t zn = (int64_t)rows * kRowWords;
-    hipLaunchKernelGGL(sel_zero_kernel, dim3((unsigned)std::min<int64_t>((zn + kSelT - 1) / kSelT, 1024)),
+    launch(sel_zero_kernel, dim3((unsigned)std::min<int64_t>((zn + kSelT - 1) / kSelT, 1024)),
                        dim3(kSelT), 0, st, ws.rowws, zn);
-    timing_mark(st);
   }
-  hipLaunchKernelGGL(sel_pool_kernel, dim3((unsigned)(rows * chunks)), dim3(kSelT), 0, st, scores, Lk, ks, window,
+  launch(sel_pool_kernel, dim3((unsigned)(rows * chunks)), dim3(kSelT), 0, st, scores, Lk, ks, window,
                      chunks, ws);
-  timing_mark(st);
   return launch_select_after_pool(scores, rows, Lk, ks, window, keep, 1, Lk, out_idx, pooled_out, ws_base, cp, st);
 }
 

@@ -144,15 +144,17 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
 
 /* Kernel timing with HIP events (no counterpart in the reference, which has
  * no timers).  dropkv_timing_enable(1) makes every later dropkv_scores /
- * dropkv_select / dropkv_compact / dropkv_compact2 / dropkv_evict call on the
- * calling thread record one HIP event on its stream when it starts and one
- * right after each kernel it launches.  dropkv_timing_read waits for the
- * last event of the most recent such call, writes the elapsed milliseconds
- * of each of its kernels, in launch order, into stage_ms (at most cap
- * values) and returns the number of kernels (0 if none were timed, a
- * negative status code on error).  The elapsed time of a kernel includes the
- * dispatch gap before it.  Only the most recent call is kept; not for use
- * while a stream is being captured into a graph. */
+ * dropkv_select / dropkv_compact / dropkv_compact2 / dropkv_evict /
+ * dropkv_decode_attention call on the calling thread launch its kernels with
+ * hipExtLaunchKernel and a (start, stop) event pair each, which the runtime
+ * sets to that dispatch's own begin and end time stamps.  dropkv_timing_read
+ * waits for the last kernel of the most recent such call, writes the
+ * execution time in milliseconds of each of its kernels, in launch order,
+ * into stage_ms (at most cap values) and returns the number of kernels (0 if
+ * none were timed, a negative status code on error).  The times exclude the
+ * dispatch gaps between kernels.  At most 16 kernels per call are timed;
+ * only the most recent call is kept; not for use while a stream is being
+ * captured into a graph. */
 int dropkv_timing_enable(int on);
 int dropkv_timing_read(double* stage_ms, int cap);
 
