@@ -37,6 +37,31 @@ __device__ __forceinline__ float round_through(float x) {
   return static_cast<float>(static_cast<T>(x));
 }
 
+// The same for two values at once (bf16: one packed conversion).
+template <typename T>
+__device__ __forceinline__ void round_through2(float& a, float& b) {
+  a = round_through<T>(a);
+  b = round_through<T>(b);
+}
+template <>
+__device__ __forceinline__ void round_through2<__bf16>(float& a, float& b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+  const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), h2));
+  a = __builtin_bit_cast(float, u << 16);
+  b = __builtin_bit_cast(float, u & 0xffff0000u);
+}
+
+// min(p, 1) for p >= 0 or NaN (as unsigned integers: NaN gives 1, like fminf)
+// and min(x, 0) for the sign of x (as signed integers): one integer op each,
+// where fminf also canonicalises its operand.
+__device__ __forceinline__ float min_one_nonneg(float p) {
+  return __builtin_bit_cast(float, min(__builtin_bit_cast(uint32_t, p), 0x3f800000u));
+}
+__device__ __forceinline__ float min_zero(float x) {
+  return __builtin_bit_cast(float, min(__builtin_bit_cast(int32_t, x), 0));
+}
+
 // Raw buffer view of `bytes` bytes at `base`.  Loads at byte offsets >= bytes
 // return zeros and issue no memory request, so a tile loop can load past the
 // end of its range without a branch.

@@ -50,6 +50,69 @@ __device__ __forceinline__ int row_bound(int m, int M, int W, int Lk) {
   return m < M ? Lk - W + (m % W) : -1;
 }
 
+// Online-softmax step (base 2) of one 32-key tile starting at key t0, for
+// the lane's kMB row blocks: scales the logits s in place, applies the causal
+// bound (kMasked: tiles that reach it, or padding rows), updates the running
+// maximum m2 and sum lsum, rescales the y accumulators when a maximum moved
+// (and then notes in acand which of the lane's keys holds it), and returns
+// the tile's P in PS parts of the element type (hi, and lo when PS == 2).
+template <typename T, int D, int PS, bool kMasked>
+__device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB], float (&lsum)[kMB],
+                                             int (&acand)[kMB], f32x4 (&yacc)[D / 16][kMB],
+                                             typename Elem<T>::v8 (&phi)[kMB], typename Elem<T>::v8 (&plo)[kMB],
+                                             const int (&bound)[kMB], int t0, int lg, float scale_log2) {
+  constexpr int DT = D / 16;
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = s[kb][mb][r] * scale_log2;
+        if (kMasked) x = (t0 + 16 * kb + 4 * lg + r) <= bound[mb] ? x : -INFINITY;
+        s[kb][mb][r] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mnew = fmaxf(m2[mb], tmax);
+    const bool empty = mnew == -INFINITY;
+    const float alpha = empty ? 1.f : __builtin_amdgcn_exp2f(m2[mb] - mnew);
+    // An empty row (every logit -inf so far) subtracts 0, so that its p are
+    // exp2(-inf) = 0 without a select per element.
+    const float msub = empty ? 0.f : mnew;
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(s[kb][mb][r] - msub);
+        psum += pv;
+        const T h = static_cast<T>(pv);
+        phi[mb][4 * kb + r] = h;
+        if constexpr (PS == 2) plo[mb][4 * kb + r] = static_cast<T>(pv - static_cast<float>(h));
+      }
+    lsum[mb] = lsum[mb] * alpha + psum;
+    m2[mb] = mnew;
+    // Rescale only when some row's maximum moved (rare after a few tiles);
+    // then the lanes of a row whose maximum moved note which of their keys
+    // hold it.
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= alpha;
+      if (alpha != 1.f && !empty) {
+        int c = INT_MAX;
+#pragma unroll
+        for (int kb = 1; kb >= 0; --kb)
+#pragma unroll
+          for (int r = 3; r >= 0; --r) c = s[kb][mb][r] == mnew ? t0 + 16 * kb + 4 * lg + r : c;
+        acand[mb] = c;
+      }
+    }
+  }
+}
+
 // One lane's Q^T operand: 8 consecutive head-dim values from column d0 of
 // query row m (zeros for padding rows).  With `qvec` (head-dim stride 1 and
 // 16-byte aligned rows, checked by the host) one 16-byte load; otherwise
@@ -248,59 +311,14 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     load_rows_op<T, D>(kop, krs, k_lane, tn);
     load_v_pairs<T, D>(va, vb, vrs, v_lane, tn);
 
-    // Online softmax (base 2) for each row block.  P enters the MFMA as PS
-    // parts: one when the scores use p rounded to the input dtype (y is then
-    // only needed to that precision, see the merge kernel), hi + lo for the
-    // fp32 semantics.
-    const bool masked = pad_chunk || t0 + kTile > unmasked_end;
+    // Online softmax.  P enters the MFMA as PS parts: one when the scores
+    // use p rounded to the input dtype (y is then only needed to that
+    // precision, see the merge kernel), hi + lo for the fp32 semantics.
     v8 phi[kMB], plo[kMB];
-#pragma unroll
-    for (int mb = 0; mb < kMB; ++mb) {
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float x = s[kb][mb][r] * scale_log2;
-          if (masked) x = (t0 + 16 * kb + 4 * lg + r) <= bound[mb] ? x : -INFINITY;
-          s[kb][mb][r] = x;
-          tmax = fmaxf(tmax, x);
-        }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const float mnew = fmaxf(m2[mb], tmax);
-      const bool empty = mnew == -INFINITY;
-      const float alpha = empty ? 1.f : __builtin_amdgcn_exp2f(m2[mb] - mnew);
-      float psum = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float pv = empty ? 0.f : __builtin_amdgcn_exp2f(s[kb][mb][r] - mnew);
-          psum += pv;
-          const T h = static_cast<T>(pv);
-          phi[mb][4 * kb + r] = h;
-          if constexpr (PS == 2) plo[mb][4 * kb + r] = static_cast<T>(pv - static_cast<float>(h));
-        }
-      lsum[mb] = lsum[mb] * alpha + psum;
-      m2[mb] = mnew;
-      // Rescale only when some row's maximum moved (rare after a few tiles);
-      // then the lanes of a row whose maximum moved note which of their keys
-      // hold it.
-      if (__any(alpha != 1.f)) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= alpha;
-        if (alpha != 1.f && !empty) {
-          int c = INT_MAX;
-#pragma unroll
-          for (int kb = 1; kb >= 0; --kb)
-#pragma unroll
-            for (int r = 3; r >= 0; --r)
-              c = s[kb][mb][r] == mnew ? t0 + 16 * kb + 4 * lg + r : c;
-          acand[mb] = c;
-        }
-      }
-    }
+    if (pad_chunk || t0 + kTile > unmasked_end)
+      softmax_tile<T, D, PS, true>(s, m2, lsum, acand, yacc, phi, plo, bound, t0, lg, scale_log2);
+    else
+      softmax_tile<T, D, PS, false>(s, m2, lsum, acand, yacc, phi, plo, bound, t0, lg, scale_log2);
 
     // Y^T += V^T P^T.  Lane (li, lg) reads V^T[16dt+li][keys 4lg..4lg+3, 16+4lg..+3].
 #pragma unroll
@@ -541,52 +559,11 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
           s[kb][mb] = acc;
         }
       }
-      const bool masked = pad_chunk || t0 + kTile > unmasked_end;
       v8 phi[kMB], plo[kMB];
-#pragma unroll
-      for (int mb = 0; mb < kMB; ++mb) {
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float x = s[kb][mb][r] * scale_log2;
-            if (masked) x = (t0 + 16 * kb + 4 * lg + r) <= bound[mb] ? x : -INFINITY;
-            s[kb][mb][r] = x;
-            tmax = fmaxf(tmax, x);
-          }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float mnew = fmaxf(m2[mb], tmax);
-        const bool empty = mnew == -INFINITY;
-        const float alpha = empty ? 1.f : __builtin_amdgcn_exp2f(m2[mb] - mnew);
-        float psum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float pv = empty ? 0.f : __builtin_amdgcn_exp2f(s[kb][mb][r] - mnew);
-            psum += pv;
-            const T h = static_cast<T>(pv);
-            phi[mb][4 * kb + r] = h;
-            if constexpr (PS == 2) plo[mb][4 * kb + r] = static_cast<T>(pv - static_cast<float>(h));
-          }
-        lsum[mb] = lsum[mb] * alpha + psum;
-        m2[mb] = mnew;
-        if (__any(alpha != 1.f)) {
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= alpha;
-          if (alpha != 1.f && !empty) {
-            int c = INT_MAX;
-#pragma unroll
-            for (int kb = 1; kb >= 0; --kb)
-#pragma unroll
-              for (int r = 3; r >= 0; --r)
-                c = s[kb][mb][r] == mnew ? t0 + 16 * kb + 4 * lg + r : c;
-            acand[mb] = c;
-          }
-        }
-      }
+      if (pad_chunk || t0 + kTile > unmasked_end)
+        softmax_tile<T, D, PS, true>(s, m2, lsum, acand, yacc, phi, plo, bound, t0, lg, scale_log2);
+      else
+        softmax_tile<T, D, PS, false>(s, m2, lsum, acand, yacc, phi, plo, bound, t0, lg, scale_log2);
       // Y^T += V^T P^T with V^T from LDS.
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
@@ -860,11 +837,11 @@ struct SelFuse {
 };
 constexpr int kScLds = 4096;  // longest split range whose scores pass 2 keeps in LDS
 
-template <typename T, int D, int WAVES, int MINW>
+template <typename T, int D, int WAVES, int MINW, bool PR>
 __global__ void __launch_bounds__(64 * WAVES, MINW)
 pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int cg, int n_splits, int kps,
-             float scale_log2, float eps, int p_round,
+             float scale_log2, float eps,
              const u32x4* __restrict__ opblk, const float* __restrict__ stblk, float* __restrict__ scores,
              SelFuse fz) {
   typedef typename Elem<T>::v8 v8;
@@ -886,7 +863,8 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
   const int li = lane & 15, lg = lane >> 4;
   const int mpad = n_mc * kRows;
 
-  const float inv_g = 1.0f / static_cast<float>(g);
+  // The per-key sums hold sum_m w * (-dist2/2): scale by -2/g at the end.
+  const float out_scale = -2.0f * (1.0f / static_cast<float>(g));
   const int k_begin = split * kps;
   const int k_end = min(k_begin + kps, Lk);
   const int64_t roff = ((int64_t)head * Lk + k_begin) * D;
@@ -964,13 +942,18 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
         const int c = cp * NC + c1;
         f32x4 sacc[2][kMB], gacc[2][kMB];
         const u32x4* ob = opnd + (size_t)(c * OPS) * 64 + lane;
+        // G starts at -(|v|^2 + |y|^2)/2, so that after the MFMAs it holds
+        // <v,y> - (|v|^2 + |y|^2)/2 = -dist2/2 of every (key, row) pair.
 #pragma unroll
-        for (int mb = 0; mb < kMB; ++mb)
+        for (int mb = 0; mb < kMB; ++mb) {
+          const float nyh = -0.5f * stat[(c * kMB + mb) * 32 + 16 + li];
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb) {
             sacc[kb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            gacc[kb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) gacc[kb][mb][r] = fmaf(vn2[kb][r], -0.5f, nyh);
           }
+        }
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
@@ -993,25 +976,41 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
           load_rows_op<T, D>(kop, krs, k_lane, tn);
           load_rows_op<T, D>(vop, vrs, k_lane, tn);
         }
+        // sc accumulates w * (-dist2/2); the causal bound is applied only in
+        // tiles that reach it (and with padding rows), so that the other
+        // tiles carry no per-element selects.
+        auto epilogue = [&](auto masked_c) __attribute__((always_inline)) {
+          constexpr bool kMasked = decltype(masked_c)::value;
 #pragma unroll
-        for (int mb = 0; mb < kMB; ++mb) {
-          const int m = (c0 + c) * kRows + mb * 16 + li;
-          const int bound = row_bound(m, M, W, Lk);
-          const float lse2 = stat[(c * kMB + mb) * 32 + li];
-          const float yn2 = stat[(c * kMB + mb) * 32 + 16 + li];
+          for (int mb = 0; mb < kMB; ++mb) {
+            const int m = (c0 + c) * kRows + mb * 16 + li;
+            const int bound = kMasked ? row_bound(m, M, W, Lk) : 0;
+            const float lse2 = stat[(c * kMB + mb) * 32 + li];
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              float p = __builtin_amdgcn_exp2f(sacc[kb][mb][r] * scale_log2 - lse2);
-              if (masked) p = (t0 + 16 * kb + 4 * lg + r) <= bound ? p : 0.f;
-              p = fminf(p, 1.f);
-              if (p_round) p = round_through<T>(p);
-              const float ratio = p * __builtin_amdgcn_rcpf(1.0f - p + eps);
-              const float dist2 = fmaxf(vn2[kb][r] - 2.0f * gacc[kb][mb][r] + yn2, 0.f);
-              sc[kb][r] += ratio * ratio * dist2;
-            }
-        }
+              for (int r = 0; r < 4; r += 2) {
+                float p[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                  p[e] = __builtin_amdgcn_exp2f(sacc[kb][mb][r + e] * scale_log2 - lse2);
+                  if (kMasked) p[e] = (t0 + 16 * kb + 4 * lg + r + e) <= bound ? p[e] : 0.f;
+                  p[e] = min_one_nonneg(p[e]);
+                }
+                if (PR) round_through2<T>(p[0], p[1]);
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                  const float ratio = p[e] * __builtin_amdgcn_rcpf(1.0f - p[e] + eps);
+                  const float nd2 = min_zero(gacc[kb][mb][r + e]);  // -dist2/2, dist2 clamped at 0
+                  sc[kb][r + e] = fmaf(ratio * ratio, nd2, sc[kb][r + e]);
+                }
+              }
+          }
+        };
+        if (masked)
+          epilogue(std::true_type{});
+        else
+          epilogue(std::false_type{});
       }
 
       // Sum over the 16 query rows held by lanes li = 0..15 as a
@@ -1032,8 +1031,8 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
         if ((li & 3) == 0 && n < k_end) {
           float* dst = scores + (int64_t)head * Lk + n;
           if (!first) v += *dst;
-          *dst = last ? v * inv_g : v;
-          if (last && fz.sc_lds) sc_row[n - k_begin] = v * inv_g;
+          *dst = last ? v * out_scale : v;
+          if (last && fz.sc_lds) sc_row[n - k_begin] = v * out_scale;
         }
       }
     };
@@ -1073,10 +1072,10 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
 static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
 // Launch-shape tuning.  Defaults come from sweeps on MI355X; the
-// DROPKV_TUNE environment variable ("p1w=8,p1occ=1,p2w=4,s1=32,s2=32",
+// DROPKV_TUNE environment variable ("p1w=8,p1occ=1,s1=32,s2=32",
 // any subset) overrides them for experiments.
 struct Tune {
-  int p1w = 4, p1occ = 1, p2w = 8, s1 = 0, s2 = 0, target = 256, p1wide = 3, p1g = 1;
+  int p1w = 4, p1occ = 1, s1 = 0, s2 = 0, target = 256, p1wide = 3, p1g = 1;
 };
 static Tune read_tune() {
   Tune t;
@@ -1087,7 +1086,6 @@ static Tune read_tune() {
   while (sscanf(e, " %15[a-z0-9_]=%d%n", key, &val, &n) == 2) {
     if (!strcmp(key, "p1w")) t.p1w = val;
     else if (!strcmp(key, "p1occ")) t.p1occ = val;
-    else if (!strcmp(key, "p2w")) t.p2w = val;
     else if (!strcmp(key, "s1")) t.s1 = val;
     else if (!strcmp(key, "s2")) t.s2 = val;
     else if (!strcmp(key, "target")) t.target = val;
@@ -1111,7 +1109,7 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   p.mpad = p.n_mc * kRows;
   p.p1_waves = tune.p1w == 8 ? 8 : 4;
   p.p1_occ = tune.p1occ == 2 ? 2 : 1;
-  p.p2_waves = tune.p2w == 8 ? 8 : 4;
+  p.p2_waves = 8;
   const int target = max(1, tune.target);  // workgroups per pass (one per CU)
   const int max_by_work = max(1, (int)(Lk / 256));
   // Several row-chunks share each K/V tile in one workgroup (pass1w) from
@@ -1218,13 +1216,12 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
     lds2 = std::max(lds2, (size_t)kPoolLdsWords * 4);
   }
   const dim3 g2(p.heads * p.s2);
-  if (p.p2_waves == 8) {
-    launch((pass2_kernel<T, D, 8, 1>), g2, dim3(512), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M,
-                       p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, opblk, stblk, scores, fz);
-  } else {
-    launch((pass2_kernel<T, D, 4, 2>), g2, dim3(256), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M,
-                       p.n_mc, cg, p.s2, p.kps2, scale_log2, eps, p_round, opblk, stblk, scores, fz);
-  }
+  if (p_round)
+    launch((pass2_kernel<T, D, 8, 1, true>), g2, dim3(512), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc,
+           cg, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
+  else
+    launch((pass2_kernel<T, D, 8, 1, false>), g2, dim3(512), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc,
+           cg, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
   return hipGetLastError();
 }
 
