@@ -36,13 +36,16 @@ namespace dkv {
 constexpr int kTile = 32;           // keys per wave tile
 constexpr int kRows = 32;           // query rows per row-chunk (2 MFMA row blocks)
 constexpr int kMB = kRows / 16;
-// The fp32 attention output y enters pass 2's G^T = V Y^T as three bf16/fp16
-// MFMA operands y = hi + mid + lo (each the rounded remainder of the one
-// before), which carry its 24 significant bits: dist2 = |v|^2 - 2<v,y> + |y|^2
-// cancels heavily where one key takes almost all of a row's attention, so
-// <v,y> needs the precision of the fp32 y it approximates.
-constexpr int kYParts = 3;
+// The fp32 attention output y enters pass 2's G^T = V Y^T as two bf16/fp16
+// MFMA operands y = hi + lo (lo the rounded remainder), ~16 significant bits:
+// <v,y> then carries a relative error of ~2^-17 |v||y|, below 1e-4 of
+// dist2 = |v|^2 - 2<v,y> + |y|^2 wherever no key takes half of the row's
+// attention.  Where one does (p_k >= 1/2, at most one key per row), dist2 at
+// that key cancels heavily (y -> v_k), so the merge computes that one pair's
+// distance directly, |v_k - y|^2 from the fp32 y, and pass 2 uses it there.
+constexpr int kYParts = 2;
 constexpr int kOpSlots = 1 + kYParts;  // Q and the parts of Y, per row block and k-step
+constexpr int kStatWords = 64;         // per 16-row block: lse, |y|^2, sink key, -dist2/2 at it
 constexpr int kPitch = 18;          // dwords per row of the transposed V tile
 
 
@@ -612,9 +615,10 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
 // workgroup barrier.  Lane l owns head-dim columns l*DPL .. +DPL-1 and split
 // l's statistics; the split weights f_s = 2^(m_s - max_s m_s) are broadcast
 // with lane shuffles and the weighted partial y rows summed with every load
-// in flight.  Writes, for the score pass, the row's Q / Y-hi / Y-mid / Y-lo operands
+// in flight.  Writes, for the score pass, the row's Q / Y-hi / Y-lo operands
 // into the head's operand block (in the order pass 2's lanes read them from
-// LDS) and its statistics (lse in log2 units, |y|^2), plus an fp32 copy of y
+// LDS) and its statistics (lse in log2 units, |y|^2, the key holding at least
+// half of the row's attention if any, and -dist2/2 at that key), plus an fp32 copy of y
 // for inspection.  Optionally clears `zero_words` words at `zero_ptr` (the
 // selection workspace of a fused layer-call), so that needs no launch of its
 // own.
@@ -671,7 +675,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   // registers, any further ones re-read in the rare loops below).
   const float2 ml = lane < n_splits ? *reinterpret_cast<const float2*>(part_ml + ((slot0 + lane) * kRows + row) * 2)
                                     : make_float2(-INFINITY, 0.f);
-  const int arg_lane = (p_round && lane < n_splits) ? part_arg[(slot0 + lane) * kRows + row] : -1;
+  const int arg_lane = lane < n_splits ? part_arg[(slot0 + lane) * kRows + row] : -1;
   float mx = ml.x;
   for (int s = 64 + lane; s < n_splits; s += 64) mx = fmaxf(mx, part_ml[((slot0 + s) * kRows + row) * 2]);
   mx = wave_max(mx);
@@ -694,11 +698,12 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   // because |v_k - y| shrinks with 1 - p_k: without it, dist2 at that key is
   // wrong by up to tens of percent once p_k approaches 1.  Below p_k = 1/2
   // the term changes no distance by more than 0.5%, and the row skips the
-  // dependent load of v_k.
+  // dependent load of v_k.  The same top key (in every mode) gets its
+  // distance computed directly below.
   int k_top = -1;
   float dk = 0.f;
   fv vk = {};
-  if (p_round && valid) {
+  if (valid) {
     const float pk = fminf(__builtin_amdgcn_exp2f(mx - lse2), 1.f);
     if (pk >= 0.5f) {
       const uint64_t hit = __ballot(lane < n_splits && ml.x == mx);
@@ -712,10 +717,12 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
           }
       }
       if (k_top >= 0 && k_top < Lk) {
-        dk = round_through<T>(pk) - pk;
+        if (p_round) dk = round_through<T>(pk) - pk;
         const T* vrow = vp + ((int64_t)head * Lk + k_top) * D + d0;
 #pragma unroll
         for (int e = 0; e < DPL; ++e) vk[e] = static_cast<float>(vrow[e]);
+      } else {
+        k_top = -1;
       }
     }
   }
@@ -741,7 +748,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
     }
   }
 
-  float ysq = 0.f;
+  float ysq = 0.f, dsq = 0.f;
   const int64_t rbase = (int64_t)head * mpad + gr;
   T* ob = reinterpret_cast<T*>(opblk + ((int64_t)head * n_mc + mc) * OPS * 64);
   const int mb = row / 16, li = row % 16;
@@ -749,45 +756,40 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   for (int e = 0; e < DPL; ++e) {
     const int d = d0 + e;
     float y = valid ? acc[e] / l + dk * vk[e] : 0.f;
-    T hi, mid, lo;
-    if (y_round) {
-      hi = static_cast<T>(y);
-      y = static_cast<float>(hi);
-      mid = static_cast<T>(0.f);
-      lo = static_cast<T>(0.f);
-    } else {
-      hi = static_cast<T>(y);
-      const float r1 = y - static_cast<float>(hi);
-      mid = static_cast<T>(r1);
-      lo = static_cast<T>(r1 - static_cast<float>(mid));
-    }
+    const T hi = static_cast<T>(y);
+    if (y_round) y = static_cast<float>(hi);
+    const T lo = static_cast<T>(y - static_cast<float>(hi));
     ysq += y * y;
+    const float dv = vk[e] - y;
+    dsq += dv * dv;
     yf32[rbase * D + d] = y;
-    // Operand block of this head: per row-chunk, the Q, Y-hi, Y-mid and Y-lo
+    // Operand block of this head: per row-chunk, the Q, Y-hi and Y-lo
     // MFMA operands in per-lane order (slot (which, mb, kk), lane li + 16*lg,
     // element e8), so that pass 2 stages them with one contiguous copy.
     const int kk = d / 32, lg = (d % 32) / 8, e8 = d % 8;
     const int word = li + 16 * lg;
     ob[((size_t)((0 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = qv[e];
     ob[((size_t)((1 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = hi;
-    ob[((size_t)((2 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = mid;
-    ob[((size_t)((3 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = lo;
+    ob[((size_t)((2 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = lo;
   }
   const float yn2 = wave_sum(ysq);
+  const float nd2_top = -0.5f * wave_sum(dsq);
   if (lane == 0) {
     const float lse_row = valid ? lse2 : INFINITY;
     ystat[rbase * 2 + 0] = lse_row;
     ystat[rbase * 2 + 1] = yn2;
-    float* sb = stblk + ((int64_t)head * n_mc + mc) * kMB * 32 + (row / 16) * 32 + (row % 16);
+    float* sb = stblk + (((int64_t)head * n_mc + mc) * kMB + row / 16) * kStatWords + (row % 16);
     sb[0] = lse_row;
     sb[16] = yn2;
+    sb[32] = __builtin_bit_cast(float, k_top);
+    sb[48] = nd2_top;
   }
 }
 
 // ---------------------------------------------------------------------------
 // Pass 2: per-key score.  Workgroup = (head, key split); each of its WAVES
 // waves streams 32-key tiles, recomputes S^T = K Q^T and G^T = V Y^T (Y as
-// hi+mid+lo) and folds w * dist2 over all query rows.  The next tile's loads are
+// hi+lo) and folds w * dist2 over all query rows.  The next tile's loads are
 // issued right after the last MFMA of the current tile, overlapping the
 // per-element work.  The Q^T / Y^T operands of up to `cg` row-chunks are
 // staged in LDS in per-lane order (one conflict-free 16-byte read per
@@ -846,11 +848,11 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
              SelFuse fz) {
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
-  constexpr int OPS = kOpSlots * kMB * KK;  // operand slots per row-chunk (Q, Yhi, Ymid, Ylo)
+  constexpr int OPS = kOpSlots * kMB * KK;  // operand slots per row-chunk (Q, Yhi, Ylo)
   constexpr int NT = 64 * WAVES;
-  extern __shared__ u32x4 opnd[];    // [cg][OPS][64] then float stats [cg][kMB][2][16]
+  extern __shared__ u32x4 opnd[];    // [cg][OPS][64] then float stats [cg][kMB][kStatWords]
   float* stat = reinterpret_cast<float*>(opnd + (size_t)cg * OPS * 64);
-  float* sc_row = stat + cg * kMB * 32;  // [kps] this workgroup's scores (fused pooling only)
+  float* sc_row = stat + cg * kMB * kStatWords;  // [kps] this workgroup's scores (fused pooling only)
   // Top-digit histogram of the fused pooling (after sc_row), zeroed now.
   uint32_t* hist_l = reinterpret_cast<uint32_t*>(sc_row + kps);
   if (fz.enabled && fz.sc_lds)
@@ -884,9 +886,10 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
     // LDS order): issue their loads, then the first tile's K/V loads, so both
     // round trips overlap; the LDS writes wait only for the former.
     constexpr int SPW = (2 * OPS * 64 + NT - 1) / NT;
-    const int nw = cn * OPS * 64, ns = cn * kMB * 32;
+    const int nw = cn * OPS * 64, ns = cn * kMB * kStatWords;
+    static_assert(4 * kMB * kStatWords <= NT, "one statistics word per thread");
     const u32x4* gop = opblk + ((size_t)head * n_mc + c0) * OPS * 64;
-    const float* gst = stblk + ((size_t)head * n_mc + c0) * kMB * 32;
+    const float* gst = stblk + ((size_t)head * n_mc + c0) * kMB * kStatWords;
     u32x4 sv[SPW];
 #pragma unroll
     for (int i = 0; i < SPW; ++i) sv[i] = gop[min((int)threadIdx.x + i * NT, nw - 1)];
@@ -946,7 +949,7 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
         // <v,y> - (|v|^2 + |y|^2)/2 = -dist2/2 of every (key, row) pair.
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb) {
-          const float nyh = -0.5f * stat[(c * kMB + mb) * 32 + 16 + li];
+          const float nyh = -0.5f * stat[(c * kMB + mb) * kStatWords + 16 + li];
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb) {
             sacc[kb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -960,13 +963,11 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
           for (int kk = 0; kk < KK; ++kk) {
             const v8 qo = __builtin_bit_cast(v8, ob[(size_t)((0 * kMB + mb) * KK + kk) * 64]);
             const v8 yh = __builtin_bit_cast(v8, ob[(size_t)((1 * kMB + mb) * KK + kk) * 64]);
-            const v8 ym = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
-            const v8 yl = __builtin_bit_cast(v8, ob[(size_t)((3 * kMB + mb) * KK + kk) * 64]);
+            const v8 yl = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
               sacc[kb][mb] = Elem<T>::mfma(kop[kb][kk], qo, sacc[kb][mb]);
               gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], yh, gacc[kb][mb]);
-              gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], ym, gacc[kb][mb]);
               gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], yl, gacc[kb][mb]);
             }
           }
@@ -976,16 +977,24 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
           load_rows_op<T, D>(kop, krs, k_lane, tn);
           load_rows_op<T, D>(vop, vrs, k_lane, tn);
         }
-        // sc accumulates w * (-dist2/2); the causal bound is applied only in
-        // tiles that reach it (and with padding rows), so that the other
-        // tiles carry no per-element selects.
+        // sc accumulates w * (-dist2/2).  The causal bound, and the direct
+        // distance at a row's dominant key (merge), are applied only in
+        // tiles that reach the bound or hold such a key (and with padding
+        // rows), so that the other tiles carry no per-element selects.
+        const float* cst = stat + (size_t)c * kMB * kStatWords + li;
+        bool sink_here = false;
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb)
+          sink_here |= (uint32_t)(__builtin_bit_cast(int, cst[mb * kStatWords + 32]) - t0) < (uint32_t)kTile;
         auto epilogue = [&](auto masked_c) __attribute__((always_inline)) {
           constexpr bool kMasked = decltype(masked_c)::value;
 #pragma unroll
           for (int mb = 0; mb < kMB; ++mb) {
             const int m = (c0 + c) * kRows + mb * 16 + li;
             const int bound = kMasked ? row_bound(m, M, W, Lk) : 0;
-            const float lse2 = stat[(c * kMB + mb) * 32 + li];
+            const int skey = kMasked ? __builtin_bit_cast(int, cst[mb * kStatWords + 32]) : -1;
+            const float snd2 = kMasked ? cst[mb * kStatWords + 48] : 0.f;
+            const float lse2 = cst[mb * kStatWords];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -1001,13 +1010,14 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
                   const float ratio = p[e] * __builtin_amdgcn_rcpf(1.0f - p[e] + eps);
-                  const float nd2 = min_zero(gacc[kb][mb][r + e]);  // -dist2/2, dist2 clamped at 0
+                  float nd2 = min_zero(gacc[kb][mb][r + e]);  // -dist2/2, dist2 clamped at 0
+                  if (kMasked) nd2 = (t0 + 16 * kb + 4 * lg + r + e) == skey ? snd2 : nd2;
                   sc[kb][r + e] = fmaf(ratio * ratio, nd2, sc[kb][r + e]);
                 }
               }
           }
         };
-        if (masked)
+        if (masked || __any(sink_here))
           epilogue(std::true_type{});
         else
           epilogue(std::false_type{});
@@ -1137,7 +1147,7 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   p.off_y = take(slots * kRows * D * sizeof(float));
   p.off_arg = take(slots * kRows * sizeof(int));
   p.off_op = take((size_t)p.heads * p.n_mc * kOpSlots * kMB * (D / 32) * 64 * 16);
-  p.off_stb = take((size_t)p.heads * p.n_mc * kMB * 32 * sizeof(float));
+  p.off_stb = take((size_t)p.heads * p.n_mc * kMB * kStatWords * sizeof(float));
   p.off_stat = take((size_t)p.heads * p.mpad * 2 * sizeof(float));
   p.off_yf = take((size_t)p.heads * p.mpad * D * sizeof(float));
   p.total = off;
@@ -1204,7 +1214,7 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   // divide n_mc (as pairs of the two-chunk body: unrolling four chunks pushes
   // pass 2 into register spills), else up to two.
   const int cg = (p.n_mc % 4 == 0) ? 4 : min(p.n_mc, 2);
-  size_t lds2 = (size_t)cg * kOpSlots * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * 32 * sizeof(float);
+  size_t lds2 = (size_t)cg * kOpSlots * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * kStatWords * sizeof(float);
   if (fuse) {
     fz.enabled = 1;
     fz.ws = sel_layout(fuse->ws, p.heads, Lk, nullptr);
