@@ -46,6 +46,12 @@ _SIGNATURES = {
                               _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                               _c_float, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
                               _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
+    "dropkv_evict_ld": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_int,
+                                 _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                 _c_float, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
+                                 _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp, _c_size, _c_vp]),
+    "dropkv_append": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                               _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "dropkv_timing_enable": (_c_int, [_c_int]),
     "dropkv_timing_read": (_c_int, [ctypes.POINTER(ctypes.c_double), _c_int]),
     "dropkv_selftest_mfma": (_c_int, [_c_vp, _c_vp]),

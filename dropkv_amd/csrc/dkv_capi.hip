@@ -119,8 +119,8 @@ int dropkv_scores(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64
   if (!workspace || workspace_bytes < p.total)
     return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", p.total, workspace_bytes);
   timing_start(static_cast<hipStream_t>(stream));
-  return hip_status(dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Hkv,
-                                       (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, scores,
+  return hip_status(dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Lk,
+                                       (int)Hkv, (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, scores,
                                        static_cast<char*>(workspace), nullptr, 0, nullptr,
                                        static_cast<hipStream_t>(stream)),
                     "dropkv_scores launch");
@@ -217,17 +217,22 @@ size_t dropkv_evict_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t 
   return a + s + dkv::select_workspace_bytes(B * Hkv, Lk);
 }
 
-int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const void* k, const void* v,
-                 int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D, int64_t W,
-                 float eps, int p_round, int y_round, int64_t splits, int64_t kernel_size, int64_t protect_window,
-                 int64_t keep, float* scores, int64_t* keep_idx, void* k_out, void* v_out, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+
+// One layer-call on K/V of [B*Hkv, kv_ld, D] (rows 0 .. Lk-1 used) into
+// outputs of [B*Hkv, out_ld, D] (rows 0 .. keep-1 written).
+static int evict_impl(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const void* k, const void* v,
+               int64_t kv_ld, int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D,
+               int64_t W, float eps, int p_round, int y_round, int64_t splits, int64_t kernel_size,
+               int64_t protect_window, int64_t keep, float* scores, int64_t* keep_idx, void* k_out, void* v_out,
+               int64_t out_ld, void* workspace, size_t workspace_bytes, void* stream) {
   (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
   int rc = check_score_args(q, k, v, dtype, B, Hq, Hkv, Lq, Lk, D, W);
   if (rc) return rc;
   rc = check_select_args(reinterpret_cast<const float*>(1), B * Hkv, Lk, kernel_size, protect_window, keep, keep_idx);
   if (rc) return rc;
   if (!k_out || !v_out) return fail(DROPKV_E_ARG, "null k_out/v_out pointer");
+  if (kv_ld < Lk || out_ld < keep) return fail(DROPKV_E_ARG, "row capacity below the rows used");
+  if (kv_ld > INT32_MAX) return fail(DROPKV_E_UNSUPPORTED, "row capacity too large");
   const dkv::ScorePlan p = dkv::make_score_plan(B, Hq, Hkv, Lk, D, W, splits);
   const size_t s_bytes = ((size_t)B * Hkv * Lk * 4 + 255) & ~size_t(255);
   const size_t need = p.total + s_bytes + dkv::select_workspace_bytes(B * Hkv, Lk);
@@ -236,19 +241,21 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
   char* ws = static_cast<char*>(workspace);
   float* sc = scores ? scores : reinterpret_cast<float*>(ws + p.total);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  timing_start(st);
   char* sel_ws = ws + p.total + s_bytes;
   // The gather runs inside the selection's emit stage when the rows allow
-  // 16-byte copies; otherwise as its own kernel.
+  // 16-byte copies; otherwise as its own kernel (contiguous outputs only).
   const bool vec = (D * 2) % 16 == 0 && aligned16(k_out) && aligned16(v_out);
-  const dkv::SelectCompact cp{k, v, Hkv * Lk * D, Lk * D, D, 2, D, (int)Hkv, k_out, v_out};
+  if (!vec && out_ld != keep)
+    return fail(DROPKV_E_UNSUPPORTED, "outputs with a row capacity need 16-byte aligned rows");
+  timing_start(st);
+  const dkv::SelectCompact cp{k, v, Hkv * kv_ld * D, kv_ld * D, D, 2, D, (int)Hkv, k_out, v_out, out_ld};
   // Pooling runs in the tail of the scoring pass when the plan allows it;
   // otherwise as the standalone selection's pool kernel.
   const bool fused = dkv::select_after_pool_ok(p.s2, p.kps2, Lk, kernel_size);
   const dkv::FuseSelect fs{sel_ws, (int)kernel_size, (int)protect_window};
-  hipError_t e = dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Hkv,
-                                    (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws,
-                                    reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv),
+  hipError_t e = dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)kv_ld,
+                                    (int)Hkv, (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc,
+                                    ws, reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv),
                                     fused ? &fs : nullptr, st);
   if (e != hipSuccess) return hip_status(e, "dropkv_evict scores");
   if (fused)
@@ -259,9 +266,46 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
                            nullptr, sel_ws, true, vec ? &cp : nullptr, st);
   if (e != hipSuccess) return hip_status(e, "dropkv_evict select");
   if (vec) return DROPKV_OK;
-  e = dkv::launch_compact(k, v, Hkv * Lk * D, Lk * D, D, Lk, nullptr, nullptr, 0, 0, 0, 0, 2, B, Hkv, D, keep_idx,
-                          keep, k_out, v_out, st);
+  e = dkv::launch_compact(k, v, Hkv * kv_ld * D, kv_ld * D, D, Lk, nullptr, nullptr, 0, 0, 0, 0, 2, B, Hkv, D,
+                          keep_idx, keep, k_out, v_out, st);
   return hip_status(e, "dropkv_evict compact");
+}
+
+int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const void* k, const void* v,
+                 int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D, int64_t W,
+                 float eps, int p_round, int y_round, int64_t splits, int64_t kernel_size, int64_t protect_window,
+                 int64_t keep, float* scores, int64_t* keep_idx, void* k_out, void* v_out, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  return evict_impl(q, q_sb, q_sh, q_ss, q_sd, k, v, Lk, dtype, B, Hq, Hkv, Lq, Lk, D, W, eps, p_round, y_round,
+                    splits, kernel_size, protect_window, keep, scores, keep_idx, k_out, v_out, keep, workspace,
+                    workspace_bytes, stream);
+}
+
+int dropkv_evict_ld(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const void* k,
+                    const void* v, int64_t kv_ld, int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq,
+                    int64_t Lk, int64_t D, int64_t W, float eps, int p_round, int y_round, int64_t splits,
+                    int64_t kernel_size, int64_t protect_window, int64_t keep, float* scores, int64_t* keep_idx,
+                    void* k_out, void* v_out, int64_t out_ld, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  return evict_impl(q, q_sb, q_sh, q_ss, q_sd, k, v, kv_ld, dtype, B, Hq, Hkv, Lq, Lk, D, W, eps, p_round, y_round,
+                    splits, kernel_size, protect_window, keep, scores, keep_idx, k_out, v_out, out_ld, workspace,
+                    workspace_bytes, stream);
+}
+
+int dropkv_append(const void* k, const void* v, int64_t s_b, int64_t s_h, int64_t s_l, int64_t elem_bytes,
+                  int64_t B, int64_t H, int64_t L, int64_t D, void* k_dst, void* v_dst, int64_t dst_ld, int64_t row0,
+                  void* stream) {
+  (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8)
+    return fail(DROPKV_E_ARG, "elem_bytes must be 1, 2, 4 or 8");
+  if (B < 0 || H < 0 || L < 0 || D < 1 || row0 < 0) return fail(DROPKV_E_ARG, "invalid shape");
+  if (row0 + L > dst_ld) return fail(DROPKV_E_ARG, "rows %lld..%lld do not fit a capacity of %lld", (long long)row0,
+                                     (long long)(row0 + L), (long long)dst_ld);
+  if (L > 0 && B * H > 0 && (!k || !v || !k_dst || !v_dst)) return fail(DROPKV_E_ARG, "null pointer");
+  timing_start(static_cast<hipStream_t>(stream));
+  return hip_status(dkv::launch_append(k, v, s_b, s_h, s_l, elem_bytes, B, H, L, D, k_dst, v_dst, dst_ld, row0,
+                                       static_cast<hipStream_t>(stream)),
+                    "dropkv_append launch");
 }
 
 int dropkv_timing_enable(int on) {

@@ -68,6 +68,68 @@ compact_kernel(Seg s0, Seg s1, int H, int units_per_row, const int64_t* __restri
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Append: rows 0 .. L-1 of each head of src to rows row0 .. of the head in a
+// [B*H, dst_ld, D] buffer.  kRowsPerBlock rows per workgroup, kItems pieces
+// per thread with every load in flight before the stores.
+template <typename U>
+__global__ void __launch_bounds__(kCopyThreads)
+append_kernel(Seg s, int H, int units_per_row, int L, int blocks_per_head, uint8_t* __restrict__ dk,
+              uint8_t* __restrict__ dv, int64_t dst_ld, int64_t row0) {
+  const int bh = blockIdx.x / blocks_per_head;
+  const int r0 = (blockIdx.x % blocks_per_head) * kRowsPerBlock;
+  const int b = bh / H, h = bh % H;
+  const int64_t row_bytes = (int64_t)units_per_row * sizeof(U);
+  const int total = min(kRowsPerBlock, L - r0) * units_per_row;
+  for (int t0 = threadIdx.x; t0 < total; t0 += kItems * kCopyThreads) {
+    U kval[kItems], vval[kItems];
+#pragma unroll
+    for (int q = 0; q < kItems; ++q) {
+      const int t = t0 + q * kCopyThreads;
+      if (t < total) {
+        const int64_t off = b * s.sb + h * s.sh + (int64_t)(r0 + t / units_per_row) * s.sl;
+        kval[q] = reinterpret_cast<const U*>(s.k + off)[t % units_per_row];
+        vval[q] = reinterpret_cast<const U*>(s.v + off)[t % units_per_row];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kItems; ++q) {
+      const int t = t0 + q * kCopyThreads;
+      if (t < total) {
+        const int64_t o = ((int64_t)bh * dst_ld + row0 + r0 + t / units_per_row) * row_bytes;
+        reinterpret_cast<U*>(dk + o)[t % units_per_row] = kval[q];
+        reinterpret_cast<U*>(dv + o)[t % units_per_row] = vval[q];
+      }
+    }
+  }
+}
+
+hipError_t launch_append(const void* k, const void* v, int64_t s_b, int64_t s_h, int64_t s_l, int64_t eb, int64_t B,
+                         int64_t H, int64_t L, int64_t D, void* dk, void* dv, int64_t dst_ld, int64_t row0,
+                         hipStream_t st) {
+  if (L <= 0 || B * H == 0) return hipSuccess;
+  const Seg a{static_cast<const uint8_t*>(k), static_cast<const uint8_t*>(v), s_b * eb, s_h * eb, s_l * eb, L};
+  const int64_t row_bytes = D * eb;
+  const bool vec = (row_bytes % 16) == 0 && aligned16(dk) && aligned16(dv) && aligned16(k) && aligned16(v) &&
+                   (a.sb % 16) == 0 && (a.sh % 16) == 0 && (a.sl % 16) == 0;
+  const int bph = (int)((L + kRowsPerBlock - 1) / kRowsPerBlock);
+  const dim3 grid((unsigned)(B * H * bph));
+  uint8_t* k8 = static_cast<uint8_t*>(dk);
+  uint8_t* v8 = static_cast<uint8_t*>(dv);
+  if (vec)
+    launch(append_kernel<uint4>, grid, dim3(kCopyThreads), 0, st, a, (int)H, (int)(row_bytes / 16), (int)L, bph, k8,
+           v8, dst_ld, row0);
+  else if (eb == 2)
+    launch(append_kernel<uint16_t>, grid, dim3(kCopyThreads), 0, st, a, (int)H, (int)D, (int)L, bph, k8, v8, dst_ld,
+           row0);
+  else if (eb == 4)
+    launch(append_kernel<uint32_t>, grid, dim3(kCopyThreads), 0, st, a, (int)H, (int)D, (int)L, bph, k8, v8, dst_ld,
+           row0);
+  else
+    launch(append_kernel<uint8_t>, grid, dim3(kCopyThreads), 0, st, a, (int)H, (int)row_bytes, (int)L, bph, k8, v8,
+           dst_ld, row0);
+  return hipGetLastError();
+}
+
 hipError_t launch_compact(const void* k0, const void* v0, int64_t s0b, int64_t s0h, int64_t s0l, int64_t L0,
                           const void* k1, const void* v1, int64_t s1b, int64_t s1h, int64_t s1l, int64_t L1,
                           int64_t eb, int64_t B, int64_t H, int64_t D, const int64_t* idx, int64_t keep, void* ko,

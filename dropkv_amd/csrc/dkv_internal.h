@@ -45,10 +45,11 @@ struct FuseSelect {
   char* ws;
   int ks, window;
 };
+// K/V: [B*Hkv, kv_ld, D] with rows 0 .. Lk-1 of each head used (kv_ld = Lk: contiguous).
 hipError_t launch_scores(const ScorePlan& p, int dtype_bf16, int D, const void* q, int64_t q_sb, int64_t q_sh,
-                         int64_t q_ss, int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk, int W,
-                         float eps, int p_round, int y_round, float* scores, char* ws, uint32_t* zero_ptr,
-                         int64_t zero_words, const FuseSelect* fuse, hipStream_t st);
+                         int64_t q_ss, int64_t q_sd, const void* k, const void* v, int kv_ld, int Hkv, int Lq,
+                         int Lk, int W, float eps, int p_round, int y_round, float* scores, char* ws,
+                         uint32_t* zero_ptr, int64_t zero_words, const FuseSelect* fuse, hipStream_t st);
 hipError_t launch_debug_state(const ScorePlan& p, const char* ws, int D, float* lse_out, float* y_out,
                               hipStream_t st);
 hipError_t launch_mfma_selftest(float* out, hipStream_t st);
@@ -90,6 +91,7 @@ struct SelectCompact {
   int H;
   void* k_out;
   void* v_out;
+  int64_t out_ld;  // rows per head in k_out / v_out ([B, H, out_ld, D]; keep: contiguous)
 };
 hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int window, int keep, int64_t* out_idx,
                          float* pooled_out, char* ws, bool pre_zeroed, const SelectCompact* cp, hipStream_t st);
@@ -100,6 +102,12 @@ hipError_t launch_select_after_pool(const float* scores, int rows, int Lk, int k
                                     const SelectCompact* cp, hipStream_t st);
 // Whether launch_select_after_pool accepts that geometry.
 bool select_after_pool_ok(int64_t n_splits, int64_t kps, int64_t Lk, int64_t ks);
+
+// Rows 0 .. L-1 of src ([B, H, L, D], element strides s_b, s_h, s_l, D
+// contiguous) to rows row0 .. row0+L-1 of dst ([B, H, dst_ld, D] contiguous).
+hipError_t launch_append(const void* k, const void* v, int64_t s_b, int64_t s_h, int64_t s_l, int64_t eb, int64_t B,
+                         int64_t H, int64_t L, int64_t D, void* dk, void* dv, int64_t dst_ld, int64_t row0,
+                         hipStream_t st);
 
 hipError_t launch_compact(const void* k0, const void* v0, int64_t s0b, int64_t s0h, int64_t s0l, int64_t L0,
                           const void* k1, const void* v1, int64_t s1b, int64_t s1h, int64_t s1l, int64_t L1,

@@ -208,7 +208,7 @@ __device__ __forceinline__ void load_v_pairs(u32x4 (&va)[(kTile / 2) / (64 / (D 
 template <typename T, int D, int WAVES, int MINW, int PS>
 __global__ void __launch_bounds__(64 * WAVES, MINW)
 pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
-             const T* __restrict__ kp, const T* __restrict__ vp,
+             const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int n_splits, int kps,
              float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y,
              int* __restrict__ part_arg) {
@@ -249,7 +249,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 
   const int k_begin = split * kps;
   const int k_end = min(k_begin + kps, Lk);
-  const int64_t roff = ((int64_t)head * Lk + k_begin) * D;
+  const int64_t roff = ((int64_t)head * kv_ld + k_begin) * D;
   const uint32_t range = (uint32_t)(k_end - k_begin) * (D * sizeof(T));
   const rsrc_t krs = make_rsrc(kp + roff, range), vrs = make_rsrc(vp + roff, range);
   const uint32_t k_lane = (li * D + 8 * lg) * sizeof(T);
@@ -436,7 +436,7 @@ constexpr int kWideWaves = 8;
 template <typename T, int D, int PS, int kWideG>
 __global__ void __launch_bounds__(64 * kWideWaves, 1)
 pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
-              const T* __restrict__ kp, const T* __restrict__ vp,
+              const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
               int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int n_splits, int kps,
               float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y,
               int* __restrict__ part_arg) {
@@ -478,7 +478,7 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
 
   const int k_begin = split * kps;
   const int k_end = min(k_begin + kps, Lk);
-  const int64_t roff = ((int64_t)head * Lk + k_begin) * D;
+  const int64_t roff = ((int64_t)head * kv_ld + k_begin) * D;
   const uint32_t range = (uint32_t)(k_end - k_begin) * (D * sizeof(T));
   const rsrc_t krs = make_rsrc(kp + roff, range), vrs = make_rsrc(vp + roff, range);
   // This thread's share of a tile: K chunk tid (row tid / CPR, chunk tid % CPR)
@@ -630,7 +630,7 @@ template <typename T, int D>
 __global__ void __launch_bounds__(64 * kMergeRows)
 merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y, const int* __restrict__ part_arg,
              int n_mc, int n_splits, int M, int n_rows, int p_round, int y_round, const T* __restrict__ q,
-             int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const T* __restrict__ vp, int Lk,
+             int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const T* __restrict__ vp, int kv_ld, int Lk,
              int Hkv, int g, int W, int Lq, u32x4* __restrict__ opblk, float* __restrict__ stblk,
              float* __restrict__ ystat, float* __restrict__ yf32, uint32_t* __restrict__ zero_ptr,
              int64_t zero_words) {
@@ -718,7 +718,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
       }
       if (k_top >= 0 && k_top < Lk) {
         if (p_round) dk = round_through<T>(pk) - pk;
-        const T* vrow = vp + ((int64_t)head * Lk + k_top) * D + d0;
+        const T* vrow = vp + ((int64_t)head * kv_ld + k_top) * D + d0;
 #pragma unroll
         for (int e = 0; e < DPL; ++e) vk[e] = static_cast<float>(vrow[e]);
       } else {
@@ -841,7 +841,7 @@ constexpr int kScLds = 4096;  // longest split range whose scores pass 2 keeps i
 
 template <typename T, int D, int WAVES, int MINW, bool PR>
 __global__ void __launch_bounds__(64 * WAVES, MINW)
-pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
+pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int cg, int n_splits, int kps,
              float scale_log2, float eps,
              const u32x4* __restrict__ opblk, const float* __restrict__ stblk, float* __restrict__ scores,
@@ -869,7 +869,7 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp,
   const float out_scale = -2.0f * (1.0f / static_cast<float>(g));
   const int k_begin = split * kps;
   const int k_end = min(k_begin + kps, Lk);
-  const int64_t roff = ((int64_t)head * Lk + k_begin) * D;
+  const int64_t roff = ((int64_t)head * kv_ld + k_begin) * D;
   const uint32_t range = (uint32_t)(k_end - k_begin) * (D * sizeof(T));
   const rsrc_t krs = make_rsrc(kp + roff, range), vrs = make_rsrc(vp + roff, range);
   const uint32_t k_lane = (li * D + 8 * lg) * sizeof(T);
@@ -1156,8 +1156,8 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
 
 template <typename T, int D>
 static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
-                                  int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk, int W,
-                                  float eps, int p_round, int y_round, float* scores, char* ws,
+                                  int64_t q_sd, const void* k, const void* v, int kv_ld, int Hkv, int Lq, int Lk,
+                                  int W, float eps, int p_round, int y_round, float* scores, char* ws,
                                   uint32_t* zero_ptr, int64_t zero_words, const FuseSelect* fuse, hipStream_t st) {
   const float scale_log2 = 1.4426950408889634f / sqrtf((float)D);
   float* part_ml = reinterpret_cast<float*>(ws + p.off_ml);
@@ -1180,7 +1180,7 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
       auto wide = [&](auto grp) {
         constexpr int G = decltype(grp)::value;
         launch((pass1w_kernel<T, D, PS, G>), dim3(p.heads * p.s1), dim3(64 * kWideWaves), 0, st, qq,
-                           q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1,
+                           q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1,
                            scale_log2, part_ml, part_y, part_arg);
       };
       if (p.p1_wide == 4)
@@ -1191,13 +1191,16 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
         wide(std::integral_constant<int, 1>{});
     } else if (p.p1_waves == 8) {
       launch((pass1_kernel<T, D, 8, 1, PS>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
-                         vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
+                         vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y,
+                         part_arg);
     } else if (p.p1_occ == 1) {
       launch((pass1_kernel<T, D, 4, 1, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
-                         vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
+                         vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y,
+                         part_arg);
     } else {
       launch((pass1_kernel<T, D, 4, 2, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
-                         vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_arg);
+                         vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y,
+                         part_arg);
     }
   };
   if (p_round)
@@ -1207,7 +1210,7 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   const int n_rows = p.heads * p.mpad;
   launch((merge_kernel<T, D>), dim3((n_rows + kMergeRows - 1) / kMergeRows), dim3(64 * kMergeRows), 0, st,
                      part_ml, part_y, part_arg, p.n_mc, p.s1, p.M, n_rows, p_round, y_round, qq, q_sb, q_sh, q_ss,
-                     q_sd, vv, Lk, Hkv, p.g, W, Lq, opblk, stblk, ystat, yf, zero_ptr, zero_words);
+                     q_sd, vv, kv_ld, Lk, Hkv, p.g, W, Lq, opblk, stblk, ystat, yf, zero_ptr, zero_words);
   SelFuse fz{};
   // Row-chunks whose operands share LDS in one sweep over the keys (every
   // further group streams the workgroup's K/V range again): four when they
@@ -1227,20 +1230,21 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   }
   const dim3 g2(p.heads * p.s2);
   if (p_round)
-    launch((pass2_kernel<T, D, 8, 1, true>), g2, dim3(512), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc,
+    launch((pass2_kernel<T, D, 8, 1, true>), g2, dim3(512), lds2, st, kk, vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc,
            cg, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
   else
-    launch((pass2_kernel<T, D, 8, 1, false>), g2, dim3(512), lds2, st, kk, vv, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc,
+    launch((pass2_kernel<T, D, 8, 1, false>), g2, dim3(512), lds2, st, kk, vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc,
            cg, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
   return hipGetLastError();
 }
 
 hipError_t launch_scores(const ScorePlan& p, int dtype_bf16, int D, const void* q, int64_t q_sb, int64_t q_sh,
-                         int64_t q_ss, int64_t q_sd, const void* k, const void* v, int Hkv, int Lq, int Lk,
-                         int W, float eps, int p_round, int y_round, float* scores, char* ws, uint32_t* zero_ptr,
-                         int64_t zero_words, const FuseSelect* fuse, hipStream_t st) {
-#define DKV_CASE(TT, DD)                                                                                     \
-  return launch_scores_t<TT, DD>(p, q, q_sb, q_sh, q_ss, q_sd, k, v, Hkv, Lq, Lk, W, eps, p_round, y_round, \
+                         int64_t q_ss, int64_t q_sd, const void* k, const void* v, int kv_ld, int Hkv, int Lq,
+                         int Lk, int W, float eps, int p_round, int y_round, float* scores, char* ws,
+                         uint32_t* zero_ptr, int64_t zero_words, const FuseSelect* fuse, hipStream_t st) {
+#define DKV_CASE(TT, DD)                                                                                   \
+  return launch_scores_t<TT, DD>(p, q, q_sb, q_sh, q_ss, q_sd, k, v, kv_ld, Hkv, Lq, Lk, W, eps, p_round, \
+                                 y_round, \
                                  scores, ws, zero_ptr, zero_words, fuse, st)
   if (dtype_bf16) {
     if (D == 64) DKV_CASE(__bf16, 64);

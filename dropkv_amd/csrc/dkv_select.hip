@@ -180,6 +180,7 @@ struct CompactArgs {
   int units;           // 16-byte units per row
   uint8_t* ko;
   uint8_t* vo;
+  int64_t out_ld;      // rows per head in ko / vo
 };
 
 constexpr int kEmitCandLds = 4096;                  // candidates held in LDS (more: read from global)
@@ -435,7 +436,7 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, int spec, SelWs ws, in
       for (int q = 0; q < kG; ++q) {
         const int t = t0 + q * kSelT;
         if (t < total) {
-          const int64_t o = ((int64_t)row * keep + s_dst[t / ca.units]) * ca.units * 16 + 16 * (t % ca.units);
+          const int64_t o = ((int64_t)row * ca.out_ld + s_dst[t / ca.units]) * ca.units * 16 + 16 * (t % ca.units);
           *reinterpret_cast<u32x4*>(ca.ko + o) = kv[q];
           *reinterpret_cast<u32x4*>(ca.vo + o) = vv[q];
         }
@@ -469,6 +470,7 @@ static CompactArgs compact_args(const SelectCompact* cp) {
     ca.units = (int)(cp->D * cp->elem_bytes / 16);
     ca.ko = static_cast<uint8_t*>(cp->k_out);
     ca.vo = static_cast<uint8_t*>(cp->v_out);
+    ca.out_ld = cp->out_ld;
   }
   return ca;
 }

@@ -97,10 +97,20 @@ def _deployed_path_scores(query_states, key_states, value_states, window_size: i
 
 class DropKVCache(_LayerCache):
     """KV cache that evicts at prefill by the DropKV score
-    (dropkv_cache.py:310-648)."""
+    (dropkv_cache.py:310-648).
+
+    ``capacity`` (not in the reference): keep each layer's K/V in two
+    preallocated buffer pairs of ``capacity`` rows per head instead of
+    concatenating and gathering into new tensors.  A chunk is appended in
+    place after the stored rows, the model attends over that buffer's first
+    rows (a view), and an eviction gathers from it straight into the other
+    pair's first rows (``dropkv_evict_ld``).  The stored and returned K/V are
+    bit for bit those of the default mode; ``capacity`` must cover the
+    largest stored-plus-chunk length, decode steps included, or ``update``
+    raises ``ValueError``.  The stored tensors are views of the buffers."""
 
     def __init__(self, keep_ratio: float = 0.1, window_size: int = 8, kernel_size: int = 11,
-                 use_triton: bool = True) -> None:
+                 use_triton: bool = True, capacity: Optional[int] = None) -> None:
         super().__init__()
         if not 0 < keep_ratio <= 1.0:
             raise ValueError(f"keep_ratio must be in (0, 1], got {keep_ratio}")
@@ -116,6 +126,11 @@ class DropKVCache(_LayerCache):
         self._prefill_mode = "single_pass"
         self._evict_use_seen_tokens = False
         self._budget_max_kv_tokens: Optional[int] = None
+        if capacity is not None and int(capacity) < 1:
+            raise ValueError(f"capacity must be a positive number of rows, got {capacity}")
+        self.capacity = None if capacity is None else int(capacity)
+        self._buf: list = []  # capacity mode, per layer: [k0, v0, k1, v1]
+        self._cur: list = []  # capacity mode, per layer: the pair holding the stored rows
 
     def batch_split(self, full_batch_size: int, split_size: int):
         raise NotImplementedError(
@@ -202,7 +217,9 @@ class DropKVCache(_LayerCache):
 
         if len(self.key_cache) < layer_idx:
             raise ValueError("Use DynamicCache.")
-        elif len(self.key_cache) == layer_idx:
+        if self.capacity is not None:
+            return self._update_capacity(query_states, key_states, value_states, layer_idx)
+        if len(self.key_cache) == layer_idx:
             # --- prefill ---
             if query_states is None:
                 if self._prefill_mode != "single_pass":
@@ -254,6 +271,127 @@ class DropKVCache(_LayerCache):
             self.value_cache[layer_idx] = torch.cat([self.value_cache[layer_idx], value_states], dim=-2)
             return self.key_cache[layer_idx], self.value_cache[layer_idx]
         raise ValueError(f"Invalid _prefill_mode {self._prefill_mode!r} in decode path")
+
+    # -- capacity mode ---------------------------------------------------------
+    def _alloc(self, layer_idx: int, like: torch.Tensor) -> None:
+        B, H, _, D = like.shape
+        shape = (B, H, self.capacity, D)
+        if layer_idx < len(self._buf):
+            b = self._buf[layer_idx][0]
+            if b.shape == shape and b.dtype == like.dtype and b.device == like.device:
+                self._cur[layer_idx] = 0
+                return
+        bufs = [torch.empty(shape, dtype=like.dtype, device=like.device) for _ in range(4)]
+        if layer_idx < len(self._buf):
+            self._buf[layer_idx], self._cur[layer_idx] = bufs, 0
+        else:
+            self._buf.append(bufs)
+            self._cur.append(0)
+
+    def _pair(self, layer_idx: int, which: Optional[int] = None):
+        i = self._cur[layer_idx] if which is None else which
+        b = self._buf[layer_idx]
+        return b[2 * i], b[2 * i + 1]
+
+    def _set_stored(self, layer_idx: int, n: int) -> None:
+        k, v = self._pair(layer_idx)
+        kv, vv = k[:, :, :n], v[:, :, :n]
+        if len(self.key_cache) == layer_idx:
+            self.key_cache.append(kv)
+            self.value_cache.append(vv)
+        else:
+            self.key_cache[layer_idx] = kv
+            self.value_cache[layer_idx] = vv
+
+    def _fits(self, layer_idx: int, rows: int) -> None:
+        if rows > self.capacity:
+            raise ValueError(f"DropKVCache capacity of {self.capacity} rows exceeded at layer {layer_idx}: "
+                             f"{rows} rows needed")
+
+    def _evict_into(self, query_states, k_src, v_src, Lk: int, k_out, v_out) -> int:
+        """Eviction of rows 0 .. Lk-1 of k_src / v_src ([B, Hkv, ld, D]) into
+        the first rows of k_out / v_out; the same scoring choice, keep length
+        and protection as _compute_keep_indices.  Returns the keep length."""
+        if query_states.shape[1] % k_src.shape[1] != 0:
+            raise ValueError(f"Query heads {query_states.shape[1]} must be divisible by KV heads {k_src.shape[1]}")
+        fast = False
+        if self.use_triton:
+            try:
+                from .dropkv_triton import check_scoring_inputs
+                check_scoring_inputs(query_states, k_src[:, :, :Lk], v_src[:, :, :Lk], self.window_size,
+                                     require_contiguous=False)
+                fast = True
+            except AssertionError:
+                fast = False
+        W = self.window_size if fast else min(self.window_size, query_states.shape[2])
+        total_tok = self._seen_tokens if self._evict_use_seen_tokens else None
+        keep = self._keep_length(Lk, total_tok, self._budget_max_kv_tokens)
+        ops.evict_ld(query_states, k_src, v_src, Lk, W, self.kernel_size, keep, k_out, v_out,
+                     protect_window=min(self.window_size, Lk), p_round=True, y_round=not fast)
+        return keep
+
+    def _update_capacity(self, query_states, key_states, value_states, layer_idx: int):
+        """update() in capacity mode: the control flow of the default mode,
+        with appends into and gathers between the layer's buffers."""
+        L = key_states.shape[2]
+        if len(self.key_cache) == layer_idx:
+            # --- prefill ---
+            self._alloc(layer_idx, key_states)
+            store_all = query_states is None
+            if store_all:
+                if self._prefill_mode != "single_pass":
+                    logger.warning("query_states is None at layer %d — storing full KV without eviction.",
+                                   layer_idx)
+            else:
+                if self._prefill_mode not in ("single_pass", "accumulate", "evict_accumulated"):
+                    raise ValueError(f"Invalid _prefill_mode: {self._prefill_mode!r}")
+                store_all = self._prefill_mode == "accumulate" or L < self.window_size
+            if store_all:
+                self._fits(layer_idx, L)
+                k, v = self._pair(layer_idx)
+                ops.append(key_states, value_states, k, v, 0)
+                self._set_stored(layer_idx, L)
+                return key_states, value_states
+            src_k, src_v = key_states.contiguous(), value_states.contiguous()
+            if src_k.data_ptr() % 16 or src_v.data_ptr() % 16:
+                src_k, src_v = src_k.clone(), src_v.clone()
+            k, v = self._pair(layer_idx)
+            keep = self._evict_into(query_states, src_k, src_v, L, k, v)
+            self._set_stored(layer_idx, keep)
+            return key_states, value_states
+
+        # --- decode / chunked-prefill continuation ---
+        if self._prefill_mode not in ("single_pass", "accumulate", "evict_accumulated"):
+            raise ValueError(f"Invalid _prefill_mode {self._prefill_mode!r} in decode path")
+        n = self.key_cache[layer_idx].shape[2]
+        self._fits(layer_idx, n + L)
+        k, v = self._pair(layer_idx)
+        ops.append(key_states, value_states, k, v, n)
+        full_k, full_v = k[:, :, :n + L], v[:, :, :n + L]
+        if (self._prefill_mode == "evict_accumulated" and query_states is not None
+                and n + L >= self.window_size):
+            other = 1 - self._cur[layer_idx]
+            ko, vo = self._pair(layer_idx, other)
+            keep = self._evict_into(query_states, k, v, n + L, ko, vo)
+            self._cur[layer_idx] = other
+            self._set_stored(layer_idx, keep)
+        else:
+            self._set_stored(layer_idx, n + L)
+        return full_k, full_v
+
+    def reorder_cache(self, beam_idx: torch.LongTensor):
+        if self.capacity is None:
+            return super().reorder_cache(beam_idx)
+        for i in range(len(self.key_cache)):
+            n = self.key_cache[i].shape[2]
+            k, v = self._pair(i)
+            other = 1 - self._cur[i]
+            ko, vo = self._pair(i, other)
+            sel = beam_idx.to(k.device)
+            ko[:, :, :n].copy_(k[:, :, :n].index_select(0, sel))
+            vo[:, :, :n].copy_(v[:, :, :n].index_select(0, sel))
+            self._cur[i] = other
+            self._set_stored(i, n)
 
     def get_seq_length(self, layer_idx: Optional[int] = 0) -> int:
         """Logical length (tokens seen) for RoPE positions (dropkv_cache.py:624-633)."""

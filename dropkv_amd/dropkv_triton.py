@@ -40,9 +40,12 @@ def _compute_num_splits(B: int, Hkv: int, L: int, BLOCK_N: int, device) -> int:
     return max(1, min(wanted, max(1, total_tiles // 4), 64))
 
 
-def check_scoring_inputs(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, window_size: int) -> None:
+def check_scoring_inputs(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, window_size: int,
+                         require_contiguous: bool = True) -> None:
     """The input contract of the fast scoring path, message for message as
-    dropkv_triton.py:680-716; raises ``AssertionError``."""
+    dropkv_triton.py:680-716; raises ``AssertionError``.  Callers whose K/V
+    are rows of a row-capacity buffer (the kernels take its row stride) pass
+    ``require_contiguous=False``."""
     B, Hq, Lq, D = Q.shape
     Hkv = K.shape[1]
     Lk = K.shape[2]
@@ -56,7 +59,7 @@ def check_scoring_inputs(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, wind
     assert Hq % Hkv == 0, f"Hq ({Hq}) must be divisible by Hkv ({Hkv})"
     assert Q.is_cuda, "Inputs must be on CUDA"
     assert Q.device == K.device == V.device, "All inputs must be on same device"
-    assert K.is_contiguous() and V.is_contiguous(), (
+    assert not require_contiguous or (K.is_contiguous() and V.is_contiguous()), (
         "K and V must be contiguous (Q is sliced internally)"
     )
     assert Q.dtype == K.dtype == V.dtype, "All inputs must have same dtype"

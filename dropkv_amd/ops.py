@@ -150,6 +150,59 @@ def compact2(K0: torch.Tensor, V0: torch.Tensor, K1: torch.Tensor, V1: torch.Ten
     return ko, vo
 
 
+def _check_buffer(buf: torch.Tensor, name: str):
+    if buf.dim() != 4 or not buf.is_contiguous() or not _aligned(buf):
+        raise RuntimeError(f"{name} must be a contiguous, 16-byte aligned [B, H, capacity, D] buffer")
+
+
+def append(K: torch.Tensor, V: torch.Tensor, k_buf: torch.Tensor, v_buf: torch.Tensor, row0: int):
+    """Copy K/V [B, H, L, D] (any strides, head dim contiguous) bit for bit
+    to rows ``row0 .. row0+L-1`` of the [B, H, capacity, D] buffers
+    (``dropkv_append``)."""
+    dev = _check_device(K, V, k_buf, v_buf)
+    _check_buffer(k_buf, "k_buf")
+    _check_buffer(v_buf, "v_buf")
+    if K.shape != V.shape or K.dtype != V.dtype or k_buf.shape != v_buf.shape:
+        raise RuntimeError("K/V and the buffers must match in shape and dtype")
+    if K.dtype != k_buf.dtype or K.shape[:2] != k_buf.shape[:2] or K.shape[3] != k_buf.shape[3]:
+        raise RuntimeError("K/V do not fit the buffers")
+    if K.stride(3) != 1 or V.stride(3) != 1 or K.stride() != V.stride():
+        K, V = K.contiguous(), V.contiguous()
+    B, H, L, D = K.shape
+    rc = _lib.load().dropkv_append(K.data_ptr(), V.data_ptr(), *_seg_strides(K), K.element_size(), B, H, L, D,
+                                   k_buf.data_ptr(), v_buf.data_ptr(), k_buf.shape[2], int(row0), _stream(dev))
+    _lib.check(rc, "dropkv_append")
+
+
+def evict_ld(Q: torch.Tensor, k_buf: torch.Tensor, v_buf: torch.Tensor, Lk: int, window: int, kernel_size: int,
+             keep: int, k_out: torch.Tensor, v_out: torch.Tensor, protect_window: int | None = None,
+             eps: float = 1e-6, p_round: bool = True, y_round: bool = False) -> torch.Tensor:
+    """One layer-call (``dropkv_evict_ld``) on K/V held in rows 0 .. Lk-1 of
+    [B, Hkv, capacity, D] buffers, writing the compressed rows to rows
+    0 .. keep-1 of the ``k_out`` / ``v_out`` buffers.  Returns the kept
+    indices [B, Hkv, keep] (ascending)."""
+    dev = _check_device(Q, k_buf, v_buf, k_out, v_out)
+    for t, n in ((k_buf, "k_buf"), (v_buf, "v_buf"), (k_out, "k_out"), (v_out, "v_out")):
+        _check_buffer(t, n)
+    if Q.dtype not in _DTYPE_CODE or k_buf.dtype != Q.dtype or v_buf.dtype != Q.dtype or k_out.dtype != Q.dtype:
+        raise RuntimeError("Q, the K/V buffers and the outputs must share a bf16/fp16 dtype")
+    if k_buf.shape != v_buf.shape or k_out.shape != v_out.shape:
+        raise RuntimeError("K and V buffers must have the same shape")
+    B, Hq, Lq, D = Q.shape
+    Hkv = k_buf.shape[1]
+    lib = _lib.load()
+    ws = _workspace(lib.dropkv_evict_workspace_bytes(B, Hq, Hkv, Lk, D, window, 0), dev)
+    idx = torch.empty(B, Hkv, keep, dtype=torch.int64, device=dev)
+    pw = window if protect_window is None else protect_window
+    rc = lib.dropkv_evict_ld(Q.data_ptr(), *Q.stride(), k_buf.data_ptr(), v_buf.data_ptr(), k_buf.shape[2],
+                             _DTYPE_CODE[Q.dtype], B, Hq, Hkv, Lq, int(Lk), D, int(window), float(eps),
+                             int(bool(p_round)), int(bool(y_round)), 0, int(kernel_size), int(pw), int(keep), None,
+                             idx.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), k_out.shape[2], ws.data_ptr(),
+                             ws.numel(), _stream(dev))
+    _lib.check(rc, "dropkv_evict_ld")
+    return idx
+
+
 class EvictPlan:
     """Pre-sized workspace and outputs for repeated layer-calls of one shape
     (``dropkv_evict``); avoids per-call allocation in tight loops."""

@@ -142,10 +142,42 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
                  float* scores, int64_t* keep_idx, void* k_out, void* v_out,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Chunked prefill on preallocated capacity.  Replaces the torch.cat of the
+ * stored K/V and the chunk and the gather that follows it in the
+ * evict_accumulated branch of DropKVCache.update (dropkv_cache.py:581-607),
+ * and the torch.cat of the accumulate branches (dropkv_cache.py:571-579,
+ * :618-620), for a cache that keeps each layer's K/V in buffers of a fixed
+ * row capacity.
+ *
+ * dropkv_append: rows 0 .. L-1 of each head of k / v ([B,H,L,D], element
+ * strides s_b, s_h, s_l, D contiguous) are copied, bit for bit, to rows
+ * row0 .. row0+L-1 of k_dst / v_dst ([B,H,dst_ld,D] contiguous).
+ * Requires row0 + L <= dst_ld.
+ *
+ * dropkv_evict_ld: dropkv_evict on K/V held in [B,Hkv,kv_ld,D] buffers (rows
+ * 0 .. Lk-1 of each head are the sequence) that writes the compressed rows
+ * to rows 0 .. keep-1 of [B,Hkv,out_ld,D] buffers.  Requires kv_ld >= Lk,
+ * out_ld >= keep and, when out_ld > keep, 16-byte aligned rows.  The output
+ * buffers must not overlap the inputs.  With kv_ld = Lk and out_ld = keep it
+ * is dropkv_evict.
+ * ------------------------------------------------------------------------ */
+int dropkv_append(const void* k, const void* v, int64_t s_b, int64_t s_h, int64_t s_l, int64_t elem_bytes,
+                  int64_t B, int64_t H, int64_t L, int64_t D, void* k_dst, void* v_dst, int64_t dst_ld,
+                  int64_t row0, void* stream);
+
+int dropkv_evict_ld(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
+                    const void* k, const void* v, int64_t kv_ld, int dtype,
+                    int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D,
+                    int64_t W, float eps, int p_round, int y_round, int64_t splits,
+                    int64_t kernel_size, int64_t protect_window, int64_t keep,
+                    float* scores, int64_t* keep_idx, void* k_out, void* v_out, int64_t out_ld,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* Kernel timing with HIP events (no counterpart in the reference, which has
  * no timers).  dropkv_timing_enable(1) makes every later dropkv_scores /
  * dropkv_select / dropkv_compact / dropkv_compact2 / dropkv_evict /
- * dropkv_decode_attention call on the calling thread launch its kernels with
+ * dropkv_evict_ld / dropkv_append / dropkv_decode_attention call on the calling thread launch its kernels with
  * hipExtLaunchKernel and a (start, stop) event pair each, which the runtime
  * sets to that dispatch's own begin and end time stamps.  dropkv_timing_read
  * waits for the last kernel of the most recent such call, writes the

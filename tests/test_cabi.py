@@ -95,3 +95,23 @@ def test_compact_argument_checks(lib):
     assert "elem_bytes" in lib.dropkv_last_error().decode()
     assert lib.dropkv_compact2(fake, fake, 0, 0, 0, -1, fake, fake, 0, 0, 0, 5, 2, 1, 1, 8, fake, 4, fake, fake,
                                None) == 1
+
+
+def test_capacity_entry_argument_checks(lib):
+    """dropkv_append / dropkv_evict_ld reject rows that do not fit the
+    buffers before enqueuing anything."""
+    fake = ctypes.c_void_p(1 << 20)
+    # 10 rows at row 95 of a 100-row buffer
+    assert lib.dropkv_append(fake, fake, 0, 0, 128, 2, 1, 8, 10, 128, fake, fake, 100, 95, None) == 1
+    assert "do not fit" in lib.dropkv_last_error().decode()
+    assert lib.dropkv_append(fake, fake, 0, 0, 128, 3, 1, 8, 10, 128, fake, fake, 100, 0, None) == 1
+    assert "elem_bytes" in lib.dropkv_last_error().decode()
+    # K/V row capacity (kv_ld = 50) below Lk = 100
+    args = [fake, 0, 0, 0, 1, fake, fake, 50, 1, 1, 32, 8, 64, 100, 128, 8, 1e-6, 1, 0, 0, 11, 8, 10,
+            None, fake, fake, fake, 10, fake, 1 << 30, None]
+    assert lib.dropkv_evict_ld(*args) == 1
+    assert "row capacity" in lib.dropkv_last_error().decode()
+    args[7] = 100
+    args[27] = 5  # output capacity below keep = 10
+    assert lib.dropkv_evict_ld(*args) == 1
+    assert "row capacity" in lib.dropkv_last_error().decode()

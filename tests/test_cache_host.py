@@ -362,3 +362,11 @@ def test_prefill_chunked_single_chunk_shortcut():
     c = _cache()
     prefill_chunked(m, torch.zeros(1, 30, dtype=torch.long), c, chunk_size=32)
     assert [e[0] for e in m.log] == ["single_pass"]
+
+
+def test_capacity_must_be_positive():
+    from dropkv_amd import DropKVCache
+    with pytest.raises(ValueError, match="capacity"):
+        DropKVCache(capacity=0)
+    assert DropKVCache(capacity=128).capacity == 128
+    assert DropKVCache().capacity is None
