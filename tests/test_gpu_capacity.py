@@ -12,7 +12,7 @@ outside the ones named are neither read (NaN-filled) nor written."""
 import pytest
 import torch
 
-from conftest import LLAMA_CFG, QWEN_CFG, make_qkv
+from conftest import BATCH2_CFG, LLAMA_CFG, QWEN_CFG, make_qkv
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +35,7 @@ def test_append_matches_slice_assignment(gpu):
         ops.append(src_k, src_v, kb, vb, C - L + 1)
 
 
-@pytest.mark.parametrize("cfg,fast", [(LLAMA_CFG, True), (LLAMA_CFG, False), (QWEN_CFG, True)])
+@pytest.mark.parametrize("cfg,fast", [(LLAMA_CFG, True), (LLAMA_CFG, False), (QWEN_CFG, True), (BATCH2_CFG, True)])
 def test_evict_ld_matches_evict(gpu, cfg, fast):
     """K/V in rows 0..Lk-1 of NaN-filled buffers, outputs into the first
     rows of sentinel-filled buffers: the same indices and rows as the
@@ -73,14 +73,17 @@ def _mode(strategy, i, n_chunks, stored, chunk_len, max_kv):
     return "evict_accumulated" if stored + chunk_len > max_kv else "accumulate"
 
 
-@pytest.mark.parametrize("strategy", ["last_chunk", "every_chunk", "budget"])
-@pytest.mark.parametrize("use_triton", [True, False])
-def test_capacity_cache_bit_exact_with_default(gpu, strategy, use_triton):
+@pytest.mark.parametrize("strategy,use_triton,cfg", [
+    ("last_chunk", True, LLAMA_CFG), ("every_chunk", True, LLAMA_CFG), ("budget", True, LLAMA_CFG),
+    ("last_chunk", False, LLAMA_CFG), ("every_chunk", False, LLAMA_CFG), ("budget", False, LLAMA_CFG),
+    ("every_chunk", True, QWEN_CFG), ("budget", True, BATCH2_CFG),
+])
+def test_capacity_cache_bit_exact_with_default(gpu, strategy, use_triton, cfg):
     """Both caches driven through update() in lock step, as a model in
     prefill_chunked drives them, compared after every layer of every chunk."""
     from dropkv_amd import DropKVCache
     L, chunk, layers, max_kv = 2304, 512, 2, 900  # the last chunk is shorter (256)
-    Q, K, V = make_qkv(LLAMA_CFG, L, seed=5, k_scale="lognormal")
+    Q, K, V = make_qkv(cfg, L, seed=5, k_scale="lognormal")
     Qg, Kg, Vg = Q.to(gpu), K.to(gpu), V.to(gpu)
     ref = DropKVCache(keep_ratio=0.3, use_triton=use_triton)
     cap = DropKVCache(keep_ratio=0.3, use_triton=use_triton, capacity=L)
@@ -108,7 +111,8 @@ def test_capacity_cache_bit_exact_with_default(gpu, strategy, use_triton):
         c._budget_max_kv_tokens = None
     # decode steps append in place
     for t in range(3):
-        kn = torch.randn(1, 8, 1, 128, generator=torch.Generator().manual_seed(t)).bfloat16().to(gpu)
+        kn = torch.randn(cfg["B"], cfg["Hkv"], 1, cfg["D"],
+                         generator=torch.Generator().manual_seed(t)).bfloat16().to(gpu)
         a = ref.update(None, kn, kn, layer_idx=0)
         b = cap.update(None, kn, kn, layer_idx=0)
         assert torch.equal(a[0], b[0]) and torch.equal(cap.key_cache[0], ref.key_cache[0])
