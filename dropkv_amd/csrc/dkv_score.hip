@@ -85,17 +85,35 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
     // An empty row (every logit -inf so far) subtracts 0, so that its p are
     // exp2(-inf) = 0 without a select per element.
     const float msub = empty ? 0.f : mnew;
-    float psum = 0.f;
+    float psum = 0.f, pv[8];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(s[kb][mb][r] - msub);
-        psum += pv;
-        const T h = static_cast<T>(pv);
-        phi[mb][4 * kb + r] = h;
-        if constexpr (PS == 2) plo[mb][4 * kb + r] = static_cast<T>(pv - static_cast<float>(h));
+        pv[4 * kb + r] = __builtin_amdgcn_exp2f(s[kb][mb][r] - msub);
+        psum += pv[4 * kb + r];
       }
+    // P in the element type, two values per packed conversion.
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef T t2 __attribute__((ext_vector_type(2)));
+    t2 h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = __builtin_convertvector((f2{pv[2 * e], pv[2 * e + 1]}), t2);
+    phi[mb] = __builtin_bit_cast(typename Elem<T>::v8,
+                                 __builtin_shufflevector(__builtin_shufflevector(h[0], h[1], 0, 1, 2, 3),
+                                                         __builtin_shufflevector(h[2], h[3], 0, 1, 2, 3), 0, 1, 2,
+                                                         3, 4, 5, 6, 7));
+    if constexpr (PS == 2) {
+      t2 l[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        l[e] = __builtin_convertvector((f2{pv[2 * e] - static_cast<float>(h[e][0]),
+                                           pv[2 * e + 1] - static_cast<float>(h[e][1])}), t2);
+      plo[mb] = __builtin_bit_cast(typename Elem<T>::v8,
+                                   __builtin_shufflevector(__builtin_shufflevector(l[0], l[1], 0, 1, 2, 3),
+                                                           __builtin_shufflevector(l[2], l[3], 0, 1, 2, 3), 0, 1,
+                                                           2, 3, 4, 5, 6, 7));
+    }
     lsum[mb] = lsum[mb] * alpha + psum;
     m2[mb] = mnew;
     // Rescale only when some row's maximum moved (rare after a few tiles);
@@ -105,11 +123,15 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= alpha;
       if (alpha != 1.f && !empty) {
+        // The empty asm pins the maximum's copy inside this branch, so that
+        // the compares below are not speculated into every tile.
+        float mm = mnew;
+        asm volatile("" : "+v"(mm));
         int c = INT_MAX;
 #pragma unroll
         for (int kb = 1; kb >= 0; --kb)
 #pragma unroll
-          for (int r = 3; r >= 0; --r) c = s[kb][mb][r] == mnew ? t0 + 16 * kb + 4 * lg + r : c;
+          for (int r = 3; r >= 0; --r) c = s[kb][mb][r] == mm ? t0 + 16 * kb + 4 * lg + r : c;
         acand[mb] = c;
       }
     }
@@ -534,16 +556,17 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
   const int nrel = k_end - k_begin;
   const int ntiles = (nrel + kTile - 1) / kTile;
   const int ngroups = (ntiles + kWideG - 1) / kWideG;
-  issue(0);
-  stage(0);
-  __syncthreads();
-  for (int grp = 0; grp < ngroups; ++grp) {
+  // One group of tiles from LDS stage `st` (a compile-time constant in
+  // both calls below, so that the LDS addresses fold into instruction
+  // offsets).
+  auto group = [&](int grp, auto st_c) __attribute__((always_inline)) {
+    constexpr int st = decltype(st_c)::value;
     if (grp + 1 < ngroups) issue(grp + 1);
     for (int gt = 0; gt < kWideG && active; ++gt) {
       const int it = grp * kWideG + gt;
       if (it >= ntiles) break;
       const int t0 = k_begin + it * kTile;
-      const uint32_t* kl = lds + (grp & 1) * kStage + gt * kTileWords;
+      const uint32_t* kl = lds + st * kStage + gt * kTileWords;
       const uint32_t* vt = kl + kKWords;
       // S^T = K Q^T with K from LDS.
       f32x4 s[2][kMB];
@@ -582,8 +605,15 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
         }
       }
     }
-    if (grp + 1 < ngroups) stage((grp + 1) & 1);
+    if (grp + 1 < ngroups) stage(1 - st);
     __syncthreads();
+  };
+  issue(0);
+  stage(0);
+  __syncthreads();
+  for (int grp = 0; grp < ngroups; grp += 2) {
+    group(grp, std::integral_constant<int, 0>{});
+    if (grp + 1 < ngroups) group(grp + 1, std::integral_constant<int, 1>{});
   }
   if (!active) return;
 
