@@ -154,3 +154,24 @@ def test_prefill_chunked_with_capacity(gpu, strategy):
     for layer in range(cfg.num_hidden_layers):
         assert torch.equal(caches[0].key_cache[layer], caches[1].key_cache[layer])
         assert torch.equal(caches[0].value_cache[layer], caches[1].value_cache[layer])
+
+
+def test_capacity_flow_makes_no_concatenation(gpu, monkeypatch):
+    """The capacity mode appends in place: a full last_chunk flow (and a
+    decode step) runs with torch.cat unavailable."""
+    from dropkv_amd import DropKVCache
+    Q, K, V = make_qkv(LLAMA_CFG, 1536, seed=8)
+    Qg, Kg, Vg = Q.to(gpu), K.to(gpu), V.to(gpu)
+    c = DropKVCache(keep_ratio=0.2, capacity=1600)
+
+    def no_cat(*a, **k):
+        raise AssertionError("torch.cat called in capacity mode")
+
+    monkeypatch.setattr(torch, "cat", no_cat)
+    for i, mode in enumerate(("accumulate", "accumulate", "evict_accumulated")):
+        c._prefill_mode = mode
+        s, e = 512 * i, 512 * (i + 1)
+        c.update(Qg[:, :, s:e], Kg[:, :, s:e], Vg[:, :, s:e], layer_idx=0)
+    c._prefill_mode = "single_pass"
+    c.update(None, Kg[:, :, :1], Vg[:, :, :1], layer_idx=0)
+    assert c.key_cache[0].shape[2] == max(int(0.2 * 1536), 8) + 1
