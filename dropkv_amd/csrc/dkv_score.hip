@@ -1115,7 +1115,7 @@ static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b)
 // DROPKV_TUNE environment variable ("p1w=8,p1occ=1,s1=32,s2=32",
 // any subset) overrides them for experiments.
 struct Tune {
-  int p1w = 4, p1occ = 1, s1 = 0, s2 = 0, target = 256, p1wide = 3, p1g = 1;
+  int p1w = 4, p1occ = 1, s1 = 0, s2 = 0, target = 256, target1_bw = 160, p1wide = 3, p1g = 1;
 };
 static Tune read_tune() {
   Tune t;
@@ -1129,6 +1129,7 @@ static Tune read_tune() {
     else if (!strcmp(key, "s1")) t.s1 = val;
     else if (!strcmp(key, "s2")) t.s2 = val;
     else if (!strcmp(key, "target")) t.target = val;
+    else if (!strcmp(key, "target1_bw")) t.target1_bw = val;
     else if (!strcmp(key, "p1wide")) t.p1wide = val;
     else if (!strcmp(key, "p1g")) t.p1g = val;
     e += n;
@@ -1158,7 +1159,14 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   p.p1_wide = (tune.p1wide > 0 && p.n_mc >= tune.p1wide && p.n_mc <= kWideWaves)
                   ? (tune.p1g == 4 ? 4 : tune.p1g == 2 ? 2 : 1) : 0;
   const int64_t p1_groups = p.p1_wide ? (int64_t)p.heads : (int64_t)p.heads * p.n_mc;
-  int s1 = splits > 0 ? (int)splits : (tune.s1 > 0 ? tune.s1 : ceil_div(target, p1_groups));
+  // Pass 1 of a bandwidth-bound call (a K/V stream of 32 MiB or more) runs
+  // fewer, longer splits: the memory system is already saturated with
+  // ~160 workgroups, and the merge then combines fewer partials (C2: 20
+  // splits per head, 75.3 us per layer-call against 76.9 us with 32).  A
+  // small call is latency-bound and keeps one workgroup per CU.
+  const bool p1_bw = (int64_t)p.heads * Lk * D * 2 * 2 >= (int64_t(32) << 20);
+  const int target1 = (p1_bw && !p.p1_wide) ? max(1, tune.target1_bw) : target;
+  int s1 = splits > 0 ? (int)splits : (tune.s1 > 0 ? tune.s1 : ceil_div(target1, p1_groups));
   s1 = max(1, min(min(s1, max_by_work), kMaxSplits));
   p.kps1 = ceil_div(ceil_div(Lk, s1), kTile) * kTile;
   p.s1 = ceil_div(Lk, p.kps1);
