@@ -175,3 +175,25 @@ def test_capacity_flow_makes_no_concatenation(gpu, monkeypatch):
     c._prefill_mode = "single_pass"
     c.update(None, Kg[:, :, :1], Vg[:, :, :1], layer_idx=0)
     assert c.key_cache[0].shape[2] == max(int(0.2 * 1536), 8) + 1
+
+
+def test_capacity_reorder_cache_matches_default(gpu):
+    """reorder_cache (beam reordering along the batch) in capacity mode gives
+    the default mode's tensors, and later appends land after them."""
+    from dropkv_amd import DropKVCache
+    Q, K, V = make_qkv(BATCH2_CFG, 1024, seed=12)
+    Qg, Kg, Vg = Q.to(gpu), K.to(gpu), V.to(gpu)
+    ref = DropKVCache(keep_ratio=0.2)
+    cap = DropKVCache(keep_ratio=0.2, capacity=1100)
+    for c in (ref, cap):
+        c._prefill_mode = "accumulate"
+        c.update(Qg[:, :, :512], Kg[:, :, :512], Vg[:, :, :512], layer_idx=0)
+        c._prefill_mode = "evict_accumulated"
+        c.update(Qg[:, :, 512:], Kg[:, :, 512:], Vg[:, :, 512:], layer_idx=0)
+        c._prefill_mode = "single_pass"
+        c.reorder_cache(torch.tensor([1, 0]))
+    assert torch.equal(cap.key_cache[0], ref.key_cache[0]) and torch.equal(cap.value_cache[0], ref.value_cache[0])
+    kn = torch.randn(2, 8, 1, 128, generator=torch.Generator().manual_seed(4)).bfloat16().to(gpu)
+    for c in (ref, cap):
+        c.update(None, kn, kn, layer_idx=0)
+    assert torch.equal(cap.key_cache[0], ref.key_cache[0])
