@@ -35,24 +35,26 @@ def test_append_matches_slice_assignment(gpu):
         ops.append(src_k, src_v, kb, vb, C - L + 1)
 
 
-@pytest.mark.parametrize("cfg,fast", [(LLAMA_CFG, True), (LLAMA_CFG, False), (QWEN_CFG, True), (BATCH2_CFG, True)])
-def test_evict_ld_matches_evict(gpu, cfg, fast):
+@pytest.mark.parametrize("cfg,fast,dtype", [(LLAMA_CFG, True, torch.bfloat16), (LLAMA_CFG, False, torch.bfloat16),
+                                            (QWEN_CFG, True, torch.bfloat16), (BATCH2_CFG, True, torch.bfloat16),
+                                            (LLAMA_CFG, True, torch.float16)])
+def test_evict_ld_matches_evict(gpu, cfg, fast, dtype):
     """K/V in rows 0..Lk-1 of NaN-filled buffers, outputs into the first
     rows of sentinel-filled buffers: the same indices and rows as the
     contiguous layer-call."""
     from dropkv_amd import ops
     Lk, Lq, C, W, ks = 3000, 1024, 3100, 8, 11
-    Q, K, V = make_qkv(cfg, Lq, Lk, seed=11, k_scale="lognormal")
+    Q, K, V = make_qkv(cfg, Lq, Lk, seed=11, dtype=dtype, k_scale="lognormal")
     Qg, Kg, Vg = Q.to(gpu), K.to(gpu), V.to(gpu)
     keep = int(0.1 * Lk)
     plan = ops.EvictPlan(Qg, Kg, W, ks, keep, p_round=True, y_round=not fast)
     idx, kc, vc = plan(Qg, Kg, Vg)
     B, H, _, D = K.shape
-    kb = torch.full((B, H, C, D), float("nan"), dtype=torch.bfloat16, device=gpu)
+    kb = torch.full((B, H, C, D), float("nan"), dtype=dtype, device=gpu)
     vb = torch.full_like(kb, float("nan"))
     kb[:, :, :Lk] = Kg
     vb[:, :, :Lk] = Vg
-    ko = torch.full((B, H, keep + 40, D), 3.0, dtype=torch.bfloat16, device=gpu)
+    ko = torch.full((B, H, keep + 40, D), 3.0, dtype=dtype, device=gpu)
     vo = torch.full_like(ko, 3.0)
     idx2 = ops.evict_ld(Qg, kb, vb, Lk, W, ks, keep, ko, vo, p_round=True, y_round=not fast)
     torch.cuda.synchronize()
