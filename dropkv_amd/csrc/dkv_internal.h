@@ -31,7 +31,7 @@ struct ScorePlan {
   int heads, g, M, n_mc, mpad;
   int s1, kps1;  // pass 1: splits per (head, row-chunk), keys per split
   int s2, kps2;  // pass 2: splits per head, keys per split
-  int p1_waves, p1_occ, p2_waves;  // launch shapes
+  int p1_waves, p2_waves;  // launch shapes
   int p1_wide;                     // pass 1 with all row-chunks of a head in one workgroup
   size_t off_ml, off_y, off_arg, off_op, off_stb, off_stat, off_yf, total;
 };

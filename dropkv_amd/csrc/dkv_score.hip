@@ -27,9 +27,6 @@
 #include <algorithm>
 #include <climits>
 #include <type_traits>
-#include <cstdio>
-#include <cstdlib>
-#include <cstring>
 
 namespace dkv {
 
@@ -1111,53 +1108,41 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
 
 static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
-// Launch-shape tuning.  Defaults come from sweeps on MI355X; the
-// DROPKV_TUNE environment variable ("p1w=8,p1occ=1,s1=32,s2=32",
-// any subset) overrides them for experiments.
-struct Tune {
-  int p1w = 4, p1occ = 1, s1 = 0, s2 = 0, target = 256, target1_bw = 160, p1wide = 3, p1g = 1;
-};
-static Tune read_tune() {
-  Tune t;
-  const char* e = getenv("DROPKV_TUNE");
-  if (!e) return t;
-  char key[16];
-  int val, n = 0;
-  while (sscanf(e, " %15[a-z0-9_]=%d%n", key, &val, &n) == 2) {
-    if (!strcmp(key, "p1w")) t.p1w = val;
-    else if (!strcmp(key, "p1occ")) t.p1occ = val;
-    else if (!strcmp(key, "s1")) t.s1 = val;
-    else if (!strcmp(key, "s2")) t.s2 = val;
-    else if (!strcmp(key, "target")) t.target = val;
-    else if (!strcmp(key, "target1_bw")) t.target1_bw = val;
-    else if (!strcmp(key, "p1wide")) t.p1wide = val;
-    else if (!strcmp(key, "p1g")) t.p1g = val;
-    e += n;
-    if (*e == ',') ++e;
-    n = 0;
-  }
-  return t;
-}
+// Launch shapes (from sweeps on MI355X).  Fixed per build: the split
+// geometry sets the floating-point summation order, so the same inputs give
+// the same bits on every call.  The -D overrides exist for sweeps only.
+#ifndef DKV_TARGET_WG
+#define DKV_TARGET_WG 256      // workgroups per pass: one per CU
+#endif
+#ifndef DKV_TARGET_P1_BW
+#define DKV_TARGET_P1_BW 160   // pass-1 workgroups of a bandwidth-bound call
+#endif
+#ifndef DKV_P1_WAVES
+#define DKV_P1_WAVES 4         // waves per pass-1 workgroup (4 or 8)
+#endif
+#ifndef DKV_P1_WIDE_MIN
+#define DKV_P1_WIDE_MIN 3      // row-chunks from which pass 1 shares tiles across chunks (0: never)
+#endif
+#ifndef DKV_P1_WIDE_GROUP
+#define DKV_P1_WIDE_GROUP 1    // tiles per LDS stage of the wide pass 1 (1, 2 or 4)
+#endif
 
 ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W,
                           int64_t splits) {
-  static const Tune tune = read_tune();
   ScorePlan p;
   p.heads = (int)(B * Hkv);
   p.g = (int)(Hq / Hkv);
   p.M = p.g * (int)W;
   p.n_mc = ceil_div(p.M, kRows);
   p.mpad = p.n_mc * kRows;
-  p.p1_waves = tune.p1w == 8 ? 8 : 4;
-  p.p1_occ = tune.p1occ == 2 ? 2 : 1;
+  p.p1_waves = DKV_P1_WAVES == 8 ? 8 : 4;
   p.p2_waves = 8;
-  const int target = max(1, tune.target);  // workgroups per pass (one per CU)
+  const int target = DKV_TARGET_WG;
   const int max_by_work = max(1, (int)(Lk / 256));
   // Several row-chunks share each K/V tile in one workgroup (pass1w) from
-  // n_mc >= p1wide (0: never) up to one chunk per wave.
+  // n_mc >= DKV_P1_WIDE_MIN up to one chunk per wave.
   // p1_wide is 0 or the pass1w tile group (1, 2 or 4 tiles per LDS stage).
-  p.p1_wide = (tune.p1wide > 0 && p.n_mc >= tune.p1wide && p.n_mc <= kWideWaves)
-                  ? (tune.p1g == 4 ? 4 : tune.p1g == 2 ? 2 : 1) : 0;
+  p.p1_wide = (DKV_P1_WIDE_MIN > 0 && p.n_mc >= DKV_P1_WIDE_MIN && p.n_mc <= kWideWaves) ? DKV_P1_WIDE_GROUP : 0;
   const int64_t p1_groups = p.p1_wide ? (int64_t)p.heads : (int64_t)p.heads * p.n_mc;
   // Pass 1 of a bandwidth-bound call (a K/V stream of 32 MiB or more) runs
   // fewer, longer splits: the memory system is already saturated with
@@ -1165,12 +1150,12 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   // splits per head, 75.3 us per layer-call against 76.9 us with 32).  A
   // small call is latency-bound and keeps one workgroup per CU.
   const bool p1_bw = (int64_t)p.heads * Lk * D * 2 * 2 >= (int64_t(32) << 20);
-  const int target1 = (p1_bw && !p.p1_wide) ? max(1, tune.target1_bw) : target;
-  int s1 = splits > 0 ? (int)splits : (tune.s1 > 0 ? tune.s1 : ceil_div(target1, p1_groups));
+  const int target1 = (p1_bw && !p.p1_wide) ? DKV_TARGET_P1_BW : target;
+  int s1 = splits > 0 ? (int)splits : ceil_div(target1, p1_groups);
   s1 = max(1, min(min(s1, max_by_work), kMaxSplits));
   p.kps1 = ceil_div(ceil_div(Lk, s1), kTile) * kTile;
   p.s1 = ceil_div(Lk, p.kps1);
-  int s2 = splits > 0 ? (int)splits : (tune.s2 > 0 ? tune.s2 : ceil_div(target, p.heads));
+  int s2 = splits > 0 ? (int)splits : ceil_div(target, p.heads);
   s2 = max(1, min(s2, max_by_work));
   p.kps2 = ceil_div(ceil_div(Lk, s2), kTile) * kTile;
   p.s2 = ceil_div(Lk, p.kps2);
@@ -1231,12 +1216,8 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
       launch((pass1_kernel<T, D, 8, 1, PS>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
                          vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y,
                          part_arg);
-    } else if (p.p1_occ == 1) {
-      launch((pass1_kernel<T, D, 4, 1, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
-                         vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y,
-                         part_arg);
     } else {
-      launch((pass1_kernel<T, D, 4, 2, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
+      launch((pass1_kernel<T, D, 4, 1, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
                          vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y,
                          part_arg);
     }

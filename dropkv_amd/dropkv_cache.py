@@ -308,10 +308,11 @@ class DropKVCache(_LayerCache):
             raise ValueError(f"DropKVCache capacity of {self.capacity} rows exceeded at layer {layer_idx}: "
                              f"{rows} rows needed")
 
-    def _evict_into(self, query_states, k_src, v_src, Lk: int, k_out, v_out) -> int:
+    def _evict_into(self, layer_idx: int, query_states, k_src, v_src, Lk: int, k_out, v_out) -> int:
         """Eviction of rows 0 .. Lk-1 of k_src / v_src ([B, Hkv, ld, D]) into
         the first rows of k_out / v_out; the same scoring choice, keep length
-        and protection as _compute_keep_indices.  Returns the keep length."""
+        and protection as _compute_keep_indices.  Returns the keep length;
+        raises ``ValueError`` when the kept rows exceed the capacity."""
         if query_states.shape[1] % k_src.shape[1] != 0:
             raise ValueError(f"Query heads {query_states.shape[1]} must be divisible by KV heads {k_src.shape[1]}")
         fast = False
@@ -326,6 +327,7 @@ class DropKVCache(_LayerCache):
         W = self.window_size if fast else min(self.window_size, query_states.shape[2])
         total_tok = self._seen_tokens if self._evict_use_seen_tokens else None
         keep = self._keep_length(Lk, total_tok, self._budget_max_kv_tokens)
+        self._fits(layer_idx, keep)
         ops.evict_ld(query_states, k_src, v_src, Lk, W, self.kernel_size, keep, k_out, v_out,
                      protect_window=min(self.window_size, Lk), p_round=True, y_round=not fast)
         return keep
@@ -356,7 +358,7 @@ class DropKVCache(_LayerCache):
             if src_k.data_ptr() % 16 or src_v.data_ptr() % 16:
                 src_k, src_v = src_k.clone(), src_v.clone()
             k, v = self._pair(layer_idx)
-            keep = self._evict_into(query_states, src_k, src_v, L, k, v)
+            keep = self._evict_into(layer_idx, query_states, src_k, src_v, L, k, v)
             self._set_stored(layer_idx, keep)
             return key_states, value_states
 
@@ -372,7 +374,7 @@ class DropKVCache(_LayerCache):
                 and n + L >= self.window_size):
             other = 1 - self._cur[layer_idx]
             ko, vo = self._pair(layer_idx, other)
-            keep = self._evict_into(query_states, k, v, n + L, ko, vo)
+            keep = self._evict_into(layer_idx, query_states, k, v, n + L, ko, vo)
             self._cur[layer_idx] = other
             self._set_stored(layer_idx, keep)
         else:

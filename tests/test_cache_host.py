@@ -370,3 +370,14 @@ def test_capacity_must_be_positive():
         DropKVCache(capacity=0)
     assert DropKVCache(capacity=128).capacity == 128
     assert DropKVCache().capacity is None
+
+
+def test_capacity_prefill_keep_above_capacity_raises():
+    """A prefill eviction whose keep length exceeds the capacity raises the
+    documented ValueError before anything is enqueued (also with CPU
+    tensors, where no kernel could run)."""
+    from dropkv_amd import DropKVCache
+    Q, K, V = make_qkv(LLAMA_CFG, 256, seed=6)
+    c = DropKVCache(keep_ratio=0.9, capacity=200)
+    with pytest.raises(ValueError, match="capacity of 200 rows exceeded at layer 0: 230 rows needed"):
+        c.update(Q, K, V, layer_idx=0)
