@@ -46,6 +46,10 @@ _SIGNATURES = {
                               _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                               _c_float, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
                               _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
+    "dropkv_evict_noalloc": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_int,
+                                      _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                      _c_float, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
+                                      _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "dropkv_evict_ld": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_int,
                                  _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                  _c_float, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
@@ -62,6 +66,10 @@ _SIGNATURES = {
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+# Size of the static per-GPU scratch of dropkv_evict_noalloc
+# (DROPKV_NOALLOC_SCRATCH_BYTES in include/dropkv_amd.h).
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _lib = None
 _lock = threading.Lock()

@@ -281,6 +281,70 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
                     workspace_bytes, stream);
 }
 
+}  // extern "C"
+
+// Scratch of dropkv_evict_noalloc: one copy per GPU, for the life of the
+// process.  In host code `scratch` names a host-side stand-in, not device
+// memory: every host use goes through the per-device address that
+// hipGetSymbolAddress returns (noalloc_scratch).
+static __device__ __align__(256) unsigned char scratch[DROPKV_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch` per device ordinal
+
+// The current device's copy of `scratch`, looked up once per device (with
+// that device current); the stream must belong to the current device.
+int noalloc_scratch(hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxScratchDevices) return fail(DROPKV_E_UNSUPPORTED, "device ordinal %d too large", dev);
+  if (st) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(st, &sdev);
+    if (e != hipSuccess) return hip_status(e, "hipStreamGetDevice");
+    if (sdev != dev)
+      return fail(DROPKV_E_ARG, "stream belongs to device %d, the current device is %d", (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(DROPKV_E_HIP, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DROPKV_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int dropkv_evict_noalloc(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const void* k,
+                         const void* v, int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk,
+                         int64_t D, int64_t W, float eps, int p_round, int y_round, int64_t splits,
+                         int64_t kernel_size, int64_t protect_window, int64_t keep, float* scores,
+                         int64_t* keep_idx, void* k_out, void* v_out, void* stream) {
+  (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
+  int rc = check_score_args(q, k, v, dtype, B, Hq, Hkv, Lq, Lk, D, W);
+  if (rc) return rc;
+  const size_t need = dropkv_evict_workspace_bytes(B, Hq, Hkv, Lk, D, W, splits);
+  if (need > DROPKV_NOALLOC_SCRATCH_BYTES)
+    return fail(DROPKV_E_UNSUPPORTED,
+                "dropkv_evict_noalloc: this shape needs %zu bytes of scratch, above the maximum of %zu; "
+                "use dropkv_evict with a workspace",
+                need, (size_t)DROPKV_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = noalloc_scratch(static_cast<hipStream_t>(stream), &ws);
+  if (rc) return rc;
+  return evict_impl(q, q_sb, q_sh, q_ss, q_sd, k, v, Lk, dtype, B, Hq, Hkv, Lq, Lk, D, W, eps, p_round, y_round,
+                    splits, kernel_size, protect_window, keep, scores, keep_idx, k_out, v_out, keep, ws,
+                    DROPKV_NOALLOC_SCRATCH_BYTES, stream);
+}
+
 int dropkv_evict_ld(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const void* k,
                     const void* v, int64_t kv_ld, int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq,
                     int64_t Lk, int64_t D, int64_t W, float eps, int p_round, int y_round, int64_t splits,

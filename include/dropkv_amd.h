@@ -143,6 +143,34 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * dropkv_evict without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops with a
+ * fixed memory budget, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference, which allocates per call.
+ *
+ * The scratch the kernels need lives in a static device array of
+ * DROPKV_NOALLOC_SCRATCH_BYTES (32 MiB), one per GPU, held until the process
+ * ends.  The first call on a device looks up its address there (make that
+ * first call outside graph capture); no call allocates or frees anything.
+ * Calls whose dropkv_evict_workspace_bytes exceeds the maximum return
+ * DROPKV_E_UNSUPPORTED: 32 MiB covers a Llama-3.1-8B layer (Hq 32, Hkv 8,
+ * D 128) up to about 300K keys and a Qwen2-0.5B layer up to about 1.3M
+ * keys; the B4 Hq64 Hkv8 128K-key stress shape needs 91 MiB and is refused.
+ * Every call on one GPU uses the same scratch and leaves its contents
+ * behind: calls that overlap on one GPU (two streams, or two threads) race
+ * and must be serialised by the caller.  No part of the scratch needs to be
+ * zero on entry.  Arguments and results are those of dropkv_evict.
+ * ------------------------------------------------------------------------ */
+#define DROPKV_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+int dropkv_evict_noalloc(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd,
+                         const void* k, const void* v, int dtype,
+                         int64_t B, int64_t Hq, int64_t Hkv, int64_t Lq, int64_t Lk, int64_t D,
+                         int64_t W, float eps, int p_round, int y_round, int64_t splits,
+                         int64_t kernel_size, int64_t protect_window, int64_t keep,
+                         float* scores, int64_t* keep_idx, void* k_out, void* v_out, void* stream);
+
+/* ------------------------------------------------------------------------
  * Chunked prefill on preallocated capacity.  Replaces the torch.cat of the
  * stored K/V and the chunk and the gather that follows it in the
  * evict_accumulated branch of DropKVCache.update (dropkv_cache.py:581-607),

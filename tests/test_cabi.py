@@ -115,3 +115,21 @@ def test_capacity_entry_argument_checks(lib):
     args[27] = 5  # output capacity below keep = 10
     assert lib.dropkv_evict_ld(*args) == 1
     assert "row capacity" in lib.dropkv_last_error().decode()
+
+
+def test_noalloc_entry_refuses_shapes_beyond_its_scratch(lib):
+    """dropkv_evict_noalloc checks its arguments and the scratch bound on the
+    host, before it looks up the scratch or enqueues anything."""
+    fake = ctypes.c_void_p(1 << 20)
+    assert _lib.NOALLOC_SCRATCH_BYTES == 32 << 20
+    # B4 Hq64 Hkv8 D128 Lk=131072 W32: 91 MiB of scratch
+    need = lib.dropkv_evict_workspace_bytes(4, 64, 8, 131072, 128, 32, 0)
+    assert need > _lib.NOALLOC_SCRATCH_BYTES
+    args = [fake, 0, 0, 0, 1, fake, fake, 1, 4, 64, 8, 131072, 131072, 128, 32, 1e-6, 1, 0, 0, 11, 32, 6553,
+            None, fake, fake, fake, None]
+    assert lib.dropkv_evict_noalloc(*args) == 2
+    msg = lib.dropkv_last_error().decode()
+    assert "needs %d bytes of scratch" % need in msg and "dropkv_evict with a workspace" in msg
+    args[14] = 0  # window 0: an argument error comes first
+    assert lib.dropkv_evict_noalloc(*args) == 1
+    assert "window must be positive" in lib.dropkv_last_error().decode()
