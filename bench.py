@@ -12,8 +12,15 @@ Prints one JSON line.  ``value`` is the K/V bytes read once per layer-call
 GB/s.  ``roofline`` describes the longest kernel of the call: its duration is
 measured with the HIP events that ``hipExtLaunchKernel`` sets to each
 dispatch's own begin and end time stamps (``dropkv_timing_*``; the same
-source as the rocprofv3 kernel trace), averaged over the timed steps.  ``cpu_baseline`` times the CPU oracle of the deployed path
-(score -> pool -> top-k -> sort -> gather) on the same inputs.
+source as the rocprofv3 kernel trace), averaged over the timed steps.
+``cpu_baseline`` times the CPU oracle of the deployed path (score -> pool ->
+top-k -> sort -> gather) on the same inputs.
+
+The same line also carries: ``dropkv_cache_update_ms`` (the drop-in
+``DropKVCache.update`` prefill eviction of this shape), ``cold`` (steps with
+K/V flushed from the caches first) and ``extras`` (the other BASELINE
+configurations: the C4 Qwen2 layer-call, the C5 stress layer-call, the C3
+chunked-prefill cache flow and the C4 end-to-end prefill / decode figures).
 
 Other modes: ``--kernels-only`` (warm-up + steps, no extras; for profiler
 runs), ``--copy-calibration MIB`` (a plain device copy, to scale the HBM byte
@@ -198,6 +205,9 @@ def main():
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--kernels-only", action="store_true", help="warm-up + timed steps only (profiler runs)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache steps")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the C3 flow / C4 layer and end-to-end / C5 stress figures of the default run")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (20 times), to calibrate HBM byte counters")
     ap.add_argument("--pmc-summary", nargs=5, metavar=("FETCH_DIR", "WRITE_DIR", "CAL_FETCH_DIR", "CAL_WRITE_DIR",
@@ -242,19 +252,11 @@ def main():
         plan(Qg, Kg, Vg)
     torch.cuda.synchronize()
 
-    def timed(fn, steps):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        start.record()
-        for _ in range(steps):
-            fn()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / steps, 1e3 * (time.perf_counter() - t0) / steps
-
-    # Headline: one dropkv_evict call per step, exactly what a caller of the
-    # drop-in API does, K steps bracketed by events on the launch stream.
+    # Headline: one fused layer-call (dropkv_evict: score, pool, protect,
+    # top-k, sort, gather) per step on a preallocated plan, K steps bracketed
+    # by events on the launch stream.  DropKVCache.update and the HF layer
+    # cache make this same call; their own cost on top (host-side guards,
+    # fresh output tensors) is timed separately below.
     print(f"[bench] timing {args.steps} layer-calls", file=sys.stderr, flush=True)
     ms_per_step, wall_ms = timed(lambda: plan(Qg, Kg, Vg), args.steps)
     if args.kernels_only:
@@ -268,26 +270,8 @@ def main():
     graph.replay()
     graph_ms, _ = timed(graph.replay, args.steps)
 
-    # Per-kernel durations from the dispatches' own time stamps (events that
-    # hipExtLaunchKernel fills; eager calls, one read per call).
     lib = _lib.load()
-    buf = (ctypes.c_double * 16)()
-    sums, nk = None, 0
-    _lib.check(lib.dropkv_timing_enable(1), "dropkv_timing_enable")
-    try:
-        for _ in range(args.steps):
-            plan(Qg, Kg, Vg)
-            nk = lib.dropkv_timing_read(buf, 16)
-            if nk < 0:
-                _lib.check(-nk, "dropkv_timing_read")
-            sums = [0.0] * nk if sums is None else sums
-            for i in range(nk):
-                sums[i] += buf[i]
-    finally:
-        lib.dropkv_timing_enable(0)
-    names = {len(STAGES_FUSED): STAGES_FUSED, len(STAGES_UNFUSED): STAGES_UNFUSED}.get(
-        nk, tuple(f"kernel{i}" for i in range(nk)))
-    kernel_us = {names[i]: 1e3 * sums[i] / args.steps for i in range(nk)}
+    kernel_us, nk = kernel_times(lib, lambda: plan(Qg, Kg, Vg), args.steps)
 
     bytes_alg = 2 * B * Hkv * Lk * D * 2
     value = bytes_alg / (ms_per_step * 1e-3) / 1e9
@@ -327,7 +311,8 @@ def main():
                    "window": W, "kernel_size": cfg["kernel"], "keep_ratio": cfg["ratio"], "keep": keep,
                    "parallelism": "single GPU"},
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
-        "timing": "steps x one dropkv_evict call, HIP events around the steps on the launch stream",
+        "timing": "steps x one dropkv_evict call, HIP events around the steps on the launch stream; K/V stay "
+                  "resident in the 256 MB memory-side cache between steps (see 'cold' for flushed steps)",
         "wall_ms_per_step": round(wall_ms, 5),
         "graph_ms_per_step": round(graph_ms, 5),
         "kernel_us": {k: round(v, 3) for k, v in kernel_us.items()},
@@ -337,6 +322,29 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "bytes_per_launch": bytes_alg},
     }
+
+    # The drop-in cache itself: DropKVCache(keep_ratio, window, kernel).update
+    # on a fresh layer per step (each is a single_pass prefill eviction:
+    # guards, keep length, fresh compressed tensors, one fused layer-call).
+    if not cfg.get("gen") == "device":
+        out["dropkv_cache_update_ms"] = round(cache_update_ms(cfg, Qg, Kg, Vg, args.steps), 5)
+
+    # Cold steps: before each step an unrelated 2 GiB buffer is read (not
+    # written, so no dirty lines are left), which evicts K/V from the L2s and
+    # the memory-side cache; events bracket the layer-call alone.
+    if not args.no_cold:
+        print("[bench] cold steps", file=sys.stderr, flush=True)
+        cold_ms, cold_kus = cold_steps(lib, lambda: plan(Qg, Kg, Vg), min(args.steps, 50), dev)
+        cold_dom = max((s for s in STREAM_STAGES if s in cold_kus), key=lambda s: cold_kus[s])
+        cold_ach = bytes_alg / (cold_kus[cold_dom] * 1e-6) / 1e9
+        out["cold"] = {"ms_per_step": round(cold_ms, 5), "value": round(bytes_alg / (cold_ms * 1e-3) / 1e9, 2),
+                       "unit": "GB/s", "pct_hbm_peak": round(100.0 * bytes_alg / (cold_ms * 1e-3) / 1e9
+                                                             / HBM_PEAK_GBPS, 2),
+                       "kernel_us": {k: round(v, 3) for k, v in cold_kus.items()},
+                       "roofline": {"kernel": cold_dom, "achieved": round(cold_ach, 1),
+                                    "frac": round(cold_ach / HBM_PEAK_GBPS, 4)},
+                       "flush": "read of an unrelated 2 GiB fp32 buffer (torch.sum) before each step, outside "
+                                "the events"}
 
     # Parity and CPU-baseline samples: the whole workload, or sampled (b, hkv)
     # rows (each with its g query heads) where the workload is too large for
@@ -385,7 +393,234 @@ def main():
                            "traffic": traffic, "flops_per_launch": flops_kernel,
                            "hbm": {"achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                                    "frac": round(achieved / HBM_PEAK_GBPS, 4), "bytes_per_launch": bytes_alg}}
+
+    # The other BASELINE configurations, measured in the same run (skipped
+    # with --no-extras): C3's chunked-prefill cache flow, C4's Qwen2 layer
+    # and end-to-end run, C5's stress layer-call.
+    if not args.no_extras and args.workload == "llama8b_layer_32k":
+        del plan, Qg, Kg, Vg
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        out["extras"] = extras(lib, dev)
     print(json.dumps(out), flush=True)
+
+
+def timed(fn, steps):
+    """(ms per call from events around ``steps`` calls, host ms per call)."""
+    import torch
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps, 1e3 * (time.perf_counter() - t0) / steps
+
+
+def kernel_times(lib, fn, steps):
+    """Mean duration in us of each kernel of ``fn`` (one library call), from
+    the dispatches' own time stamps (events that hipExtLaunchKernel fills;
+    eager calls, one read per call)."""
+    from dropkv_amd import _lib
+    buf = (ctypes.c_double * 16)()
+    sums, nk = None, 0
+    _lib.check(lib.dropkv_timing_enable(1), "dropkv_timing_enable")
+    try:
+        for _ in range(steps):
+            fn()
+            nk = lib.dropkv_timing_read(buf, 16)
+            if nk < 0:
+                _lib.check(-nk, "dropkv_timing_read")
+            sums = [0.0] * nk if sums is None else sums
+            for i in range(nk):
+                sums[i] += buf[i]
+    finally:
+        lib.dropkv_timing_enable(0)
+    names = {len(STAGES_FUSED): STAGES_FUSED, len(STAGES_UNFUSED): STAGES_UNFUSED}.get(
+        nk, tuple(f"kernel{i}" for i in range(nk)))
+    return {names[i]: 1e3 * sums[i] / steps for i in range(nk)}, nk
+
+
+def cold_steps(lib, fn, steps, dev):
+    """Mean ms per call of ``fn`` and its per-kernel us when the caches hold
+    none of its inputs: before each call, a 2 GiB buffer that the call never
+    touches is read.  The call time comes from steps with plain launches
+    (events around the call), the kernel times from a second series with the
+    per-kernel time stamps (whose event launches add gaps between kernels)."""
+    import torch
+    from dropkv_amd import _lib
+    flush = torch.ones(1 << 29, dtype=torch.float32, device=dev)
+    acc = torch.empty((), dtype=torch.float32, device=dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    total = 0.0
+    for _ in range(steps):
+        torch.sum(flush, dim=0, out=acc)
+        start.record()
+        fn()
+        end.record()
+        end.synchronize()
+        total += start.elapsed_time(end)
+    buf = (ctypes.c_double * 16)()
+    sums, nk = None, 0
+    _lib.check(lib.dropkv_timing_enable(1), "dropkv_timing_enable")
+    try:
+        for _ in range(steps):
+            torch.sum(flush, dim=0, out=acc)
+            fn()
+            nk = lib.dropkv_timing_read(buf, 16)
+            if nk < 0:
+                _lib.check(-nk, "dropkv_timing_read")
+            sums = [0.0] * nk if sums is None else sums
+            for i in range(nk):
+                sums[i] += buf[i]
+    finally:
+        lib.dropkv_timing_enable(0)
+    del flush
+    names = {len(STAGES_FUSED): STAGES_FUSED, len(STAGES_UNFUSED): STAGES_UNFUSED}.get(
+        nk, tuple(f"kernel{i}" for i in range(nk)))
+    return total / steps, {names[i]: 1e3 * sums[i] / steps for i in range(nk)}
+
+
+def cache_update_ms(cfg, Qg, Kg, Vg, steps):
+    """ms per DropKVCache.update prefill eviction (single_pass) of this
+    layer shape: one cache, layer i at step i (as a model's prefill fills
+    it), events around the steps.  A first cache of as many layers, then
+    dropped, warms the caching allocator, as the previous request does in a
+    serving loop: the timed layers' compressed K/V reuse its blocks instead
+    of growing device memory."""
+    import torch
+    from dropkv_amd import DropKVCache
+
+    def fresh():
+        return DropKVCache(keep_ratio=cfg["ratio"], window_size=cfg["window"], kernel_size=cfg["kernel"])
+
+    cache = fresh()
+    for i in range(steps):
+        cache.update(Qg, Kg, Vg, layer_idx=i)
+    torch.cuda.synchronize()
+    del cache
+    cache = fresh()
+    ms, _ = timed(lambda: cache.update(Qg, Kg, Vg, layer_idx=len(cache.key_cache)), steps)
+    assert len(cache.key_cache) == steps
+    del cache
+    return ms
+
+
+# ---------------------------------------------------------------------------
+# C3: the chunked-prefill cache flow (dropkv_cache.py:651-807) on one layer of
+# the Llama-3.1-8B head shape, 16 chunks of 4096 up to 65536 tokens, driven
+# through DropKVCache.update exactly as prefill_chunked drives it, in the
+# default mode (torch.cat, gather into new tensors) and the capacity mode
+# (append in place, gather between preallocated buffers).
+# ---------------------------------------------------------------------------
+def _flow_mode(strategy: str, i: int, n: int, stored: int, chunk: int, max_kv: int) -> str:
+    last = i == n - 1
+    if strategy == "last_chunk":
+        return "evict_accumulated" if last else "accumulate"
+    if strategy == "every_chunk":
+        return "single_pass" if i == 0 else "evict_accumulated"
+    if last:
+        return "evict_accumulated"
+    return "evict_accumulated" if stored + chunk > max_kv else "accumulate"
+
+
+def run_flow(cache, chunks, strategy: str, max_kv: int) -> None:
+    """The mode schedule of prefill_chunked (dropkv_cache.py:764-788) over
+    one layer's pre-drawn (q, k, v) chunks."""
+    cache._evict_use_seen_tokens = strategy in ("budget", "every_chunk")
+    cache._budget_max_kv_tokens = max_kv if strategy == "budget" else None
+    n = len(chunks)
+    try:
+        for i, (q, k, v) in enumerate(chunks):
+            stored = cache.key_cache[0].shape[2] if cache.key_cache else 0
+            cache._prefill_mode = _flow_mode(strategy, i, n, stored, k.shape[2], max_kv)
+            cache.update(q, k, v, layer_idx=0)
+    finally:
+        cache._prefill_mode = "single_pass"
+        cache._evict_use_seen_tokens = False
+        cache._budget_max_kv_tokens = None
+
+
+def c3_flow(dev, length=65536, chunk=4096, ratio=0.1, max_kv=32768, reps=3):
+    import torch
+    from dropkv_amd import DropKVCache
+    B, Hq, Hkv, D = 1, 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    chunks = []
+    for s in range(0, length, chunk):
+        n = min(chunk, length - s)
+        chunks.append(tuple(torch.randn(B, h, n, D, device=dev, generator=g).bfloat16() for h in (Hq, Hkv, Hkv)))
+    res = {"B": B, "Hq": Hq, "Hkv": Hkv, "D": D, "length": length, "chunk": chunk, "keep_ratio": ratio,
+           "max_kv_tokens": max_kv, "timing": "HIP events around one layer's whole flow (host launch work "
+                                              f"included), median of {reps} after 1 warm-up"}
+    for strategy in ("every_chunk", "last_chunk", "budget"):
+        for label, capacity in (("default", None), ("capacity", length)):
+            times = []
+            for rep in range(reps + 1):
+                cache = DropKVCache(keep_ratio=ratio, capacity=capacity)
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                start.record()
+                run_flow(cache, chunks, strategy, max_kv)
+                end.record()
+                torch.cuda.synchronize()
+                if rep:
+                    times.append(start.elapsed_time(end))
+                stored = cache.key_cache[0].shape[2]
+                del cache
+            res[f"{strategy}/{label}"] = {"ms_per_flow": round(statistics.median(times), 3),
+                                          "stored_rows": stored}
+    return res
+
+
+def extras(lib, dev):
+    import torch
+    from dropkv_amd import ops
+    ex = {}
+    # C4 layer shape (Qwen2-0.5B, Lk 16384) and C5 (stress) layer-calls.
+    for name, steps in (("qwen05b_layer_16k", 50), ("stress_b4_128k", 10)):
+        print(f"[bench] extra: {name}", file=sys.stderr, flush=True)
+        cfg = WORKLOADS[name]
+        B, Hq, Hkv, D, Lk, W = (cfg[k] for k in ("B", "Hq", "Hkv", "D", "Lk", "window"))
+        keep = min(Lk, max(int(cfg["ratio"] * Lk), W, 1))
+        if cfg.get("gen") == "device":
+            Qg, Kg, Vg = make_device_inputs(cfg, dev)
+        else:
+            Qg, Kg, Vg = (t.to(dev) for t in make_inputs(cfg))
+        plan = ops.EvictPlan(Qg, Kg, W, cfg["kernel"], keep)
+        for _ in range(3):
+            plan(Qg, Kg, Vg)
+        ms, _ = timed(lambda: plan(Qg, Kg, Vg), steps)
+        kus, _ = kernel_times(lib, lambda: plan(Qg, Kg, Vg), steps)
+        bytes_alg = 2 * B * Hkv * Lk * D * 2
+        M = (Hq // Hkv) * W
+        e = {"ms_per_step": round(ms, 5), "steps": steps, "keep": keep,
+             "kv_GBps": round(bytes_alg / (ms * 1e-3) / 1e9, 1),
+             "kernel_us": {k: round(v, 3) for k, v in kus.items()}}
+        if 2 * M > MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBPS * 1e9):
+            flops = 4 * B * Hkv * M * D * Lk
+            e["mfma_frac"] = {k: round(flops / (kus[k] * 1e-6) / 1e12 / MFMA_PEAK_TFLOPS, 4)
+                              for k in STREAM_STAGES if k in kus}
+        ex[name] = e
+        del plan, Qg, Kg, Vg
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    print("[bench] extra: C3 chunked flow", file=sys.stderr, flush=True)
+    ex["chunked_llama8b_64k"] = c3_flow(dev)
+    torch.cuda.empty_cache()
+    print("[bench] extra: C4 end to end", file=sys.stderr, flush=True)
+    from dropkv_amd import e2e_qwen2
+    e2e = e2e_qwen2.run(argparse.Namespace(prompt=16384, decode=256, layers=24, keep_ratio=0.1, window=8,
+                                           kernel_size=11, reps=1, warmup=1, seed=0, compare=False))
+    ex["qwen2_0.5b_e2e"] = {"c4_prefill_ms": round(e2e["dropkv"]["prefill_ms"], 3),
+                            "c4_decode_tok_s": round(e2e["dropkv"]["decode_tok_s"], 2),
+                            "decode_setup_ms": round(e2e["dropkv"]["decode_setup_ms"], 3),
+                            "stored_kv_rows_layer0": e2e["dropkv"]["stored_kv_rows_layer0"],
+                            "config": e2e["config"], "data": e2e["data"]}
+    torch.cuda.empty_cache()
+    return ex
 
 
 if __name__ == "__main__":

@@ -101,7 +101,15 @@ def check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed (code {rc}): {msg}")
 
 
+_head_dims = None
+
+
 def supported_head_dims() -> tuple[int, ...]:
-    buf = (_c_i64 * 16)()
-    n = load().dropkv_supported_head_dims(buf, 16)
-    return tuple(int(buf[i]) for i in range(min(n, 16)))
+    """Head dimensions the matrix-core scoring kernels are compiled for
+    (asked once; the library does not change while loaded)."""
+    global _head_dims
+    if _head_dims is None:
+        buf = (_c_i64 * 16)()
+        n = load().dropkv_supported_head_dims(buf, 16)
+        _head_dims = tuple(int(buf[i]) for i in range(min(n, 16)))
+    return _head_dims

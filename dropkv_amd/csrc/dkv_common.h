@@ -103,6 +103,51 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
   return base + slot;
 }
 
+// Wave-wide reductions over DPP row operations: a max / min / sum within each
+// row of 16 lanes (two quad permutes, the half-row mirror, the row mirror),
+// then the four rows combined from lane reads.  The result is wave-uniform.
+// Far shorter latency than lane shuffles through LDS (ds_bpermute).
+template <int kCtrl>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_mov_dpp(x, kCtrl, 0xf, 0xf, false);
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, dpp_i<kCtrl>(__builtin_bit_cast(int, x)));
+}
+constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror
+constexpr int kDppMirror = 0x140;     // row_mirror
+__device__ __forceinline__ float read_lane_f(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float x) {
+  x = fmaxf(x, dpp_f<kDppQuadSwap1>(x));
+  x = fmaxf(x, dpp_f<kDppQuadSwap2>(x));
+  x = fmaxf(x, dpp_f<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp_f<kDppMirror>(x));
+  return fmaxf(fmaxf(read_lane_f(x, 0), read_lane_f(x, 16)), fmaxf(read_lane_f(x, 32), read_lane_f(x, 48)));
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float x) {
+  x += dpp_f<kDppQuadSwap1>(x);
+  x += dpp_f<kDppQuadSwap2>(x);
+  x += dpp_f<kDppHalfMirror>(x);
+  x += dpp_f<kDppMirror>(x);
+  return (read_lane_f(x, 0) + read_lane_f(x, 16)) + (read_lane_f(x, 32) + read_lane_f(x, 48));
+}
+
+__device__ __forceinline__ int wave_min_dpp(int x) {
+  x = min(x, dpp_i<kDppQuadSwap1>(x));
+  x = min(x, dpp_i<kDppQuadSwap2>(x));
+  x = min(x, dpp_i<kDppHalfMirror>(x));
+  x = min(x, dpp_i<kDppMirror>(x));
+  return min(min(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+             min(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);

@@ -33,7 +33,7 @@ struct ScorePlan {
   int s2, kps2;  // pass 2: splits per head, keys per split
   int p1_waves, p2_waves;  // launch shapes
   int p1_wide;                     // pass 1 with all row-chunks of a head in one workgroup
-  size_t off_ml, off_y, off_arg, off_op, off_stb, off_stat, off_yf, total;
+  size_t off_ml, off_y, off_cand, off_op, off_stb, off_stat, off_yf, total;
 };
 
 ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W, int64_t splits);

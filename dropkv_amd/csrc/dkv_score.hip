@@ -44,6 +44,9 @@ constexpr int kYParts = 2;
 constexpr int kOpSlots = 1 + kYParts;  // Q and the parts of Y, per row block and k-step
 constexpr int kStatWords = 64;         // per 16-row block: lse, |y|^2, sink key, -dist2/2 at it
 constexpr int kPitch = 18;          // dwords per row of the transposed V tile
+// Candidate keys per (row, split) for merge's rounding correction of y: the
+// keys holding the largest logits among those of individual lanes.
+constexpr int kCand = 4;
 
 
 __device__ __forceinline__ int row_bound(int m, int M, int W, int Lk) {
@@ -53,12 +56,14 @@ __device__ __forceinline__ int row_bound(int m, int M, int W, int Lk) {
 // Online-softmax step (base 2) of one 32-key tile starting at key t0, for
 // the lane's kMB row blocks: scales the logits s in place, applies the causal
 // bound (kMasked: tiles that reach it, or padding rows), updates the running
-// maximum m2 and sum lsum, rescales the y accumulators when a maximum moved
-// (and then notes in acand which of the lane's keys holds it), and returns
-// the tile's P in PS parts of the element type (hi, and lo when PS == 2).
-template <typename T, int D, int PS, bool kMasked>
+// maximum m2 and sum lsum, rescales the y accumulators when a maximum moved,
+// keeps the largest logit among the lane's own keys and the lowest key
+// holding it (lmax, larg: the candidates of merge's correction of y), and
+// returns the tile's P as two parts in the element type, hi and the rounded
+// remainder lo (~16 significant bits together).
+template <typename T, int D, bool kMasked>
 __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB], float (&lsum)[kMB],
-                                             int (&acand)[kMB], f32x4 (&yacc)[D / 16][kMB],
+                                             float (&lmax)[kMB], int (&larg)[kMB], f32x4 (&yacc)[D / 16][kMB],
                                              typename Elem<T>::v8 (&phi)[kMB], typename Elem<T>::v8 (&plo)[kMB],
                                              const int (&bound)[kMB], int t0, int lg, float scale_log2) {
   constexpr int DT = D / 16;
@@ -74,6 +79,27 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
         s[kb][mb][r] = x;
         tmax = fmaxf(tmax, x);
       }
+#if defined(DKV_EXP_CAND) && DKV_EXP_CAND == 2
+    {
+      const bool up = tmax > lmax[mb];
+      lmax[mb] = up ? tmax : lmax[mb];
+      larg[mb] = up ? t0 + 4 * lg : larg[mb];
+    }
+#elif defined(DKV_EXP_CAND) && DKV_EXP_CAND == 0
+#else
+    {
+      // The lane's own maximum so far and the lowest of its keys holding it
+      // (key t0 + 16 kb + 4 lg + r; scanned downwards so the lowest wins).
+      int off = 0;
+#pragma unroll
+      for (int kb = 1; kb >= 0; --kb)
+#pragma unroll
+        for (int r = 3; r >= 0; --r) off = s[kb][mb][r] == tmax ? 16 * kb + r : off;
+      const bool up = tmax > lmax[mb];
+      lmax[mb] = up ? tmax : lmax[mb];
+      larg[mb] = up ? t0 + 4 * lg + off : larg[mb];
+    }
+#endif
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const float mnew = fmaxf(m2[mb], tmax);
@@ -100,7 +126,7 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
                                  __builtin_shufflevector(__builtin_shufflevector(h[0], h[1], 0, 1, 2, 3),
                                                          __builtin_shufflevector(h[2], h[3], 0, 1, 2, 3), 0, 1, 2,
                                                          3, 4, 5, 6, 7));
-    if constexpr (PS == 2) {
+    {
       t2 l[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -113,24 +139,10 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
     }
     lsum[mb] = lsum[mb] * alpha + psum;
     m2[mb] = mnew;
-    // Rescale only when some row's maximum moved (rare after a few tiles);
-    // then the lanes of a row whose maximum moved note which of their keys
-    // hold it.
+    // Rescale only when some row's maximum moved (rare after a few tiles).
     if (__any(alpha != 1.f)) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= alpha;
-      if (alpha != 1.f && !empty) {
-        // The empty asm pins the maximum's copy inside this branch, so that
-        // the compares below are not speculated into every tile.
-        float mm = mnew;
-        asm volatile("" : "+v"(mm));
-        int c = INT_MAX;
-#pragma unroll
-        for (int kb = 1; kb >= 0; --kb)
-#pragma unroll
-          for (int r = 3; r >= 0; --r) c = s[kb][mb][r] == mm ? t0 + 16 * kb + 4 * lg + r : c;
-        acand[mb] = c;
-      }
     }
   }
 }
@@ -176,6 +188,30 @@ __device__ __forceinline__ int grab_tile(uint32_t* ctr) {
   uint32_t v = 0u;
   if ((threadIdx.x & 63) == 0) v = atomicAdd(ctr, 1u);
   return __builtin_amdgcn_readfirstlane(v);
+}
+
+// Candidate order: the larger logit first, the lower key among equal logits;
+// no candidate (key < 0) last.
+__device__ __forceinline__ bool cand_before(float va, int ka, float vb, int kb) {
+  return ka >= 0 && (kb < 0 || va > vb || (va == vb && ka < kb));
+}
+
+// Sorts the four (logit, key) candidates of a row held by the lanes of its
+// four lane groups (lg = lane / 16) into candidate order along lg (a bitonic
+// network over lane shuffles).
+__device__ __forceinline__ void sort_lane_groups(float& v, int& k, int lg) {
+  auto step = [&](int mask, bool keep_first) {
+    const float ov = __shfl_xor(v, mask);
+    const int ok = __shfl_xor(k, mask);
+    const bool mine_first = cand_before(v, k, ov, ok);
+    if (mine_first != keep_first) {
+      v = ov;
+      k = ok;
+    }
+  };
+  step(16, ((lg & 1) == 0) == ((lg & 2) == 0));  // pairs: (0,1) descending, (2,3) ascending
+  step(32, (lg & 2) == 0);
+  step(16, (lg & 1) == 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -224,13 +260,13 @@ __device__ __forceinline__ void load_v_pairs(u32x4 (&va)[(kTile / 2) / (64 / (D 
 // end.  Output per (head, chunk, split, row): running max (log2 domain),
 // running sum, and the unnormalised fp32 y row.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int WAVES, int MINW, int PS>
+template <typename T, int D, int WAVES, int MINW>
 __global__ void __launch_bounds__(64 * WAVES, MINW)
 pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
              const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int n_splits, int kps,
              float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y,
-             int* __restrict__ part_arg) {
+             int2* __restrict__ part_cand) {
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
   constexpr int DT = D / 16;
@@ -241,7 +277,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 
   constexpr int kYPitch = D + 4;  // fp32 row pitch of the merge buffer
   constexpr int kLdsTiles = WAVES * D * kPitch;
-  constexpr int kLdsMerge = 4 * WAVES * kRows + WAVES * kRows * kYPitch;
+  constexpr int kLdsMerge = 3 * WAVES * kRows + 8 * WAVES * kRows + WAVES * kRows * kYPitch;
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsTiles > kLdsMerge ? kLdsTiles : kLdsMerge];
 
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -276,15 +312,17 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   uint32_t* vt = lds + wv * D * kPitch;
 
   float m2[kMB], lsum[kMB];
-  // Per lane: the lowest of its keys that holds the row's running maximum
-  // (INT_MAX if none of this lane's keys does).
-  int acand[kMB];
+  // Per lane: the largest logit among its own keys and the lowest key
+  // holding it (-1: none yet).
+  float lmax[kMB];
+  int larg[kMB];
   f32x4 yacc[DT][kMB];
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
     m2[mb] = -INFINITY;
     lsum[mb] = 0.f;
-    acand[mb] = INT_MAX;
+    lmax[mb] = -INFINITY;
+    larg[mb] = -1;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -333,14 +371,15 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     load_rows_op<T, D>(kop, krs, k_lane, tn);
     load_v_pairs<T, D>(va, vb, vrs, v_lane, tn);
 
-    // Online softmax.  P enters the MFMA as PS parts: one when the scores
-    // use p rounded to the input dtype (y is then only needed to that
-    // precision, see the merge kernel), hi + lo for the fp32 semantics.
+    // Online softmax.  P enters the MFMA as hi + lo: the p of a tile is
+    // relative to the running maximum, so rounding it to the input dtype
+    // here would not be the reference's rounding of the final p (merge
+    // applies that one to the keys where it matters).
     v8 phi[kMB], plo[kMB];
     if (pad_chunk || t0 + kTile > unmasked_end)
-      softmax_tile<T, D, PS, true>(s, m2, lsum, acand, yacc, phi, plo, bound, t0, lg, scale_log2);
+      softmax_tile<T, D, true>(s, m2, lsum, lmax, larg, yacc, phi, plo, bound, t0, lg, scale_log2);
     else
-      softmax_tile<T, D, PS, false>(s, m2, lsum, acand, yacc, phi, plo, bound, t0, lg, scale_log2);
+      softmax_tile<T, D, false>(s, m2, lsum, lmax, larg, yacc, phi, plo, bound, t0, lg, scale_log2);
 
     // Y^T += V^T P^T.  Lane (li, lg) reads V^T[16dt+li][keys 4lg..4lg+3, 16+4lg..+3].
 #pragma unroll
@@ -353,7 +392,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 #pragma unroll
       for (int mb = 0; mb < kMB; ++mb) {
         yacc[dt][mb] = Elem<T>::mfma(aop, phi[mb], yacc[dt][mb]);
-        if constexpr (PS == 2) yacc[dt][mb] = Elem<T>::mfma(aop, plo[mb], yacc[dt][mb]);
+        yacc[dt][mb] = Elem<T>::mfma(aop, plo[mb], yacc[dt][mb]);
       }
     }
   };
@@ -375,25 +414,25 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 
   // Cross-wave merge in LDS (the V tiles are dead now): every wave stores
   // its unscaled accumulator once; then all threads combine the waves with
-  // weights 2^(m_w - max_w m_w) and write the workgroup's partial.
+  // weights 2^(m_w - max_w m_w) and write the workgroup's partial.  The
+  // lanes' (logit, key) candidates of a row (4 per wave) are reduced to the
+  // kCand largest (the lowest key first among equal logits).
   __syncthreads();
   float* sm_m = reinterpret_cast<float*>(lds);
   float* sm_l = sm_m + WAVES * kRows;
   float* sm_f = sm_l + WAVES * kRows;
-  int* sm_a = reinterpret_cast<int*>(sm_f + WAVES * kRows);
-  float* wbuf = sm_f + 2 * WAVES * kRows;  // [WAVES][kRows][kYPitch]
-  // Key of each row's maximum: the lowest candidate over the lane groups.
+  float* sm_cs = sm_f + WAVES * kRows;                       // [WAVES][kRows][4]
+  int* sm_ck = reinterpret_cast<int*>(sm_cs + 4 * WAVES * kRows);
+  float* wbuf = sm_cs + 8 * WAVES * kRows;                   // [WAVES][kRows][kYPitch]
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
-    acand[mb] = min(acand[mb], __shfl_xor(acand[mb], 16));
-    acand[mb] = min(acand[mb], __shfl_xor(acand[mb], 32));
-  }
-  if (lg == 0) {
-#pragma unroll
-    for (int mb = 0; mb < kMB; ++mb) {
+    const int ci = (wv * kRows + 16 * mb + li) * 4 + lg;
+    sort_lane_groups(lmax[mb], larg[mb], lg);
+    sm_cs[ci] = lmax[mb];
+    sm_ck[ci] = larg[mb];
+    if (lg == 0) {
       sm_m[wv * kRows + 16 * mb + li] = m2[mb];
       sm_l[wv * kRows + 16 * mb + li] = lsum[mb];
-      sm_a[wv * kRows + 16 * mb + li] = acand[mb] == INT_MAX ? -1 : acand[mb];
     }
   }
 #pragma unroll
@@ -407,15 +446,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   if (threadIdx.x < kRows) {
     const int row = threadIdx.x;
     float mx = -INFINITY;
-    int arg = -1;
-    for (int w = 0; w < WAVES; ++w) {
-      const float mw = sm_m[w * kRows + row];
-      if (mw > mx) {
-        mx = mw;
-        arg = sm_a[w * kRows + row];
-      }
-    }
-    part_arg[slot * kRows + row] = arg;
+    for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, sm_m[w * kRows + row]);
     float l = 0.f;
     for (int w = 0; w < WAVES; ++w) {
       const float mw = sm_m[w * kRows + row];
@@ -425,6 +456,46 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     }
     part_ml[(slot * kRows + row) * 2 + 0] = mx;
     part_ml[(slot * kRows + row) * 2 + 1] = l;
+    // Merge the waves' sorted candidate lists (4 each) into the row's kCand
+    // first: each step takes the best head and advances that list.
+    static_assert(kCand <= 4, "at most one list's length");
+    float hv[WAVES];
+    int hk[WAVES], hp[WAVES];
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      hp[w] = 0;
+      hv[w] = sm_cs[(w * kRows + row) * 4];
+      hk[w] = sm_ck[(w * kRows + row) * 4];
+    }
+    float cs[kCand];
+    int ck[kCand];
+#pragma unroll
+    for (int j = 0; j < kCand; ++j) {
+      int bw = 0;
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) bw = cand_before(hv[w], hk[w], hv[bw], hk[bw]) ? w : bw;
+      float bv = hv[0];
+      int bk = hk[0];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) {
+        bv = bw == w ? hv[w] : bv;
+        bk = bw == w ? hk[w] : bk;
+      }
+      cs[j] = bv;
+      ck[j] = bk;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        if (bw == w) {
+          ++hp[w];
+          const bool more = hp[w] < 4;
+          hv[w] = more ? sm_cs[(w * kRows + row) * 4 + min(hp[w], 3)] : -INFINITY;
+          hk[w] = more ? sm_ck[(w * kRows + row) * 4 + min(hp[w], 3)] : -1;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kCand; ++j)
+      part_cand[(slot * kRows + row) * kCand + j] = make_int2(ck[j], __float_as_int(cs[j]));
   }
   __syncthreads();
   float* py = part_y + slot * kRows * D;
@@ -452,13 +523,13 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 // ---------------------------------------------------------------------------
 constexpr int kWideWaves = 8;
 
-template <typename T, int D, int PS, int kWideG>
+template <typename T, int D, int kWideG>
 __global__ void __launch_bounds__(64 * kWideWaves, 1)
 pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, bool qvec,
               const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
               int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int n_splits, int kps,
               float scale_log2, float* __restrict__ part_ml, float* __restrict__ part_y,
-              int* __restrict__ part_arg) {
+              int2* __restrict__ part_cand) {
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
   constexpr int DT = D / 16;
@@ -538,14 +609,15 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
     }
   };
 
-  float m2[kMB], lsum[kMB];
-  int acand[kMB];
+  float m2[kMB], lsum[kMB], lmax[kMB];
+  int larg[kMB];
   f32x4 yacc[DT][kMB];
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
     m2[mb] = -INFINITY;
     lsum[mb] = 0.f;
-    acand[mb] = INT_MAX;
+    lmax[mb] = -INFINITY;
+    larg[mb] = -1;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -584,9 +656,9 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
       }
       v8 phi[kMB], plo[kMB];
       if (pad_chunk || t0 + kTile > unmasked_end)
-        softmax_tile<T, D, PS, true>(s, m2, lsum, acand, yacc, phi, plo, bound, t0, lg, scale_log2);
+        softmax_tile<T, D, true>(s, m2, lsum, lmax, larg, yacc, phi, plo, bound, t0, lg, scale_log2);
       else
-        softmax_tile<T, D, PS, false>(s, m2, lsum, acand, yacc, phi, plo, bound, t0, lg, scale_log2);
+        softmax_tile<T, D, false>(s, m2, lsum, lmax, larg, yacc, phi, plo, bound, t0, lg, scale_log2);
       // Y^T += V^T P^T with V^T from LDS.
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
@@ -598,7 +670,7 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb) {
           yacc[dt][mb] = Elem<T>::mfma(aop, phi[mb], yacc[dt][mb]);
-          if constexpr (PS == 2) yacc[dt][mb] = Elem<T>::mfma(aop, plo[mb], yacc[dt][mb]);
+          yacc[dt][mb] = Elem<T>::mfma(aop, plo[mb], yacc[dt][mb]);
         }
       }
     }
@@ -614,22 +686,22 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
   }
   if (!active) return;
 
-  // This wave's rows are complete for the split: write the partials.
+  // This wave's rows are complete for the split: write the partials, and
+  // each lane its (logit, key) candidate of the row (kCand = 4 lanes a row).
+  static_assert(kCand == 4, "one candidate per lane group");
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
     lsum[mb] += __shfl_xor(lsum[mb], 16);
     lsum[mb] += __shfl_xor(lsum[mb], 32);
-    acand[mb] = min(acand[mb], __shfl_xor(acand[mb], 16));
-    acand[mb] = min(acand[mb], __shfl_xor(acand[mb], 32));
   }
   const int64_t slot = ((int64_t)head * n_mc + mc) * n_splits + split;
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
     const int row = 16 * mb + li;
+    part_cand[(slot * kRows + row) * kCand + lg] = make_int2(larg[mb], __float_as_int(lmax[mb]));
     if (lg == 0) {
       part_ml[(slot * kRows + row) * 2 + 0] = m2[mb];
       part_ml[(slot * kRows + row) * 2 + 1] = lsum[mb];
-      part_arg[slot * kRows + row] = acand[mb] == INT_MAX ? -1 : acand[mb];
     }
     float* py = part_y + (slot * kRows + row) * D;
 #pragma unroll
@@ -645,17 +717,21 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
 // in flight.  Writes, for the score pass, the row's Q / Y-hi / Y-lo operands
 // into the head's operand block (in the order pass 2's lanes read them from
 // LDS) and its statistics (lse in log2 units, |y|^2, the key holding at least
-// half of the row's attention if any, and -dist2/2 at that key), plus an fp32 copy of y
-// for inspection.  Optionally clears `zero_words` words at `zero_ptr` (the
+// half of the row's attention if any, and -dist2/2 at that key), plus an fp32
+// copy of y for inspection.  Optionally clears `zero_words` words at `zero_ptr` (the
 // selection workspace of a fused layer-call), so that needs no launch of its
 // own.
 // ---------------------------------------------------------------------------
 constexpr int kMergeRows = 1;  // waves (rows) per workgroup
 constexpr int kMaxSplits = 1024;
+// Candidates whose final p is at least this get their rounding error
+// (round(p) - p) v added to y; below it, that error is under 2^-20 |v|.
+constexpr float kCorrMinP = 1.0f / 4096.0f;
+constexpr int kCorrKeys = 8;  // candidates corrected per row (the largest p)
 
 template <typename T, int D>
 __global__ void __launch_bounds__(64 * kMergeRows)
-merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y, const int* __restrict__ part_arg,
+merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y, const int2* __restrict__ part_cand,
              int n_mc, int n_splits, int M, int n_rows, int p_round, int y_round, const T* __restrict__ q,
              int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_sd, const T* __restrict__ vp, int kv_ld, int Lk,
              int Hkv, int g, int W, int Lq, u32x4* __restrict__ opblk, float* __restrict__ stblk,
@@ -698,14 +774,28 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
 #pragma unroll
     for (int e = 0; e < DPL; ++e) qv[e] = valid ? qrow[(int64_t)(d0 + e) * q_sd] : static_cast<T>(0.f);
   }
+  // The row's (key, logit) candidates, kCand per split: lane l reads
+  // candidates l, l + 64, ... and keeps its two largest (lowest key first
+  // among equal logits).  Ranking by logit ranks by p, so the kCorrKeys
+  // largest are chosen, and their value rows loaded, before the lse is
+  // known; the p threshold is applied once it is.
+  const int ncand = n_splits * kCand;
+  typedef int i32x2 __attribute__((ext_vector_type(2)));
+  const i32x2* pc2 = reinterpret_cast<const i32x2*>(part_cand);
+  auto cand_at = [&](int c) {
+    return pc2[((slot0 + c / kCand) * kRows + row) * kCand + c % kCand];
+  };
+  constexpr int kCandPre = 4;  // candidates per lane loaded up front
+  i32x2 kcp[kCandPre];
+#pragma unroll
+  for (int j = 0; j < kCandPre; ++j) kcp[j] = lane + 64 * j < ncand ? cand_at(lane + 64 * j) : i32x2{-1, 0};
   // Split statistics: lane s holds (m, l) of split s (the first 64 in
   // registers, any further ones re-read in the rare loops below).
   const float2 ml = lane < n_splits ? *reinterpret_cast<const float2*>(part_ml + ((slot0 + lane) * kRows + row) * 2)
                                     : make_float2(-INFINITY, 0.f);
-  const int arg_lane = lane < n_splits ? part_arg[(slot0 + lane) * kRows + row] : -1;
   float mx = ml.x;
   for (int s = 64 + lane; s < n_splits; s += 64) mx = fmaxf(mx, part_ml[((slot0 + s) * kRows + row) * 2]);
-  mx = wave_max(mx);
+  mx = wave_max_dpp(mx);
   const bool valid = gr < M && mx != -INFINITY;
 
   auto weight = [&](float m) { return (m == -INFINITY || mx == -INFINITY) ? 0.f : exp2f(m - mx); };
@@ -713,44 +803,85 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   float lpart = ml.y * f_lane;
   for (int s = 64 + lane; s < n_splits; s += 64)
     lpart += part_ml[((slot0 + s) * kRows + row) * 2 + 1] * weight(part_ml[((slot0 + s) * kRows + row) * 2]);
-  const float l = wave_sum(lpart);
+  const float l = wave_sum_dpp(lpart);
   const float lse2 = mx + log2f(fmaxf(l, 1e-40f));
 
   // y from the probabilities rounded to the input dtype (the reference's
   // semantics with p rounding, dropkv_triton.py:88-93).  Pass 1 summed the
-  // unrounded p; adding (round(p_k) - p_k) v_k for the row's top key k makes
-  // up the part that matters.  Every key's rounding error is at most 2^-9 of
-  // its p, so the others move y by at most 2^-9 (1 - p_k) |v|, a relative
-  // error below 1e-3 in every distance.  The top key's own term matters
-  // because |v_k - y| shrinks with 1 - p_k: without it, dist2 at that key is
-  // wrong by up to tens of percent once p_k approaches 1.  Below p_k = 1/2
-  // the term changes no distance by more than 0.5%, and the row skips the
-  // dependent load of v_k.  The same top key (in every mode) gets its
-  // distance computed directly below.
-  int k_top = -1;
-  float dk = 0.f;
-  fv vk = {};
-  if (valid) {
-    const float pk = fminf(__builtin_amdgcn_exp2f(mx - lse2), 1.f);
-    if (pk >= 0.5f) {
-      const uint64_t hit = __ballot(lane < n_splits && ml.x == mx);
-      if (hit) {
-        k_top = __shfl(arg_lane, __builtin_ctzll(hit));
-      } else {
-        for (int s = 64; s < n_splits; ++s)
-          if (part_ml[((slot0 + s) * kRows + row) * 2] == mx) {
-            k_top = part_arg[(slot0 + s) * kRows + row];
-            break;
-          }
-      }
-      if (k_top >= 0 && k_top < Lk) {
-        if (p_round) dk = round_through<T>(pk) - pk;
-        const T* vrow = vp + ((int64_t)head * kv_ld + k_top) * D + d0;
+  // unrounded p (the rounded p needs the final lse).  Of the candidates (the
+  // keys holding the largest logits of individual lanes of pass 1), the
+  // kCorrKeys largest that take at least kCorrMinP of the row's attention
+  // get (round(p) - p) v added here.  Each key's rounding error is at most
+  // 2^-8 of its p, so these are the errors that can move a distance: a row
+  // whose few largest keys went uncorrected would leave relative errors of
+  // 1e-3 in other keys' scores.  The largest candidate is the row's top key
+  // (the lowest key among those holding the maximum); when it takes at least
+  // half of the attention its distance is also computed directly below.
+  int ck[kCorrKeys];
+  float cs[kCorrKeys];
+  fv vb[kCorrKeys];
+  {
+    float sa = -INFINITY, sb = -INFINITY;
+    int ka = -1, kb = -1;
+    // Branch-free insertion into the lane's two best (selects only, so the
+    // four values stay in registers).
+    auto offer = [&](i32x2 kc) __attribute__((always_inline)) {
+      const float sc = __int_as_float(kc.y);
+      const int kx = (kc.x >= 0 && kc.x < Lk) ? kc.x : -1;
+      const bool ga = cand_before(sc, kx, sa, ka);
+      const bool gb = !ga && cand_before(sc, kx, sb, kb);
+      const float nsb = ga ? sa : (gb ? sc : sb);
+      const int nkb = ga ? ka : (gb ? kx : kb);
+      sa = ga ? sc : sa;
+      ka = ga ? kx : ka;
+      sb = nsb;
+      kb = nkb;
+    };
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) vk[e] = static_cast<float>(vrow[e]);
-      } else {
-        k_top = -1;
+    for (int j = 0; j < kCandPre; ++j) offer(kcp[j]);
+    for (int c = lane + 64 * kCandPre; c < ncand; c += 64) offer(cand_at(c));
+#pragma unroll
+    for (int u = 0; u < kCorrKeys; ++u) {
+      const float best = wave_max_dpp(ka >= 0 ? sa : -INFINITY);
+      const uint64_t tie = __ballot(ka >= 0 && sa == best);
+      int kmin = INT_MAX;
+      if (tie) {
+        kmin = __builtin_amdgcn_readlane(ka, __builtin_ctzll(tie));
+        if (tie & (tie - 1)) kmin = wave_min_dpp((ka >= 0 && sa == best) ? ka : INT_MAX);  // equal logits
       }
+      ck[u] = kmin == INT_MAX ? -1 : kmin;
+      cs[u] = best;
+      if (ka == kmin && kmin != INT_MAX) {
+        sa = sb;
+        ka = kb;
+        sb = -INFINITY;
+        kb = -1;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kCorrKeys; ++u) {
+      vb[u] = fv{};
+      if (ck[u] >= 0 && (p_round || u == 0)) {
+        const T* vrow = vp + ((int64_t)head * kv_ld + ck[u]) * D + d0;
+#pragma unroll
+        for (int e2 = 0; e2 < DPL; ++e2) vb[u][e2] = static_cast<float>(vrow[e2]);
+      }
+    }
+  }
+  int k_top = -1;
+  fv vk = {}, corr = {};
+  if (valid) {
+    if (p_round) {
+#pragma unroll
+      for (int u = 0; u < kCorrKeys; ++u) {
+        const float pc = ck[u] >= 0 ? fminf(__builtin_amdgcn_exp2f(cs[u] - lse2), 1.f) : 0.f;
+        if (pc >= kCorrMinP) corr += (round_through<T>(pc) - pc) * vb[u];
+      }
+    }
+    const float pk = fminf(__builtin_amdgcn_exp2f(mx - lse2), 1.f);
+    if (pk >= 0.5f && ck[0] >= 0 && cs[0] == mx) {
+      k_top = ck[0];
+      vk = vb[0];
     }
   }
 
@@ -758,7 +889,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   fv acc = {};
 #pragma unroll
   for (int s = 0; s < kPre; ++s)
-    if (s < n_splits) acc += __shfl(f_lane, s) * yv[s];
+    if (s < n_splits) acc += read_lane_f(f_lane, s) * yv[s];
   // Further splits in batches of 8 whose loads are all issued before use.
   for (int s0 = kPre; s0 < n_splits; s0 += 8) {
     fv yb[8];
@@ -769,7 +900,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
     for (int u = 0; u < 8; ++u) {
       const int s = s0 + u;
       if (s < n_splits) {
-        const float fs = s < 64 ? __shfl(f_lane, s) : weight(part_ml[((slot0 + s) * kRows + row) * 2]);
+        const float fs = s < 64 ? read_lane_f(f_lane, s) : weight(part_ml[((slot0 + s) * kRows + row) * 2]);
         acc += fs * yb[u];
       }
     }
@@ -782,7 +913,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
 #pragma unroll
   for (int e = 0; e < DPL; ++e) {
     const int d = d0 + e;
-    float y = valid ? acc[e] / l + dk * vk[e] : 0.f;
+    float y = valid ? acc[e] / l + corr[e] : 0.f;
     const T hi = static_cast<T>(y);
     if (y_round) y = static_cast<float>(hi);
     const T lo = static_cast<T>(y - static_cast<float>(hi));
@@ -799,8 +930,8 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
     ob[((size_t)((1 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = hi;
     ob[((size_t)((2 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = lo;
   }
-  const float yn2 = wave_sum(ysq);
-  const float nd2_top = -0.5f * wave_sum(dsq);
+  const float yn2 = wave_sum_dpp(ysq);
+  const float nd2_top = -0.5f * wave_sum_dpp(dsq);
   if (lane == 0) {
     const float lse_row = valid ? lse2 : INFINITY;
     ystat[rbase * 2 + 0] = lse_row;
@@ -1168,7 +1299,7 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   const size_t slots = (size_t)p.heads * p.n_mc * p.s1;
   p.off_ml = take(slots * kRows * 2 * sizeof(float));
   p.off_y = take(slots * kRows * D * sizeof(float));
-  p.off_arg = take(slots * kRows * sizeof(int));
+  p.off_cand = take(slots * kRows * kCand * sizeof(int2));
   p.off_op = take((size_t)p.heads * p.n_mc * kOpSlots * kMB * (D / 32) * 64 * 16);
   p.off_stb = take((size_t)p.heads * p.n_mc * kMB * kStatWords * sizeof(float));
   p.off_stat = take((size_t)p.heads * p.mpad * 2 * sizeof(float));
@@ -1189,7 +1320,7 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   float* stblk = reinterpret_cast<float*>(ws + p.off_stb);
   float* ystat = reinterpret_cast<float*>(ws + p.off_stat);
   float* yf = reinterpret_cast<float*>(ws + p.off_yf);
-  int* part_arg = reinterpret_cast<int*>(ws + p.off_arg);
+  int2* part_cand = reinterpret_cast<int2*>(ws + p.off_cand);
   const T* qq = static_cast<const T*>(q);
   const T* kk = static_cast<const T*>(k);
   const T* vv = static_cast<const T*>(v);
@@ -1197,38 +1328,20 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   const bool qvec = q_sd == 1 && (q_sb % 8) == 0 && (q_sh % 8) == 0 && (q_ss % 8) == 0 &&
                     (reinterpret_cast<uintptr_t>(q) & 15u) == 0;
   const dim3 g1(p.heads * p.n_mc * p.s1);
-  auto launch1 = [&](auto ps) {
-    constexpr int PS = decltype(ps)::value;
-    if (p.p1_wide) {
-      auto wide = [&](auto grp) {
-        constexpr int G = decltype(grp)::value;
-        launch((pass1w_kernel<T, D, PS, G>), dim3(p.heads * p.s1), dim3(64 * kWideWaves), 0, st, qq,
-                           q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1,
-                           scale_log2, part_ml, part_y, part_arg);
-      };
-      if (p.p1_wide == 4)
-        wide(std::integral_constant<int, 4>{});
-      else if (p.p1_wide == 2)
-        wide(std::integral_constant<int, 2>{});
-      else
-        wide(std::integral_constant<int, 1>{});
-    } else if (p.p1_waves == 8) {
-      launch((pass1_kernel<T, D, 8, 1, PS>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
-                         vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y,
-                         part_arg);
-    } else {
-      launch((pass1_kernel<T, D, 4, 1, PS>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk,
-                         vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y,
-                         part_arg);
-    }
-  };
-  if (p_round)
-    launch1(std::integral_constant<int, 1>{});
-  else
-    launch1(std::integral_constant<int, 2>{});
+  if (p.p1_wide) {
+    launch((pass1w_kernel<T, D, DKV_P1_WIDE_GROUP>), dim3(p.heads * p.s1), dim3(64 * kWideWaves), 0, st, qq, q_sb,
+           q_sh, q_ss, q_sd, qvec, kk, vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml,
+           part_y, part_cand);
+  } else if (p.p1_waves == 8) {
+    launch((pass1_kernel<T, D, 8, 1>), g1, dim3(512), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, kv_ld, Hkv,
+           Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_cand);
+  } else {
+    launch((pass1_kernel<T, D, 4, 1>), g1, dim3(256), 0, st, qq, q_sb, q_sh, q_ss, q_sd, qvec, kk, vv, kv_ld, Hkv,
+           Lq, Lk, W, p.g, p.M, p.n_mc, p.s1, p.kps1, scale_log2, part_ml, part_y, part_cand);
+  }
   const int n_rows = p.heads * p.mpad;
   launch((merge_kernel<T, D>), dim3((n_rows + kMergeRows - 1) / kMergeRows), dim3(64 * kMergeRows), 0, st,
-                     part_ml, part_y, part_arg, p.n_mc, p.s1, p.M, n_rows, p_round, y_round, qq, q_sb, q_sh, q_ss,
+                     part_ml, part_y, part_cand, p.n_mc, p.s1, p.M, n_rows, p_round, y_round, qq, q_sb, q_sh, q_ss,
                      q_sd, vv, kv_ld, Lk, Hkv, p.g, W, Lq, opblk, stblk, ystat, yf, zero_ptr, zero_words);
   SelFuse fz{};
   // Row-chunks whose operands share LDS in one sweep over the keys (every

@@ -177,6 +177,40 @@ class DropKVCache(_LayerCache):
         protect = min(self.window_size, seq_len)
         return ops.select(scores, self.kernel_size, protect, keep_len)
 
+    def _fast_path_ok(self, query_states, key_states, value_states) -> bool:
+        """Whether ``dropkv_scores_triton`` accepts these inputs (its
+        ``AssertionError`` guards, dropkv_triton.py:680-716); K/V count as
+        contiguous because the fused call makes them so, as
+        ``_compute_keep_indices`` passes ``.contiguous()`` copies
+        (dropkv_cache.py:392-398)."""
+        if not self.use_triton:
+            return False
+        try:
+            from .dropkv_triton import check_scoring_inputs
+            check_scoring_inputs(query_states, key_states, value_states, self.window_size,
+                                 require_contiguous=False)
+            return True
+        except (ImportError, AssertionError):
+            return False
+
+    def _evict_layer(self, query_states: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,
+                     total_tokens: Optional[int] = None, max_keep_len: Optional[int] = None):
+        """``_compute_keep_indices`` followed by ``_gather_compressed``
+        (dropkv_cache.py:355-491) as one fused layer-call (``dropkv_evict``:
+        score, pool, protect, top-k, sort, gather), with the same scoring
+        choice, keep length and protection.  Returns the compressed K/V."""
+        bsz, num_kv_heads, seq_len, head_dim = key_states.shape
+        num_query_heads = query_states.shape[1]
+        if num_query_heads % num_kv_heads != 0:
+            raise ValueError(f"Query heads {num_query_heads} must be divisible by KV heads {num_kv_heads}")
+        fast = self._fast_path_ok(query_states, key_states, value_states)
+        W = self.window_size if fast else min(self.window_size, query_states.shape[2])
+        keep = self._keep_length(seq_len, total_tokens, max_keep_len)
+        _, key_c, value_c = ops.evict(query_states, key_states, value_states, W, self.kernel_size, keep,
+                                      protect_window=min(self.window_size, seq_len), eps=1e-6, p_round=True,
+                                      y_round=not fast)
+        return key_c, value_c
+
     @staticmethod
     def _gather_compressed(key_states: torch.Tensor, value_states: torch.Tensor,
                            keep_idx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -238,10 +272,8 @@ class DropKVCache(_LayerCache):
                 return key_states, value_states
 
             total_tok = self._seen_tokens if self._evict_use_seen_tokens else None
-            keep_idx = self._compute_keep_indices(query_states, key_states, value_states,
-                                                  total_tokens=total_tok,
-                                                  max_keep_len=self._budget_max_kv_tokens)
-            key_c, value_c = self._gather_compressed(key_states, value_states, keep_idx)
+            key_c, value_c = self._evict_layer(query_states, key_states, value_states, total_tokens=total_tok,
+                                               max_keep_len=self._budget_max_kv_tokens)
             self.key_cache.append(key_c)
             self.value_cache.append(value_c)
             return key_states, value_states
@@ -256,10 +288,8 @@ class DropKVCache(_LayerCache):
             full_value = torch.cat([self.value_cache[layer_idx], value_states], dim=-2)
             if query_states is not None and full_key.shape[2] >= self.window_size:
                 total_tok = self._seen_tokens if self._evict_use_seen_tokens else None
-                keep_idx = self._compute_keep_indices(query_states, full_key, full_value,
-                                                      total_tokens=total_tok,
-                                                      max_keep_len=self._budget_max_kv_tokens)
-                key_c, value_c = self._gather_compressed(full_key, full_value, keep_idx)
+                key_c, value_c = self._evict_layer(query_states, full_key, full_value, total_tokens=total_tok,
+                                                   max_keep_len=self._budget_max_kv_tokens)
                 self.key_cache[layer_idx] = key_c
                 self.value_cache[layer_idx] = value_c
             else:
@@ -315,15 +345,7 @@ class DropKVCache(_LayerCache):
         raises ``ValueError`` when the kept rows exceed the capacity."""
         if query_states.shape[1] % k_src.shape[1] != 0:
             raise ValueError(f"Query heads {query_states.shape[1]} must be divisible by KV heads {k_src.shape[1]}")
-        fast = False
-        if self.use_triton:
-            try:
-                from .dropkv_triton import check_scoring_inputs
-                check_scoring_inputs(query_states, k_src[:, :, :Lk], v_src[:, :, :Lk], self.window_size,
-                                     require_contiguous=False)
-                fast = True
-            except AssertionError:
-                fast = False
+        fast = self._fast_path_ok(query_states, k_src[:, :, :Lk], v_src[:, :, :Lk])
         W = self.window_size if fast else min(self.window_size, query_states.shape[2])
         total_tok = self._seen_tokens if self._evict_use_seen_tokens else None
         keep = self._keep_length(Lk, total_tok, self._budget_max_kv_tokens)

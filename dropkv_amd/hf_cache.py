@@ -47,6 +47,9 @@ def _evict(query_states: torch.Tensor, key_states: torch.Tensor, value_states: t
     dtype, ``y = p @ V`` in the input dtype).  Pooling over ``kernel_size``,
     protection of the last ``window_size`` keys at ``max + 1``, top-``keep``
     and the ascending sort follow patch:181-192; the gather patch:194-202.
+    One fused layer-call; the outputs are new tensors and the workspace is
+    the current stream's shared one, so consecutive layers allocate no
+    workspace.
     """
     key_states = key_states.contiguous()
     value_states = value_states.contiguous()
@@ -58,9 +61,8 @@ def _evict(query_states: torch.Tensor, key_states: torch.Tensor, value_states: t
         except AssertionError:
             fast = False
     W = window_size if fast else min(window_size, query_states.shape[2])
-    plan = ops.EvictPlan(query_states, key_states, W, kernel_size, keep, protect_window=window_size,
-                         p_round=True, y_round=not fast)
-    return plan(query_states, key_states, value_states)
+    return ops.evict(query_states, key_states, value_states, W, kernel_size, keep, protect_window=window_size,
+                     p_round=True, y_round=not fast)
 
 
 class DropKVLayer(DynamicLayer):

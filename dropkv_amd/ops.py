@@ -9,6 +9,8 @@ alignment) and raise ``RuntimeError`` otherwise; the reference-compatible
 
 from __future__ import annotations
 
+import threading
+
 import torch
 
 from . import _lib
@@ -22,6 +24,27 @@ def _stream(dev: torch.device) -> int:
 
 def _workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+
+# One workspace per (device, stream), grown on demand and reused by every
+# ``evict`` call on that stream: calls on one stream run in order, so they
+# never use it at the same time.
+_shared_ws: dict = {}
+_shared_ws_lock = threading.Lock()
+
+
+def _stream_workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
+    nbytes = max(int(nbytes), 1)
+    stream = torch.cuda.current_stream(dev)
+    if torch.cuda.is_current_stream_capturing():
+        return _workspace(nbytes, dev)  # a graph keeps its own (private-pool) workspace
+    key = (dev.index, stream.cuda_stream)
+    with _shared_ws_lock:
+        ws = _shared_ws.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            _shared_ws[key] = ws
+    return ws
 
 
 def _aligned(t: torch.Tensor) -> bool:
@@ -201,6 +224,37 @@ def evict_ld(Q: torch.Tensor, k_buf: torch.Tensor, v_buf: torch.Tensor, Lk: int,
                              ws.numel(), _stream(dev))
     _lib.check(rc, "dropkv_evict_ld")
     return idx
+
+
+def evict(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, window: int, kernel_size: int, keep: int,
+          protect_window: int | None = None, eps: float = 1e-6, p_round: bool = True, y_round: bool = False,
+          splits: int = 0):
+    """One layer-call (``dropkv_evict``): score, pool, protect, top-k, sort and
+    gather in one call.  Returns fresh ``(keep_idx [B,Hkv,keep] int64,
+    k_out, v_out [B,Hkv,keep,D])``, like the reference's
+    ``_compute_keep_indices`` + ``_gather_compressed``; the workspace is the
+    current stream's shared one."""
+    dev = _check_device(Q, K, V)
+    if Q.dtype not in _DTYPE_CODE or K.dtype != Q.dtype or V.dtype != Q.dtype:
+        raise RuntimeError(f"unsupported dtype combination {Q.dtype}/{K.dtype}/{V.dtype}")
+    if K.shape != V.shape:
+        raise RuntimeError("K and V must have the same shape")
+    B, Hq, Lq, D = Q.shape
+    Hkv, Lk = K.shape[1], K.shape[2]
+    K = _kv_operand(K)
+    V = _kv_operand(V)
+    lib = _lib.load()
+    ws = _stream_workspace(lib.dropkv_evict_workspace_bytes(B, Hq, Hkv, Lk, D, window, splits), dev)
+    idx = torch.empty(B, Hkv, keep, dtype=torch.int64, device=dev)
+    ko = torch.empty(B, Hkv, keep, D, dtype=K.dtype, device=dev)
+    vo = torch.empty_like(ko)
+    pw = window if protect_window is None else protect_window
+    rc = lib.dropkv_evict(Q.data_ptr(), *Q.stride(), K.data_ptr(), V.data_ptr(), _DTYPE_CODE[Q.dtype],
+                          B, Hq, Hkv, Lq, Lk, D, int(window), float(eps), int(bool(p_round)), int(bool(y_round)),
+                          int(splits), int(kernel_size), int(pw), int(keep), None, idx.data_ptr(), ko.data_ptr(),
+                          vo.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+    _lib.check(rc, "dropkv_evict")
+    return idx, ko, vo
 
 
 class EvictPlan:

@@ -80,3 +80,92 @@ def golden_case(name):
         if key in d:
             out[key] = torch.from_numpy(d[key].copy())
     return out
+
+
+# ---------------------------------------------------------------------------
+# Score bars that bind at full size
+# ---------------------------------------------------------------------------
+def binding_keys(ref, pooled_ref, keep, frac=0.1):
+    """Keys whose reference score is at least ``frac`` times the row's keep
+    threshold (the keep-th largest pooled, protected reference value): the
+    keys whose scores can move the selection.  At full size almost every
+    other key scores far below any absolute tolerance (scores scale like
+    p^2 with p ~ 1/Lk), so a bar over all keys binds on almost nothing."""
+    T = torch.topk(pooled_ref.double(), keep, dim=-1).values[..., -1:]
+    return ref.double() >= frac * T
+
+
+def assert_binding_scores(got, ref, pooled_ref, keep, Qt, K, V, W, p_round, max_rel, rel_bar, frac_above,
+                          frac=0.1, excuse_sinks=True, max_arbitrated=4096):
+    """Relative bars on the binding keys: every one within ``max_rel`` and
+    fewer than ``frac_above`` of them beyond ``rel_bar``.
+
+    A key beyond ``rel_bar`` against the float32 reference is arbitrated in
+    float64 (the oracle's ``dropkv_scores_fp64``: the same formula with the
+    direct distance, p rounded from a float64 p, and with p off by 2^-20
+    before the rounding, which can flip it to the neighbouring bf16 value):
+    it counts as within a bar if it is within it of either evaluation.  With
+    ``excuse_sinks`` a key beyond ``max_rel`` of both may still pass within
+    four times the rounding bound of a float32 expansion of that score (an
+    attention sink, p ~ 1: no float32 evaluation determines it); such keys
+    must stay under 1e-3 of the row; the same rule excuses a key from the
+    count beyond ``rel_bar``.  Returns (binding keys, worst relative error
+    after arbitration, keys beyond rel_bar, sink-excused keys)."""
+    from oracle import dropkv_ref as R
+    got, ref = got.double().cpu(), ref.double().cpu()
+    sel = binding_keys(ref, pooled_ref.cpu(), keep, frac)
+    rel = torch.where(sel, (got - ref).abs() / ref.abs().clamp_min(1e-300), torch.zeros_like(ref))
+    B, Hkv, Lk = ref.shape
+    g = Qt.shape[1] // Hkv
+    worst, n_above, n_excused = 0.0, 0, 0
+    probes = (1.0,) if p_round is None else (1.0, 1 - 2.0 ** -20, 1 + 2.0 ** -20)
+    for b in range(B):
+        for h in range(Hkv):
+            r = rel[b, h]
+            keys = torch.nonzero(r > rel_bar).flatten()
+            assert keys.numel() <= max_arbitrated, ((b, h), keys.numel(), float(r.max()))
+            best = r.clone()
+            if keys.numel():
+                gk = got[b, h, keys]
+                qh = Qt[b:b + 1, h * g:(h + 1) * g].cpu()
+                kh, vh = K[b:b + 1, h:h + 1].cpu(), V[b:b + 1, h:h + 1].cpu()
+                r64s, bnd = [], None
+                for f in probes:
+                    r64, bb = R.dropkv_scores_fp64(qh, kh, vh, W, p_round=p_round, p_scale=f, keys=keys,
+                                                   return_bound=True)
+                    r64s.append(r64[0, 0])
+                    bnd = bb[0, 0] if bnd is None else torch.maximum(bnd, bb[0, 0])
+                r64s = torch.stack(r64s)
+                rel64 = ((gk[None] - r64s).abs() / r64s.abs().clamp_min(1e-300)).min(0).values
+                best[keys] = torch.minimum(r[keys], rel64)
+                beyond = best[keys] > max_rel
+                if beyond.any():
+                    assert excuse_sinks, ((b, h), keys[beyond][:8].tolist(), best[keys][beyond][:8].tolist())
+                    slack = ((gk[None] - r64s).abs() - max_rel * r64s.abs() - 4 * bnd[None]).min(0).values
+                    assert (slack[beyond] <= 0).all(), ((b, h), keys[beyond][slack[beyond] > 0][:8].tolist())
+                    row_sinks = int(beyond.sum())
+                    best[keys[beyond]] = 0.0
+                else:
+                    row_sinks = 0
+                # Keys beyond rel_bar whose distance from a float64 evaluation
+                # is within four times the float32 rounding bound of their
+                # score are sinks too (no float32 evaluation determines them
+                # to rel_bar).
+                beyond_bar = best[keys] > rel_bar
+                if excuse_sinks and beyond_bar.any():
+                    slack = ((gk[None] - r64s).abs() - rel_bar * r64s.abs() - 4 * bnd[None]).min(0).values
+                    sink = beyond_bar & (slack <= 0)
+                    row_sinks += int(sink.sum())
+                    best[keys[sink]] = 0.0
+                assert row_sinks <= 1e-3 * Lk, ((b, h), row_sinks)
+                n_excused += row_sinks
+            worst = max(worst, float(best.max()))
+            above = torch.nonzero(best > rel_bar).flatten()
+            n_above += int(above.numel())
+            for key in above[:8].tolist():
+                print(f"  beyond {rel_bar:g}: (b={b}, h={h}) key {key}: got {float(got[b, h, key]):.6e} "
+                      f"ref32 {float(ref[b, h, key]):.6e} rel32 {float(r[key]):.2e} best {float(best[key]):.2e}")
+    n_sel = int(sel.sum())
+    assert n_above < frac_above * max(n_sel, 1), (n_above, n_sel)
+    assert worst <= max_rel, worst
+    return n_sel, worst, n_above, n_excused

@@ -237,6 +237,40 @@ def test_fast_path_guard_falls_back_to_deployed_semantics(monkeypatch):
         c._compute_keep_indices(Q, K, V)
 
 
+def test_update_evicts_in_one_fused_call(monkeypatch):
+    """update() runs _compute_keep_indices + _gather_compressed as one
+    ops.evict call (score, pool, protect, top-k, sort, gather) with the same
+    choice of scoring semantics: the fast path's (W = window, y in fp32) when
+    its guards pass, else the deployed path's (W = min(window, Lq), y rounded
+    to the input dtype), and the same keep length and protection."""
+    import dropkv_amd.dropkv_cache as C
+    import dropkv_amd.dropkv_triton as T
+    calls = []
+
+    def evict(q, k, v, W, ks, keep, protect_window=None, eps=1e-6, p_round=True, y_round=False, splits=0):
+        calls.append((W, ks, keep, protect_window, p_round, y_round))
+        idx = torch.arange(keep).expand(k.shape[0], k.shape[1], keep)
+        return idx, k[:, :, :keep], v[:, :, :keep]
+
+    monkeypatch.setattr(C.ops, "evict", evict)
+    Q, K, V = make_qkv(LLAMA_CFG, 64)
+    c = _cache(use_triton=True)          # CPU tensors fail the fast-path guard
+    c.update(Q[:, :, -4:], K, V, layer_idx=0)
+    assert calls[-1] == (4, 11, 19, 8, True, True)
+    assert c.key_cache[0].shape[2] == 19
+    monkeypatch.setattr(T, "check_scoring_inputs", lambda *a, **k: None)   # guards pass
+    c.update(Q, K, V, layer_idx=1)
+    assert calls[-1] == (8, 11, 19, 8, True, False)
+    c2 = _cache(use_triton=False)
+    c2.update(Q, K, V, layer_idx=0)
+    assert calls[-1] == (8, 11, 19, 8, True, True)
+    # evict_accumulated: stored || chunk, keep from the tokens seen
+    c2._prefill_mode = "evict_accumulated"
+    c2._evict_use_seen_tokens = True
+    rk, _ = c2.update(Q[:, :, :32], K[:, :, :32], V[:, :, :32], layer_idx=0)
+    assert rk.shape[2] == 19 + 32 and calls[-1] == (8, 11, int(0.3 * 96), 8, True, True)
+
+
 # --- prefill_chunked (dropkv_cache.py:651-807) --------------------------------
 
 def test_prefill_chunked_rejects_wrong_cache_type():

@@ -145,20 +145,33 @@ def test_fast_path_handles_mismatched_q_length(gpu):
 
 
 def test_fast_path_is_the_hip_op(gpu, monkeypatch):
-    """With use_triton=True the cache calls dropkv_scores_triton (reference
-    tests:1919-1960)."""
+    """With use_triton=True the cache scores with the fast path's semantics
+    (reference tests:1919-1960): its prefill eviction is one fused HIP
+    layer-call with y in fp32, and _compute_keep_indices calls
+    dropkv_scores_triton; both keep the same rows."""
     import dropkv_amd.dropkv_triton as T
+    from dropkv_amd import ops
     calls = []
-    real = T.dropkv_scores_triton
+    real_scores, real_evict = T.dropkv_scores_triton, ops.evict
 
-    def spy(*a, **k):
-        calls.append(1)
-        return real(*a, **k)
+    def spy_scores(*a, **k):
+        calls.append("scores")
+        return real_scores(*a, **k)
 
-    monkeypatch.setattr(T, "dropkv_scores_triton", spy)
+    def spy_evict(*a, **k):
+        calls.append(("evict", k.get("y_round")))
+        return real_evict(*a, **k)
+
+    monkeypatch.setattr(T, "dropkv_scores_triton", spy_scores)
+    monkeypatch.setattr(ops, "evict", spy_evict)
     Q, K, V = _qkv(LLAMA_CFG, 128, seed=10, dev=gpu)
-    _cache(use_triton=True).update(Q, K, V, layer_idx=0)
-    assert calls == [1]
+    c = _cache(use_triton=True)
+    c.update(Q, K, V, layer_idx=0)
+    assert calls == [("evict", False)]
+    idx = c._compute_keep_indices(Q, K, V)
+    assert calls[-1] == "scores"
+    rk, rv = ops.compact(K, V, idx)
+    assert torch.equal(c.key_cache[0], rk) and torch.equal(c.value_cache[0], rv)
 
 
 @pytest.mark.parametrize("cfg,L", [(LLAMA_CFG, 4096), (QWEN_CFG, 4096)])

@@ -49,11 +49,13 @@ def _oracle_evict(calls=None):
 
 
 def _oracle_standalone(monkeypatch):
-    def keep_indices(self, q, k, v, total_tokens=None, max_keep_len=None):
-        return R.compute_keep_indices(q, k, v, self.keep_ratio, self.window_size, self.kernel_size,
-                                      total_tokens, max_keep_len)[0]
-    monkeypatch.setattr(DropKVCache, "_compute_keep_indices", keep_indices)
-    monkeypatch.setattr(DropKVCache, "_gather_compressed", staticmethod(R.gather_compressed))
+    """The standalone cache's fused eviction (score .. gather) replaced by
+    the oracle's deployed path."""
+    def evict_layer(self, q, k, v, total_tokens=None, max_keep_len=None):
+        idx = R.compute_keep_indices(q, k, v, self.keep_ratio, self.window_size, self.kernel_size,
+                                     total_tokens, max_keep_len)[0]
+        return R.gather_compressed(k, v, idx)
+    monkeypatch.setattr(DropKVCache, "_evict_layer", evict_layer)
 
 
 def _decode_reference(model, cfg, layers_kv, token, position):
@@ -228,11 +230,11 @@ def test_hf5_update_forms_route_the_query(monkeypatch):
     from dropkv_amd import hf_query
     seen = []
 
-    def keep_indices(self, q, k, v, total_tokens=None, max_keep_len=None):
+    def evict_layer(self, q, k, v, total_tokens=None, max_keep_len=None):
         seen.append(q)
-        return torch.arange(k.shape[2] - 8, k.shape[2]).expand(k.shape[0], k.shape[1], 8)
-    monkeypatch.setattr(DropKVCache, "_compute_keep_indices", keep_indices)
-    monkeypatch.setattr(DropKVCache, "_gather_compressed", staticmethod(R.gather_compressed))
+        idx = torch.arange(k.shape[2] - 8, k.shape[2]).expand(k.shape[0], k.shape[1], 8)
+        return R.gather_compressed(k, v, idx)
+    monkeypatch.setattr(DropKVCache, "_evict_layer", evict_layer)
     q = torch.randn(1, 4, 32, 64)
     k = torch.randn(1, 2, 32, 64)
     c = DropKVCache(keep_ratio=0.1)

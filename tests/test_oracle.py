@@ -395,3 +395,35 @@ def test_oracle_vs_golden(name):
     assert_rel(R.fallback_scores(q, k, v, W), c["deployed"], 1e-4)
     assert torch.equal(R.topk_sorted(c["pooled_deployed"], keep), c["keep_idx_deployed"])
     assert R.keep_length(float(c["ratio"]), Lk, W) == keep
+
+
+def test_binding_bars_bind():
+    """The full-size score bars (conftest.assert_binding_scores) catch a
+    2e-2 error on one key above 0.1x the keep threshold and a 1e-3 error on
+    more than 1e-3 of those keys, and ignore any error on keys far below."""
+    from conftest import assert_binding_scores, binding_keys
+    Q, K, V = make_qkv(dict(B=1, Hq=4, Hkv=2, D=32), 600, seed=31)
+    W, ks, keep = 8, 5, 60
+    Qt = Q[:, :, -W:].contiguous()
+    ref = R.dropkv_scores_reference(Qt, K, V, W, match_pytorch_precision=False)
+    pooled = R.pool_protect(ref.clone(), ks, W)
+    sel = binding_keys(ref, pooled, keep)
+    assert 0 < int(sel.sum()) < sel.numel()
+    n, worst, above, _ = assert_binding_scores(ref.clone(), ref, pooled, keep, Qt, K, V, W, None, 1e-4, 1e-4, 1.0,
+                                               excuse_sinks=False)
+    assert n == int(sel.sum()) and worst == 0.0 and above == 0
+    far = (~sel).nonzero()[0].tolist()
+    bad = ref.clone()
+    bad[tuple(far)] *= 10.0                      # a key far below the threshold: not bound
+    assert_binding_scores(bad, ref, pooled, keep, Qt, K, V, W, None, 1e-4, 1e-4, 1.0, excuse_sinks=False)
+    hit = sel.nonzero()[0].tolist()
+    bad = ref.clone()
+    bad[tuple(hit)] *= 1.0 + 3e-2                # one binding key off by 3%
+    with pytest.raises(AssertionError):
+        assert_binding_scores(bad, ref, pooled, keep, Qt, K, V, W, None, 2e-2, 1e-3, 1e-3, excuse_sinks=False)
+    bad = ref.clone()
+    idx = sel.nonzero()[:2]
+    for i in idx.tolist():
+        bad[tuple(i)] *= 1.0 + 5e-3              # two binding keys off by 0.5%: above the 1e-3 share of ~100
+    with pytest.raises(AssertionError):
+        assert_binding_scores(bad, ref, pooled, keep, Qt, K, V, W, None, 2e-2, 1e-3, 1e-3, excuse_sinks=False)
