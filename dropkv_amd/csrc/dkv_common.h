@@ -75,6 +75,28 @@ __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t voff) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
 }
 
+__device__ __forceinline__ uint16_t buf_load2(rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0));
+}
+
+__device__ __forceinline__ uint32_t buf_load4(rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+}
+
+// 8-byte loads come back as a float or an int vector, each converted from
+// the load's result as a whole: this compiler turned a 64- or 128-bit buffer
+// load whose uint32 elements were then bit-cast to float one by one into a
+// 32-bit load (the other elements read undefined registers).  Elements of a
+// uint32 vector used as integers are unaffected.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f32x2 buf_load8f(rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0));
+}
+__device__ __forceinline__ i32x2 buf_load8i(rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0));
+}
+
 template <typename V>
 __device__ __forceinline__ V bitcast_u4(u32x4 x) {
   return __builtin_bit_cast(V, x);

@@ -727,6 +727,7 @@ constexpr int kMaxSplits = 1024;
 // Candidates whose final p is at least this get their rounding error
 // (round(p) - p) v added to y; below it, that error is under 2^-20 |v|.
 constexpr float kCorrMinP = 1.0f / 4096.0f;
+constexpr float kCorrMinLog2P = -12.0f;  // log2(kCorrMinP)
 constexpr int kCorrKeys = 8;  // candidates corrected per row (the largest p)
 
 template <typename T, int D>
@@ -750,7 +751,8 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   const int mpad = n_mc * kRows;
   // (head, padded row); a head's rows on the XCD whose pass-1 workgroups
   // wrote its partials (pass 1 maps heads to XCDs the same way).
-  const int rid = xcd_remap(blockIdx.x, gridDim.x) * kMergeRows + (threadIdx.x >> 6);
+  const int rid =
+      __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x) * kMergeRows + (threadIdx.x >> 6));
   if (rid >= n_rows) return;
   const int head = rid / mpad;
   const int gr = rid % mpad;
@@ -759,40 +761,54 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   const int d0 = lane * DPL;
 
   // Every load up front: the partial y columns of the first kPre splits, the
-  // query row and the per-split statistics.
+  // query row, the per-split statistics and the candidates.  They go through
+  // buffer views of this row-chunk's partials, where loads past the last
+  // split return zeros without a memory request: every load is
+  // unconditional, so all are in flight before the first wait.
   typedef float fv __attribute__((ext_vector_type(DPL)));
-  const float* py = part_y + (slot0 * kRows + row) * D + d0;
+  static_assert(DPL == 1 || DPL == 2, "columns per lane");
+  const uint32_t nsr = (uint32_t)n_splits * kRows;  // (split, row) slots of the row-chunk
+  const rsrc_t ry = make_rsrc(part_y + slot0 * kRows * D, nsr * D * 4);
+  const rsrc_t rml = make_rsrc(part_ml + slot0 * kRows * 2, nsr * 8);
+  const rsrc_t rcd = make_rsrc(part_cand + slot0 * kRows * kCand, nsr * kCand * 8);
+  // First the statistics and the candidates (needed first: a wait for a
+  // load also waits for every load issued before it), then the y columns.
+  const f32x2 ml_raw = buf_load8f(rml, ((uint32_t)lane * kRows + row) * 8);
+  auto cand_at = [&](int c) __attribute__((always_inline)) {
+    const uint32_t idx = (((uint32_t)(c / kCand)) * kRows + row) * kCand + c % kCand;
+    return buf_load8i(rcd, idx * 8);
+  };
+  constexpr int kCandPre = 4;  // candidates per lane loaded up front
+  i32x2 kcp[kCandPre];
+#pragma unroll
+  for (int j = 0; j < kCandPre; ++j) kcp[j] = cand_at(lane + 64 * j);
+  auto load_y = [&](int s) __attribute__((always_inline)) {
+    const uint32_t off = (((uint32_t)s * kRows + row) * D + d0) * 4;
+    if constexpr (DPL == 1)
+      return __builtin_bit_cast(fv, buf_load4(ry, off));
+    else
+      return __builtin_bit_cast(fv, buf_load8f(ry, off));
+  };
   fv yv[kPre];
 #pragma unroll
-  for (int s = 0; s < kPre; ++s)
-    yv[s] = s < n_splits ? *reinterpret_cast<const fv*>(py + (int64_t)s * kRows * D) : fv{};
+  for (int s = 0; s < kPre; ++s) yv[s] = load_y(s);
   T qv[DPL];
   {
     const bool valid = gr < M;
     const int b = head / Hkv, hkv = head % Hkv, gi = valid ? gr / W : 0, w = valid ? gr % W : 0;
     const T* qrow = q + (int64_t)b * q_sb + (int64_t)(hkv * g + gi) * q_sh + (int64_t)(Lq - W + w) * q_ss;
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) qv[e] = valid ? qrow[(int64_t)(d0 + e) * q_sd] : static_cast<T>(0.f);
+    for (int e = 0; e < DPL; ++e) qv[e] = qrow[(int64_t)(d0 + e) * q_sd];  // padding rows: zeroed at the store
   }
-  // The row's (key, logit) candidates, kCand per split: lane l reads
-  // candidates l, l + 64, ... and keeps its two largest (lowest key first
-  // among equal logits).  Ranking by logit ranks by p, so the kCorrKeys
-  // largest are chosen, and their value rows loaded, before the lse is
-  // known; the p threshold is applied once it is.
+  // The row's (key, logit) candidates, kCand per split, loaded with the
+  // partials: lane l reads candidates l, l + 64, ... and keeps its two
+  // largest (lowest key first among equal logits).  Once the lse is known,
+  // the wave takes the largest in turn (ranking by logit ranks by p) while
+  // their p can matter, and loads their value rows together.
   const int ncand = n_splits * kCand;
-  typedef int i32x2 __attribute__((ext_vector_type(2)));
-  const i32x2* pc2 = reinterpret_cast<const i32x2*>(part_cand);
-  auto cand_at = [&](int c) {
-    return pc2[((slot0 + c / kCand) * kRows + row) * kCand + c % kCand];
-  };
-  constexpr int kCandPre = 4;  // candidates per lane loaded up front
-  i32x2 kcp[kCandPre];
-#pragma unroll
-  for (int j = 0; j < kCandPre; ++j) kcp[j] = lane + 64 * j < ncand ? cand_at(lane + 64 * j) : i32x2{-1, 0};
   // Split statistics: lane s holds (m, l) of split s (the first 64 in
   // registers, any further ones re-read in the rare loops below).
-  const float2 ml = lane < n_splits ? *reinterpret_cast<const float2*>(part_ml + ((slot0 + lane) * kRows + row) * 2)
-                                    : make_float2(-INFINITY, 0.f);
+  const float2 ml = lane < n_splits ? make_float2(ml_raw[0], ml_raw[1]) : make_float2(-INFINITY, 0.f);
   float mx = ml.x;
   for (int s = 64 + lane; s < n_splits; s += 64) mx = fmaxf(mx, part_ml[((slot0 + s) * kRows + row) * 2]);
   mx = wave_max_dpp(mx);
@@ -838,11 +854,20 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
       kb = nkb;
     };
 #pragma unroll
-    for (int j = 0; j < kCandPre; ++j) offer(kcp[j]);
+    for (int j = 0; j < kCandPre; ++j) offer(lane + 64 * j < ncand ? kcp[j] : i32x2{-1, 0});
     for (int c = lane + 64 * kCandPre; c < ncand; c += 64) offer(cand_at(c));
+    // Only candidates that can matter take part: p >= kCorrMinP with p
+    // rounding, otherwise only a key with p >= 1/2 (its direct distance).
+    const float s_min = !valid ? INFINITY : p_round ? lse2 + kCorrMinLog2P : lse2 - 1.0f;
+    bool more = true;
 #pragma unroll
     for (int u = 0; u < kCorrKeys; ++u) {
+      ck[u] = -1;
+      cs[u] = -INFINITY;
+      if (!more) continue;
       const float best = wave_max_dpp(ka >= 0 ? sa : -INFINITY);
+      more = best >= s_min && (p_round || u == 0);
+      if (!more) continue;
       const uint64_t tie = __ballot(ka >= 0 && sa == best);
       int kmin = INT_MAX;
       if (tie) {
@@ -858,13 +883,19 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
         kb = -1;
       }
     }
+    // Their value rows, all loads unconditional (a row of no candidate reads
+    // past the view: zeros, no memory request).
+    const rsrc_t rv = make_rsrc(vp + (int64_t)head * kv_ld * D, (uint32_t)Lk * D * sizeof(T));
 #pragma unroll
     for (int u = 0; u < kCorrKeys; ++u) {
-      vb[u] = fv{};
-      if (ck[u] >= 0 && (p_round || u == 0)) {
-        const T* vrow = vp + ((int64_t)head * kv_ld + ck[u]) * D + d0;
-#pragma unroll
-        for (int e2 = 0; e2 < DPL; ++e2) vb[u][e2] = static_cast<float>(vrow[e2]);
+      const uint32_t off = ck[u] >= 0 ? ((uint32_t)ck[u] * D + d0) * sizeof(T) : (uint32_t)Lk * D * sizeof(T);
+      if constexpr (DPL == 1) {
+        vb[u][0] = static_cast<float>(__builtin_bit_cast(T, buf_load2(rv, off)));
+      } else {
+        typedef T t2v __attribute__((ext_vector_type(2)));
+        const t2v x = __builtin_bit_cast(t2v, buf_load4(rv, off));
+        vb[u][0] = static_cast<float>(x[0]);
+        vb[u][1] = static_cast<float>(x[1]);
       }
     }
   }
@@ -894,8 +925,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   for (int s0 = kPre; s0 < n_splits; s0 += 8) {
     fv yb[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      yb[u] = s0 + u < n_splits ? *reinterpret_cast<const fv*>(py + (int64_t)(s0 + u) * kRows * D) : fv{};
+    for (int u = 0; u < 8; ++u) yb[u] = load_y(s0 + u);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int s = s0 + u;
@@ -926,7 +956,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
     // element e8), so that pass 2 stages them with one contiguous copy.
     const int kk = d / 32, lg = (d % 32) / 8, e8 = d % 8;
     const int word = li + 16 * lg;
-    ob[((size_t)((0 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = qv[e];
+    ob[((size_t)((0 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = gr < M ? qv[e] : static_cast<T>(0.f);
     ob[((size_t)((1 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = hi;
     ob[((size_t)((2 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = lo;
   }
