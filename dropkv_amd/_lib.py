@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libdropkv_amd.so")
 
 DROPKV_BF16 = 1
 DROPKV_FP16 = 2
+DROPKV_FP32 = 3
 
 _c_i64 = ctypes.c_int64
 _c_vp = ctypes.c_void_p
@@ -105,8 +106,9 @@ _head_dims = None
 
 
 def supported_head_dims() -> tuple[int, ...]:
-    """Head dimensions the matrix-core scoring kernels are compiled for
-    (asked once; the library does not change while loaded)."""
+    """Head dimensions of the matrix-core scoring kernels (asked once; the
+    library does not change while loaded).  Other head dimensions up to 512
+    and fp32 inputs are scored by the library's generic kernels."""
     global _head_dims
     if _head_dims is None:
         buf = (_c_i64 * 16)()

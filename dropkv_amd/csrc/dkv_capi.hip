@@ -33,21 +33,20 @@ int hip_status(hipError_t e, const char* what) {
   return fail(DROPKV_E_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-constexpr int64_t kHeadDims[] = {64, 128};
 constexpr int64_t kMaxLk = (int64_t)1 << 30;
 
-bool head_dim_supported(int64_t D) {
-  for (int64_t d : kHeadDims)
-    if (d == D) return true;
-  return false;
-}
+// Head dimensions of the decode kernels.
+bool decode_head_dim_supported(int64_t D) { return D == 64 || D == 128; }
+
+int64_t elem_size(int dtype) { return dtype == DROPKV_FP32 ? 4 : 2; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int check_score_args(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
                      int64_t Lq, int64_t Lk, int64_t D, int64_t W) {
   if (!q || !k || !v) return fail(DROPKV_E_ARG, "null q/k/v pointer");
-  if (dtype != DROPKV_BF16 && dtype != DROPKV_FP16) return fail(DROPKV_E_ARG, "dtype must be bf16 or fp16");
+  if (dtype != DROPKV_BF16 && dtype != DROPKV_FP16 && dtype != DROPKV_FP32)
+    return fail(DROPKV_E_ARG, "dtype must be bf16, fp16 or fp32");
   if (B < 1 || Hq < 1 || Hkv < 1) return fail(DROPKV_E_ARG, "B, Hq, Hkv must be positive");
   if (Hq % Hkv != 0) return fail(DROPKV_E_ARG, "Hq (%lld) must be divisible by Hkv (%lld)", (long long)Hq,
                                  (long long)Hkv);
@@ -56,9 +55,10 @@ int check_score_args(const void* q, const void* k, const void* v, int dtype, int
   if (Lk < W) return fail(DROPKV_E_ARG, "Lk (%lld) must be >= window_size (%lld)", (long long)Lk, (long long)W);
   if (Lq > Lk) return fail(DROPKV_E_ARG, "Lq (%lld) must be <= Lk (%lld)", (long long)Lq, (long long)Lk);
   if (Lk > kMaxLk) return fail(DROPKV_E_UNSUPPORTED, "Lk (%lld) too large", (long long)Lk);
-  if (!head_dim_supported(D)) return fail(DROPKV_E_UNSUPPORTED, "head dim %lld not supported", (long long)D);
+  if (D < 1) return fail(DROPKV_E_ARG, "head dim must be positive");
+  if (dkv::scores_generic(dtype, D, (Hq / Hkv) * W) && D > dkv::generic_max_head_dim())
+    return fail(DROPKV_E_UNSUPPORTED, "head dim %lld above %lld", (long long)D, (long long)dkv::generic_max_head_dim());
   if (!aligned16(k) || !aligned16(v)) return fail(DROPKV_E_ARG, "k and v must be 16-byte aligned");
-  if ((int64_t)(Hq / Hkv) * W > 4096) return fail(DROPKV_E_UNSUPPORTED, "g*window above 4096");
   return DROPKV_OK;
 }
 
@@ -96,8 +96,8 @@ int dropkv_version(void) { return 100; }
 const char* dropkv_last_error(void) { return g_err.c_str(); }
 
 int dropkv_supported_head_dims(int64_t* out, int cap) {
-  const int n = (int)(sizeof(kHeadDims) / sizeof(kHeadDims[0]));
-  for (int i = 0; i < n && i < cap; ++i) out[i] = kHeadDims[i];
+  const int n = (int)(sizeof(dkv::kMfmaHeadDims) / sizeof(dkv::kMfmaHeadDims[0]));
+  for (int i = 0; i < n && i < cap; ++i) out[i] = dkv::kMfmaHeadDims[i];
   return n;
 }
 
@@ -119,7 +119,7 @@ int dropkv_scores(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64
   if (!workspace || workspace_bytes < p.total)
     return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", p.total, workspace_bytes);
   timing_start(static_cast<hipStream_t>(stream));
-  return hip_status(dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Lk,
+  return hip_status(dkv::launch_scores(p, dtype, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Lk,
                                        (int)Hkv, (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, scores,
                                        static_cast<char*>(workspace), nullptr, 0, nullptr,
                                        static_cast<hipStream_t>(stream)),
@@ -130,7 +130,7 @@ int dropkv_scores_debug_state(const void* workspace, int64_t B, int64_t Hq, int6
                               int64_t W, int64_t splits, float* lse_out, float* y_out, void* stream) {
   (void)hipGetLastError();  // a failure left by an unrelated earlier call is not ours
   if (!workspace || !lse_out || !y_out) return fail(DROPKV_E_ARG, "null pointer");
-  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || W < 1 || Lk < W || !head_dim_supported(D))
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || W < 1 || Lk < W || D < 1 || D > dkv::generic_max_head_dim())
     return fail(DROPKV_E_ARG, "invalid shape");
   const dkv::ScorePlan p = dkv::make_score_plan(B, Hq, Hkv, Lk, D, W, splits);
   return hip_status(dkv::launch_debug_state(p, static_cast<const char*>(workspace), (int)D, lse_out, y_out,
@@ -244,16 +244,18 @@ static int evict_impl(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, i
   char* sel_ws = ws + p.total + s_bytes;
   // The gather runs inside the selection's emit stage when the rows allow
   // 16-byte copies; otherwise as its own kernel (contiguous outputs only).
-  const bool vec = (D * 2) % 16 == 0 && aligned16(k_out) && aligned16(v_out);
+  const int64_t eb = elem_size(dtype);
+  const bool vec = (D * eb) % 16 == 0 && aligned16(k_out) && aligned16(v_out);
   if (!vec && out_ld != keep)
     return fail(DROPKV_E_UNSUPPORTED, "outputs with a row capacity need 16-byte aligned rows");
   timing_start(st);
-  const dkv::SelectCompact cp{k, v, Hkv * kv_ld * D, kv_ld * D, D, 2, D, (int)Hkv, k_out, v_out, out_ld};
-  // Pooling runs in the tail of the scoring pass when the plan allows it;
-  // otherwise as the standalone selection's pool kernel.
-  const bool fused = dkv::select_after_pool_ok(p.s2, p.kps2, Lk, kernel_size);
+  const dkv::SelectCompact cp{k, v, Hkv * kv_ld * D, kv_ld * D, D, eb, D, (int)Hkv, k_out, v_out, out_ld};
+  // Pooling runs in the tail of the scoring pass when the plan allows it
+  // (the matrix-core kernels only); otherwise as the standalone selection's
+  // pool kernel.
+  const bool fused = !dkv::scores_generic(dtype, D, p.M) && dkv::select_after_pool_ok(p.s2, p.kps2, Lk, kernel_size);
   const dkv::FuseSelect fs{sel_ws, (int)kernel_size, (int)protect_window};
-  hipError_t e = dkv::launch_scores(p, dtype == DROPKV_BF16, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)kv_ld,
+  hipError_t e = dkv::launch_scores(p, dtype, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)kv_ld,
                                     (int)Hkv, (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc,
                                     ws, reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv),
                                     fused ? &fs : nullptr, st);
@@ -266,7 +268,7 @@ static int evict_impl(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, i
                            nullptr, sel_ws, true, vec ? &cp : nullptr, st);
   if (e != hipSuccess) return hip_status(e, "dropkv_evict select");
   if (vec) return DROPKV_OK;
-  e = dkv::launch_compact(k, v, Hkv * kv_ld * D, kv_ld * D, D, Lk, nullptr, nullptr, 0, 0, 0, 0, 2, B, Hkv, D,
+  e = dkv::launch_compact(k, v, Hkv * kv_ld * D, kv_ld * D, D, Lk, nullptr, nullptr, 0, 0, 0, 0, eb, B, Hkv, D,
                           keep_idx, keep, k_out, v_out, st);
   return hip_status(e, "dropkv_evict compact");
 }
@@ -406,7 +408,7 @@ int dropkv_timing_read(double* stage_ms, int cap) {
 }
 
 size_t dropkv_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t capacity) {
-  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || capacity < 1 || !head_dim_supported(D)) return 0;
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || capacity < 1 || !decode_head_dim_supported(D)) return 0;
   return dkv::decode_workspace_bytes((int)B, (int)Hq, (int)Hkv, (int)D, (int)capacity);
 }
 
@@ -421,7 +423,7 @@ int dropkv_decode_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q
   if (dtype != DROPKV_BF16 && dtype != DROPKV_FP16) return fail(DROPKV_E_ARG, "dtype must be bf16 or fp16");
   if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv) return fail(DROPKV_E_ARG, "B, Hq, Hkv must be positive, Hkv | Hq");
   if (Hq / Hkv > 16) return fail(DROPKV_E_UNSUPPORTED, "more than 16 query heads per KV head");
-  if (!head_dim_supported(D)) return fail(DROPKV_E_UNSUPPORTED, "head dim %lld not supported", (long long)D);
+  if (!decode_head_dim_supported(D)) return fail(DROPKV_E_UNSUPPORTED, "head dim %lld not supported", (long long)D);
   if (capacity < 1 || capacity * D * 2 > ((int64_t)1 << 31)) return fail(DROPKV_E_ARG, "capacity out of range");
   if (!aligned16(k_cache) || !aligned16(v_cache)) return fail(DROPKV_E_ARG, "cache buffers must be 16-byte aligned");
   if (workspace_bytes < dkv::decode_workspace_bytes((int)B, (int)Hq, (int)Hkv, (int)D, (int)capacity))

@@ -26,6 +26,24 @@ inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shm
     hipLaunchKernelGGL(kernel, grid, block, shmem, st, args...);
 }
 
+// Element types (the DROPKV_BF16 / _FP16 / _FP32 codes of the C ABI).
+constexpr int kDtypeBf16 = 1, kDtypeFp16 = 2, kDtypeFp32 = 3;
+
+// Head dimensions of the matrix-core scoring kernels; every other one (and
+// fp32 inputs) takes the generic kernels (dkv_generic.hip).
+constexpr int64_t kMfmaHeadDims[] = {32, 64, 128};
+inline bool mfma_head_dim(int64_t D) {
+  for (int64_t d : kMfmaHeadDims)
+    if (d == D) return true;
+  return false;
+}
+// Query rows per KV head (g * W) the matrix-core kernels take; more go to the
+// generic kernels too.
+constexpr int64_t kMfmaMaxRows = 4096;
+inline bool scores_generic(int dtype, int64_t D, int64_t M) {
+  return dtype == kDtypeFp32 || !mfma_head_dim(D) || M > kMfmaMaxRows;
+}
+
 // Launch geometry and workspace layout of one scoring call.
 struct ScorePlan {
   int heads, g, M, n_mc, mpad;
@@ -46,12 +64,19 @@ struct FuseSelect {
   int ks, window;
 };
 // K/V: [B*Hkv, kv_ld, D] with rows 0 .. Lk-1 of each head used (kv_ld = Lk: contiguous).
-hipError_t launch_scores(const ScorePlan& p, int dtype_bf16, int D, const void* q, int64_t q_sb, int64_t q_sh,
+hipError_t launch_scores(const ScorePlan& p, int dtype, int D, const void* q, int64_t q_sb, int64_t q_sh,
                          int64_t q_ss, int64_t q_sd, const void* k, const void* v, int kv_ld, int Hkv, int Lq,
                          int Lk, int W, float eps, int p_round, int y_round, float* scores, char* ws,
                          uint32_t* zero_ptr, int64_t zero_words, const FuseSelect* fuse, hipStream_t st);
 hipError_t launch_debug_state(const ScorePlan& p, const char* ws, int D, float* lse_out, float* y_out,
                               hipStream_t st);
+// The generic scoring kernels (fp32 arithmetic on the vector ALUs) on the
+// same plan's workspace; no fused pooling.
+hipError_t launch_scores_generic(const ScorePlan& p, int dtype, int D, const void* q, int64_t q_sb, int64_t q_sh,
+                                 int64_t q_ss, int64_t q_sd, const void* k, const void* v, int kv_ld, int Hkv, int Lq,
+                                 int Lk, int W, float eps, int p_round, int y_round, float* scores, char* ws,
+                                 uint32_t* zero_ptr, int64_t zero_words, hipStream_t st);
+int64_t generic_max_head_dim();
 hipError_t launch_mfma_selftest(float* out, hipStream_t st);
 
 // Decode step on the compressed cache (dkv_decode.hip).

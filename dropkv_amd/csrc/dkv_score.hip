@@ -738,10 +738,10 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
              int Hkv, int g, int W, int Lq, u32x4* __restrict__ opblk, float* __restrict__ stblk,
              float* __restrict__ ystat, float* __restrict__ yf32, uint32_t* __restrict__ zero_ptr,
              int64_t zero_words) {
-  constexpr int DPL = D / 64;  // columns per lane
+  constexpr int DPL = D >= 64 ? D / 64 : 1;  // columns per lane (D = 32: lanes 32..63 hold none)
   constexpr int KK = D / 32;
   constexpr int OPS = kOpSlots * kMB * KK;
-  constexpr int kPre = 4096 / D;  // splits whose partial y is loaded up front (64 registers)
+  constexpr int kPre = 64 / DPL;  // splits whose partial y is loaded up front (64 registers)
   const int lane = threadIdx.x & 63;
   if (zero_ptr)
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_words;
@@ -759,6 +759,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
   const int mc = gr / kRows, row = gr % kRows;
   const int64_t slot0 = ((int64_t)head * n_mc + mc) * n_splits;
   const int d0 = lane * DPL;
+  const bool col = d0 < D;  // this lane holds head-dim columns
 
   // Every load up front: the partial y columns of the first kPre splits, the
   // query row, the per-split statistics and the candidates.  They go through
@@ -783,7 +784,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
 #pragma unroll
   for (int j = 0; j < kCandPre; ++j) kcp[j] = cand_at(lane + 64 * j);
   auto load_y = [&](int s) __attribute__((always_inline)) {
-    const uint32_t off = (((uint32_t)s * kRows + row) * D + d0) * 4;
+    const uint32_t off = col ? (((uint32_t)s * kRows + row) * D + d0) * 4 : nsr * D * 4;
     if constexpr (DPL == 1)
       return __builtin_bit_cast(fv, buf_load4(ry, off));
     else
@@ -798,7 +799,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
     const int b = head / Hkv, hkv = head % Hkv, gi = valid ? gr / W : 0, w = valid ? gr % W : 0;
     const T* qrow = q + (int64_t)b * q_sb + (int64_t)(hkv * g + gi) * q_sh + (int64_t)(Lq - W + w) * q_ss;
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) qv[e] = qrow[(int64_t)(d0 + e) * q_sd];  // padding rows: zeroed at the store
+    for (int e = 0; e < DPL; ++e) qv[e] = qrow[(int64_t)(col ? d0 + e : 0) * q_sd];  // padding rows: zeroed at the store
   }
   // The row's (key, logit) candidates, kCand per split, loaded with the
   // partials: lane l reads candidates l, l + 64, ... and keeps its two
@@ -888,7 +889,8 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
     const rsrc_t rv = make_rsrc(vp + (int64_t)head * kv_ld * D, (uint32_t)Lk * D * sizeof(T));
 #pragma unroll
     for (int u = 0; u < kCorrKeys; ++u) {
-      const uint32_t off = ck[u] >= 0 ? ((uint32_t)ck[u] * D + d0) * sizeof(T) : (uint32_t)Lk * D * sizeof(T);
+      const uint32_t off =
+          ck[u] >= 0 && col ? ((uint32_t)ck[u] * D + d0) * sizeof(T) : (uint32_t)Lk * D * sizeof(T);
       if constexpr (DPL == 1) {
         vb[u][0] = static_cast<float>(__builtin_bit_cast(T, buf_load2(rv, off)));
       } else {
@@ -943,6 +945,7 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
 #pragma unroll
   for (int e = 0; e < DPL; ++e) {
     const int d = d0 + e;
+    if (!col) break;
     float y = valid ? acc[e] / l + corr[e] : 0.f;
     const T hi = static_cast<T>(y);
     if (y_round) y = static_cast<float>(hi);
@@ -1400,18 +1403,24 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   return hipGetLastError();
 }
 
-hipError_t launch_scores(const ScorePlan& p, int dtype_bf16, int D, const void* q, int64_t q_sb, int64_t q_sh,
+hipError_t launch_scores(const ScorePlan& p, int dtype, int D, const void* q, int64_t q_sb, int64_t q_sh,
                          int64_t q_ss, int64_t q_sd, const void* k, const void* v, int kv_ld, int Hkv, int Lq,
                          int Lk, int W, float eps, int p_round, int y_round, float* scores, char* ws,
                          uint32_t* zero_ptr, int64_t zero_words, const FuseSelect* fuse, hipStream_t st) {
+  if (scores_generic(dtype, D, p.M)) {
+    if (fuse) return hipErrorInvalidValue;  // the generic kernels have no pooling tail
+    return launch_scores_generic(p, dtype, D, q, q_sb, q_sh, q_ss, q_sd, k, v, kv_ld, Hkv, Lq, Lk, W, eps, p_round,
+                                 y_round, scores, ws, zero_ptr, zero_words, st);
+  }
 #define DKV_CASE(TT, DD)                                                                                   \
   return launch_scores_t<TT, DD>(p, q, q_sb, q_sh, q_ss, q_sd, k, v, kv_ld, Hkv, Lq, Lk, W, eps, p_round, \
-                                 y_round, \
-                                 scores, ws, zero_ptr, zero_words, fuse, st)
-  if (dtype_bf16) {
+                                 y_round, scores, ws, zero_ptr, zero_words, fuse, st)
+  if (dtype == kDtypeBf16) {
+    if (D == 32) DKV_CASE(__bf16, 32);
     if (D == 64) DKV_CASE(__bf16, 64);
     if (D == 128) DKV_CASE(__bf16, 128);
-  } else {
+  } else if (dtype == kDtypeFp16) {
+    if (D == 32) DKV_CASE(_Float16, 32);
     if (D == 64) DKV_CASE(_Float16, 64);
     if (D == 128) DKV_CASE(_Float16, 128);
   }

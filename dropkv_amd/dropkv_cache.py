@@ -14,8 +14,9 @@ libdropkv_amd.so:
 * selection (dropkv_cache.py:464-475) and gather (:479-491) always run on the
   HIP select / compact kernels.
 
-There is no CPU fallback: inputs the kernels cannot take (CPU tensors, fp32,
-an uncompiled head dimension) raise ``RuntimeError``.
+fp32 inputs and head dimensions outside the matrix-core set run on the
+library's generic HIP kernels with the same semantics.  There is no CPU
+fallback: CPU tensors raise ``RuntimeError``.
 """
 
 from __future__ import annotations

@@ -16,7 +16,6 @@ import math
 import torch
 
 from . import ops
-from ._lib import supported_head_dims
 
 
 def _next_power_of_2(n: int) -> int:
@@ -72,7 +71,6 @@ def check_scoring_inputs(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, wind
     )
     assert D >= 32, f"D ({D}) must be >= BLOCK_K (32)"
     assert D & (D - 1) == 0, f"D ({D}) must be a power of 2"
-    assert D in supported_head_dims(), f"D ({D}) is not compiled into the MI355X kernels"
 
 
 def dropkv_scores_triton(
@@ -92,6 +90,9 @@ def dropkv_scores_triton(
 
     ``match_pytorch_precision=True`` rounds the softmax probabilities to the
     input dtype before ``w = (p/(1-p+eps))^2`` (dropkv_triton.py:584-587).
+    Head dimensions 32, 64 and 128 run on the matrix-core kernels, other
+    powers of two (up to 512) on the library's generic fp32 kernels.
+
     ``allow_tf32`` is accepted for compatibility and has no effect: gfx950 has
     no TF32 matrix path; P.V and Y.V^T run as bf16/fp16 MFMAs with the fp32
     operand split into two bf16/fp16 terms, which is at least as accurate.

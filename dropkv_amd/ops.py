@@ -15,7 +15,7 @@ import torch
 
 from . import _lib
 
-_DTYPE_CODE = {torch.bfloat16: _lib.DROPKV_BF16, torch.float16: _lib.DROPKV_FP16}
+_DTYPE_CODE = {torch.bfloat16: _lib.DROPKV_BF16, torch.float16: _lib.DROPKV_FP16, torch.float32: _lib.DROPKV_FP32}
 
 
 def _stream(dev: torch.device) -> int:

@@ -25,6 +25,7 @@ extern "C" {
 /* element type codes */
 #define DROPKV_BF16 1
 #define DROPKV_FP16 2
+#define DROPKV_FP32 3  /* scoring and eviction only (not decode) */
 
 /* status codes */
 #define DROPKV_OK 0
@@ -39,8 +40,11 @@ int dropkv_version(void);
 /* Message describing the last failure on this thread ("" if none). */
 const char* dropkv_last_error(void);
 
-/* Head dimensions the scoring kernels are compiled for; writes up to `cap`
- * values into `out` and returns how many exist. */
+/* Head dimensions of the matrix-core scoring kernels (bf16 / fp16 inputs);
+ * writes up to `cap` values into `out` and returns how many exist.  Every
+ * other head dimension up to 512, fp32 inputs, and GQA groups of more than
+ * 4096 query rows (g * W) are scored by generic fp32 kernels on the vector
+ * ALUs with the same arguments and results. */
 int dropkv_supported_head_dims(int64_t* out, int cap);
 
 /* ------------------------------------------------------------------------
@@ -54,6 +58,7 @@ int dropkv_supported_head_dims(int64_t* out, int cap);
  *   q      [B,Hq,Lq,D], arbitrary element strides q_s* (only the last W rows
  *          along Lq are read; query row w sits at key position Lk-W+w)
  *   k, v   [B,Hkv,Lk,D] contiguous, 16-byte aligned, same dtype as q
+ *          (bf16, fp16 or fp32)
  *   scores [B,Hkv,Lk] fp32 contiguous (output)
  *   p_round 0: keep softmax probabilities in fp32; 1: round them to the input
  *          dtype before w = (p/(1-p+eps))^2 (match_pytorch_precision=True,
@@ -62,7 +67,7 @@ int dropkv_supported_head_dims(int64_t* out, int cap);
  *          (deployed path, dropkv_cache.py:434)
  *   splits 0 = automatic split-K depth over keys, otherwise that many splits
  *          per (b, hkv, row-chunk)
- * Requires Hq % Hkv == 0, 1 <= W <= Lq <= Lk, D in the supported set.
+ * Requires Hq % Hkv == 0, 1 <= W <= Lq <= Lk, 1 <= D <= 512.
  * ------------------------------------------------------------------------ */
 size_t dropkv_scores_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk,
                                      int64_t D, int64_t W, int64_t splits);

@@ -46,7 +46,7 @@ def test_binding_table_matches_header():
 
 def test_version_and_head_dims(lib):
     assert lib.dropkv_version() >= 100
-    assert _lib.supported_head_dims() == (64, 128)
+    assert _lib.supported_head_dims() == (32, 64, 128)
 
 
 def test_workspace_queries(lib):
@@ -62,12 +62,13 @@ def test_workspace_queries(lib):
 @pytest.mark.parametrize("args,code,msg", [
     # (q, k, v) null
     (dict(q=None), 1, "null q/k/v"),
-    (dict(dtype=3), 1, "bf16 or fp16"),
+    (dict(dtype=4), 1, "bf16, fp16 or fp32"),
     (dict(Hq=30), 1, "divisible"),
     (dict(W=0), 1, "window must be positive"),
     (dict(Lq=4), 1, "must be >= window_size"),
     (dict(Lq=200), 1, "must be <= Lk"),
-    (dict(D=96), 2, "head dim"),
+    (dict(D=0), 1, "head dim must be positive"),
+    (dict(D=1024), 2, "head dim 1024 above 512"),
 ])
 def test_score_argument_checks(lib, args, code, msg):
     """Checks happen on the host before anything is enqueued."""
