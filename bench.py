@@ -45,8 +45,8 @@ HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
 # kernels of one dropkv_evict call, in launch order: with the selection fused
 # into the scoring pass's tail, and with the standalone selection kernels
-STAGES_FUSED = ("pass1_partials", "merge", "pass2_scores_pool", "select_cand", "emit_compact")
-STAGES_UNFUSED = ("pass1_partials", "merge", "pass2_scores", "select_pool", "select_cand", "emit_compact")
+STAGES_FUSED = ("pass1_partials", "merge", "pass2_scores_pool", "select_resolve", "emit_compact")
+STAGES_UNFUSED = ("pass1_partials", "merge", "pass2_scores", "select_pool", "select_resolve", "emit_compact")
 # kernels that stream all of K and V
 STREAM_STAGES = ("pass1_partials", "pass2_scores", "pass2_scores_pool")
 
@@ -166,7 +166,7 @@ def pmc_summary(fetch_dir, write_dir, calib_fetch_dir, calib_write_dir, calib_mi
     sf, sw = true_kib / copy_f, true_kib / copy_w
     rows = {}
     for name, vals in fetch.items():
-        short = next((s for s in ("pass1", "pass2", "merge", "sel_pool", "sel_cand", "sel_emit", "compact")
+        short = next((s for s in ("pass1", "pass2", "merge", "sel_pool", "sel_resolve", "sel_emit", "compact")
                       if s in name), None)
         if short is None:
             continue

@@ -120,7 +120,7 @@ struct SelectCompact {
 };
 hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int window, int keep, int64_t* out_idx,
                          float* pooled_out, char* ws, bool pre_zeroed, const SelectCompact* cp, hipStream_t st);
-// The cand and emit stages after a pooling stage that pooled every key
+// The resolve and emit stages after a pooling stage that pooled every key
 // except those within kernel_size/2 of j = i*kps (1 <= i < n_splits).
 hipError_t launch_select_after_pool(const float* scores, int rows, int Lk, int ks, int window, int keep,
                                     int n_splits, int kps, int64_t* out_idx, float* pooled_out, char* ws,

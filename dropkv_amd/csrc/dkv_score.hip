@@ -347,6 +347,10 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
         for (int kk = 0; kk < KK; ++kk) acc = Elem<T>::mfma(kop[kb][kk], qop[mb][kk], acc);
         s[kb][mb] = acc;
       }
+    // The K registers are free again: start the K loads of tile tn (zeros
+    // past the range; unconditional, so that the compiler's wait counts stay
+    // exact) before waiting for this tile's V.
+    load_rows_op<T, D>(kop, krs, k_lane, tn);
 
     // Transposed V tile -> LDS: dword (d, pair p) = {V[2p][d], V[2p+1][d]}.
     // The pair column is XOR-swizzled with bits 4-5 of d to spread banks.
@@ -365,10 +369,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
       }
     }
 
-    // The K/V registers are free again: start the loads of tile tn.  They
-    // are unconditional (zeros past the range) so that the compiler's wait
-    // counts stay exact.
-    load_rows_op<T, D>(kop, krs, k_lane, tn);
+    // The V registers are free again: start the V loads of tile tn.
     load_v_pairs<T, D>(va, vb, vrs, v_lane, tn);
 
     // Online softmax.  P enters the MFMA as hi + lo: the p of a tile is
@@ -1016,7 +1017,7 @@ __device__ __forceinline__ float sumsq8<_Float16>(Elem<_Float16>::v8 x, float ac
 // workgroup owns the key range [k_begin, k_end) of one row and, once its
 // scores are stored, pools the keys whose whole window lies in that range
 // (its interior) into the pooled row, the row maximum and the top-digit
-// histogram (pool_range).  The selection's cand stage pools the keys next to
+// histogram (pool_range).  The selection's resolve stage pools the keys next to
 // the split boundaries.  The kernel boundary is the only synchronisation: an
 // in-kernel handoff between workgroups would need agent-scope
 // release/acquire, which on gfx950 writes back and invalidates an XCD's whole
@@ -1148,26 +1149,32 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
             for (int r = 0; r < 4; ++r) gacc[kb][mb][r] = fmaf(vn2[kb][r], -0.5f, nyh);
           }
         }
+        // S^T first: after the last row-chunk's S MFMAs the K registers are
+        // free, and the K loads of tile tn (relative; zeros past the range)
+        // start while G^T is computed; then the same for V.
+        const bool refill = c1 == NC - 1 && cp == npairs - 1;
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
           for (int kk = 0; kk < KK; ++kk) {
             const v8 qo = __builtin_bit_cast(v8, ob[(size_t)((0 * kMB + mb) * KK + kk) * 64]);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) sacc[kb][mb] = Elem<T>::mfma(kop[kb][kk], qo, sacc[kb][mb]);
+          }
+        if (refill) load_rows_op<T, D>(kop, krs, k_lane, tn);
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) {
             const v8 yh = __builtin_bit_cast(v8, ob[(size_t)((1 * kMB + mb) * KK + kk) * 64]);
             const v8 yl = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-              sacc[kb][mb] = Elem<T>::mfma(kop[kb][kk], qo, sacc[kb][mb]);
               gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], yh, gacc[kb][mb]);
               gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], yl, gacc[kb][mb]);
             }
           }
-        // After the last row-chunk's MFMAs the K/V registers are free: start
-        // the loads of tile tn (relative; zeros past the range).
-        if (c1 == NC - 1 && cp == npairs - 1) {
-          load_rows_op<T, D>(kop, krs, k_lane, tn);
-          load_rows_op<T, D>(vop, vrs, k_lane, tn);
-        }
+        if (refill) load_rows_op<T, D>(vop, vrs, k_lane, tn);
         // sc accumulates w * (-dist2/2).  The causal bound, and the direct
         // distance at a row's dominant key (merge), are applied only in
         // tiles that reach the bound or hold such a key (and with padding

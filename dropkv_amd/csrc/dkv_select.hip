@@ -4,8 +4,8 @@
 // (DropKVCache._gather_compressed, dropkv_cache.py:479-491).  The stages are
 // described in dkv_select_dev.h.
 //
-// Standalone (dropkv_select): zero -> pool -> cand -> emit.
-// After a scoring pass that pooled its interiors (dropkv_evict): cand -> emit.
+// Standalone (dropkv_select): zero -> pool -> resolve -> emit.
+// After a scoring pass that pooled its interiors (dropkv_evict): resolve -> emit.
 #include "dkv_common.h"
 #include "dkv_internal.h"
 #include "dkv_select_dev.h"
@@ -40,37 +40,60 @@ sel_pool_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
 }
 
 // ---------------------------------------------------------------------------
-// cand: grid = rows * chunks.
+// resolve: one workgroup per row.
+//   A. Pools the keys next to the scoring pass's split boundaries (their
+//      windows straddle two workgroup ranges), which completes the row's
+//      top-digit histogram and maximum; finds the top-digit bin b1 of the
+//      keep-th largest key.
+//   B. One sweep over the pooled row: per chunk, the keys above b1; the keys
+//      inside b1 (the candidates, a few percent of the row) into LDS.
+//   C. Digits 2 and 3 over the candidates: the threshold key T and how many
+//      keys equal to T are kept (the lowest indices).
+//   D. Per chunk, the kept keys above T and the keys equal to T in the
+//      chunks before it (exclusive prefix sums), for emit.
+// Past kResCandCap candidates (near-constant rows), C and D sweep the row
+// again instead of reading the list.
 // ---------------------------------------------------------------------------
-constexpr int kBndPer = kBndLds / kSelT;  // boundary raw scores per thread (at most)
+constexpr int kResT = 1024;
+constexpr int kResWaves = kResT / 64;
+constexpr int kWaveKeys = 2 * kChunk;              // keys per wave and sweep round: 8 x 4 per lane
+constexpr int kRoundKeys = kResWaves * kWaveKeys;  // keys per sweep round
+constexpr int kResCandCap = 4096;                  // candidates held in LDS as (key, index)
+constexpr int kResUnion = kBndLds > 2 * kResCandCap ? kBndLds : 2 * kResCandCap;
+constexpr int kBndPer = kBndLds / kResT;           // boundary raw scores per thread (at most)
+constexpr int kCntPer = kMaxChunks / kResT;        // chunk counters per thread (at most)
+static_assert(kBins1 == 2 * kResT, "two top-digit histogram words per thread");
+static_assert(kWaveKeys == 2 * kChunk, "a wave's share of a round is two whole chunks");
 
-__global__ void __launch_bounds__(kSelT)
-sel_cand_kernel(const float* __restrict__ scores, int Lk, int ks, int window, int keep, int chunks, SplitGeom geom,
-                SelWs ws) {
-  __shared__ __attribute__((aligned(16))) uint32_t hist[kBins1];
-  __shared__ float bxs[kBndLds];
+// Sort key of a pooled value given as its bits (the buffer load's integer
+// lanes), with the protected tail mapped to kbig.
+__device__ __forceinline__ uint32_t pooled_key(uint32_t bits, int j, int prot, uint32_t kbig) {
+  if (bits == 0x80000000u) bits = 0u;
+  const uint32_t k = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+  return j >= prot ? kbig : k;
+}
+
+__global__ void __launch_bounds__(kResT)
+sel_resolve_kernel(const float* __restrict__ scores, int Lk, int ks, int window, int keep, int chunks,
+                   SplitGeom geom, SelWs ws) {
+  __shared__ __attribute__((aligned(16))) uint32_t hist1[kBins1];
+  __shared__ uint32_t hist2[kBins2];
+  __shared__ uint32_t hist3[kBins3];
+  __shared__ uint32_t gtc[kMaxChunks];  // per chunk: keys above b1, then kept keys above T
+  __shared__ uint32_t eqc[kMaxChunks];  // per chunk: keys equal to T
   __shared__ float bpool[kBndPoolLds];
-  __shared__ uint32_t small[128];  // scan partials [0, 32), bin / counts at 64.., max at 96..
-  const int tid = threadIdx.x;
-  const int row = blockIdx.x / chunks;
-  const int c = blockIdx.x % chunks;
+  __shared__ __attribute__((aligned(16))) uint32_t un[kResUnion];  // boundary raw scores, then candidates
+  __shared__ uint32_t small[128];  // scan partials [0, 32), bin / counts at 64.., max at 96.., count at 112
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int row = blockIdx.x;
   const int h = ks / 2;
   const int prot = Lk - window;
   uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
   const float* srow = scores + (int64_t)row * Lk;
   float* prow = ws.pooled + (int64_t)row * Lk;
-  uint32_t* wsum = small;
 
-  // One round trip: this chunk's pooled values (complete except the boundary
-  // keys), the row's top-digit histogram and interior maximum, and the raw
-  // scores [b-2h, b+2h) around each split boundary b = i*kps (1 <= i < n_splits).
-  float cv[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = c * kChunk + tid + i * kSelT;
-    cv[i] = j < Lk ? prow[j] : 0.f;
-  }
-  static_assert(kBins1 == 2 * kSelT, "two histogram words per thread");
+  // A. One round trip: the top-digit histogram and interior maximum, and the
+  // raw scores [b-2h, b+2h) around each split boundary b = i*kps.
   const uint2 hv = reinterpret_cast<const uint2*>(rw + kRowHist1)[tid];
   const uint32_t rmax = rw[kRowMax];
   const int nb = geom.n_splits - 1;
@@ -79,26 +102,29 @@ sel_cand_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
   float bv[kBndPer];
 #pragma unroll
   for (int i = 0; i < kBndPer; ++i) {
-    if (i * kSelT >= nbx) break;
-    const int t = tid + i * kSelT;
+    if (i * kResT >= nbx) break;
+    const int t = tid + i * kResT;
     bv[i] = -INFINITY;
     if (t < nbx) {
       const int u = (t / w4 + 1) * geom.kps - 2 * h + t % w4;
       if (u >= 0 && u < Lk) bv[i] = srow[u];
     }
   }
-  reinterpret_cast<uint2*>(hist)[tid] = hv;
+  for (int i = tid; i < chunks; i += kResT) eqc[i] = 0u;
+  for (int i = tid; i < kBins2; i += kResT) hist2[i] = 0u;
+  for (int i = tid; i < kBins3; i += kResT) hist3[i] = 0u;
+  if (tid == 0) small[112] = 0u;
+  reinterpret_cast<uint2*>(hist1)[tid] = hv;
+  float* bxs = reinterpret_cast<float*>(un);
 #pragma unroll
   for (int i = 0; i < kBndPer; ++i) {
-    if (i * kSelT >= nbx) break;
-    const int t = tid + i * kSelT;
+    if (i * kResT >= nbx) break;
+    const int t = tid + i * kResT;
     if (t < nbx) bxs[t] = bv[i];
   }
   __syncthreads();
-
-  // The boundary keys' windows, read from LDS; they complete the histogram.
   uint32_t bmax = 0u;
-  for (int t = tid; t < nb * w2; t += kSelT) {
+  for (int t = tid; t < nb * w2; t += kResT) {
     const int bi = t / w2, k = t % w2;
     const int j = (bi + 1) * geom.kps - h + k;
     float m = -INFINITY;
@@ -107,70 +133,158 @@ sel_cand_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
       for (int u = 0; u <= 2 * h; ++u) m = fmaxf(m, w[u]);
       const uint32_t key = float_key(m);
       bmax = max(bmax, key);
-      if (j < prot) atomicAdd(&hist[key >> kShift1], 1u);
+      if (j < prot) atomicAdd(&hist1[key >> kShift1], 1u);
+      prow[j] = m;  // read back by this workgroup's sweep (after the barriers below) and by emit
     }
     bpool[t] = m;
   }
   const uint32_t gmax = block_max_u32(max(bmax, rmax), small + 96);
   const uint32_t kbig = float_key(key_float(gmax) + 1.0f);
-  if (tid == 0) hist[kbig >> kShift1] += (uint32_t)window;
+  if (tid == 0) hist1[kbig >> kShift1] += (uint32_t)window;
   __syncthreads();
-  uint32_t* fb = small + 64;  // wave_find_bin result
-  if (tid < 64) wave_find_bin<kBins1>(hist, nullptr, (uint32_t)keep, fb);
+  uint32_t* fb = small + 64;
+  if (tid < 64) wave_find_bin<kBins1>(hist1, nullptr, (uint32_t)keep, fb);
   __syncthreads();
   const uint32_t b1 = fb[0];
   const uint32_t k1 = (uint32_t)keep - fb[1];
 
-  // This chunk: the count above b1 and the candidates (keys in b1), which go
-  // to the chunk's own region of the candidate arrays.  Boundary keys take
-  // their value from bpool and are written to the pooled row here.
-  uint32_t keys[kPer];
-  uint32_t nab = 0u, ncand = 0u;
+  // B. Sweep: wave w of round r reads keys r*kRoundKeys + w*kWaveKeys + ..,
+  // lane l the 4-key groups l + 64 i; groups i < 4 lie in the wave's first
+  // chunk, the rest in its second.  Past Lk the loads return zeros (masked).
+  const rsrc_t prs = make_rsrc(prow, (uint32_t)Lk * 4u);
+  uint2* cl = reinterpret_cast<uint2*>(un);
+  for (int r0 = 0; r0 < Lk; r0 += kRoundKeys) {
+    const int base = r0 + wv * kWaveKeys;
+    if (base >= Lk) break;
+    u32x4 x[8];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = c * kChunk + tid + i * kSelT;
-    keys[i] = 0u;
-    if (j < Lk) {
-      float v = cv[i];
-      const int bi = (j + h) / geom.kps;
-      const int off = j + h - bi * geom.kps;
-      if (bi >= 1 && bi <= nb && off < w2) {
-        v = bpool[(bi - 1) * w2 + off];
-        prow[j] = v;
+    for (int i = 0; i < 8; ++i) x[i] = buf_load16(prs, (uint32_t)(base + 4 * (lane + 64 * i)) * 4u);
+    uint32_t keys[8][4];
+    uint32_t na0 = 0u, na1 = 0u, nc = 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = base + 4 * (lane + 64 * i) + e;
+        const uint32_t key = pooled_key(x[i][e], j, prot, kbig);
+        keys[i][e] = key;
+        const uint32_t d = key >> kShift1;
+        const bool valid = j < Lk;
+        const uint32_t above = (valid && d > b1) ? 1u : 0u;
+        if (i < 4) na0 += above;
+        else na1 += above;
+        nc += (valid && d == b1) ? 1u : 0u;
       }
-      keys[i] = j >= prot ? kbig : float_key(v);
-      const uint32_t d = keys[i] >> kShift1;
-      nab += d > b1 ? 1u : 0u;
-      ncand += d == b1 ? 1u : 0u;
+    const uint32_t s0 = wave_reduce_add(na0), s1 = wave_reduce_add(na1);
+    const int c0 = base / kChunk;
+    if (lane == 0) {
+      gtc[c0] = s0;
+      if (base + kChunk < Lk) gtc[c0 + 1] = s1;
+    }
+    // Candidate slots: a wave-wide exclusive scan of the lanes' counts and
+    // one LDS atomic per wave.
+    const uint32_t incl = wave_incl_scan(nc);
+    const uint32_t wtot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    uint32_t wbase = 0u;
+    if (lane == 0 && wtot) wbase = atomicAdd(&small[112], wtot);
+    wbase = (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase);
+    if (nc) {
+      uint32_t pos = wbase + incl - nc;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = base + 4 * (lane + 64 * i) + e;
+          if (j < Lk && (keys[i][e] >> kShift1) == b1) {
+            if (pos < (uint32_t)kResCandCap) cl[pos] = make_uint2(keys[i][e], (uint32_t)j);
+            ++pos;
+          }
+        }
     }
   }
-  uint32_t pc, dummy, tot_c, tot_ab;
-  block_excl_scan2<kSelT>(ncand, nab, &pc, &dummy, &tot_c, &tot_ab, wsum);
-  uint32_t pos = (uint32_t)c * kChunk + pc;
-  uint32_t* ckey = ws.cand_key + (int64_t)row * Lk;
+  __syncthreads();
+  const uint32_t ncand = small[112];
+  const bool in_lds = ncand <= (uint32_t)kResCandCap;
+
+  // Every candidate (key, index): from the LDS list, or by sweeping the row.
+  auto for_cands = [&](auto&& f) __attribute__((always_inline)) {
+    if (in_lds) {
+      for (uint32_t p = tid; p < ncand; p += kResT) {
+        const uint2 cv = cl[p];
+        f(cv.x, (int)cv.y);
+      }
+    } else {
+      for (int j0 = 4 * tid; j0 < Lk; j0 += 4 * kResT) {
+        const u32x4 xv = buf_load16(prs, (uint32_t)j0 * 4u);
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = c * kChunk + tid + i * kSelT;
-    if (j < Lk && (keys[i] >> kShift1) == b1) {
-      ckey[pos] = keys[i];
-      ++pos;
+        for (int e = 0; e < 4; ++e) {
+          const int j = j0 + e;
+          const uint32_t key = pooled_key(xv[e], j, prot, kbig);
+          if (j < Lk && (key >> kShift1) == b1) f(key, j);
+        }
+      }
+    }
+  };
+
+  // C. Digits 2 and 3.
+  for_cands([&](uint32_t key, int) { atomicAdd(&hist2[(key >> kShift2) & (kBins2 - 1)], 1u); });
+  __syncthreads();
+  if (tid < 64) wave_find_bin<kBins2>(hist2, nullptr, k1, fb);
+  __syncthreads();
+  const uint32_t b2 = fb[0];
+  const uint32_t k2 = k1 - fb[1];
+  const uint32_t pre = (b1 << kBits2) | b2;
+  for_cands([&](uint32_t key, int) {
+    if ((key >> kShift2) == pre) atomicAdd(&hist3[key & (kBins3 - 1)], 1u);
+  });
+  __syncthreads();
+  if (tid < 64) wave_find_bin<kBins3>(hist3, nullptr, k2, fb + 4);
+  __syncthreads();
+  const uint32_t T = (pre << kBits3) | fb[4];
+  const uint32_t take_eq = k2 - fb[5];
+
+  // D. Per-chunk counts, then their exclusive prefix sums for emit.
+  for_cands([&](uint32_t key, int j) {
+    if (key > T) atomicAdd(&gtc[j / kChunk], 1u);
+    else if (key == T) atomicAdd(&eqc[j / kChunk], 1u);
+  });
+  __syncthreads();
+  const int seg = (chunks + kResT - 1) / kResT;  // consecutive chunks per thread (<= kCntPer)
+  uint32_t sg = 0u, se = 0u;
+#pragma unroll
+  for (int i = 0; i < kCntPer; ++i) {
+    if (i >= seg) break;
+    const int cc = tid * seg + i;
+    if (cc < chunks) {
+      sg += gtc[cc];
+      se += eqc[cc];
+    }
+  }
+  uint32_t pg, pe;
+  block_excl_scan2<kResT>(sg, se, &pg, &pe, nullptr, nullptr, small);
+  uint2* cnt = ws.cnt + (int64_t)row * chunks;
+#pragma unroll
+  for (int i = 0; i < kCntPer; ++i) {
+    if (i >= seg) break;
+    const int cc = tid * seg + i;
+    if (cc < chunks) {
+      cnt[cc] = make_uint2(pg, pe);
+      pg += gtc[cc];
+      pe += eqc[cc];
     }
   }
   if (tid == 0) {
-    ws.cnt[(int64_t)row * chunks + c] = make_uint2(tot_ab, tot_c);
-    if (c == 0) {
-      rw[kRowB1 + 0] = b1;
-      rw[kRowB1 + 1] = k1;
-      rw[kRowB1 + 2] = gmax;
-    }
+    rw[kRowB1 + 0] = T;
+    rw[kRowB1 + 1] = take_eq;
+    rw[kRowB1 + 2] = gmax;
   }
 }
 
 // ---------------------------------------------------------------------------
-// emit: grid = rows * chunks.  Gathers the row's candidates into LDS and
-// resolves T from them, then thread t owns the kPer consecutive keys
-// c*kChunk + kPer*t ..; kept keys are written in index order, then (when ko
-// is given) their K/V rows are copied.
+// emit: grid = rows * chunks.  Thread t owns the kPer consecutive keys
+// c*kChunk + kPer*t ..; the kept keys of the chunk are written in index
+// order from the chunk's offsets (resolve), then (when ko is given) their
+// K/V rows are copied.
 // ---------------------------------------------------------------------------
 struct CompactArgs {
   const uint8_t* k;
@@ -183,200 +297,29 @@ struct CompactArgs {
   int64_t out_ld;      // rows per head in ko / vo
 };
 
-constexpr int kEmitCandLds = 4096;                  // candidates held in LDS (more: read from global)
-constexpr int kSpecPer = kEmitCandLds / (4 * kSelT);  // speculative 4-candidate groups per thread
-constexpr int kCntPer = kMaxChunks / kSelT;           // chunk counts per thread (at most)
-constexpr int kSpecMax = 128;                         // speculative candidates per chunk region (at most)
-
-// Candidate p of the row's list (chunk-major) when it is not in LDS: chunk
-// by binary search over the exclusive prefix counts s_pref[0..chunks].
-__device__ __forceinline__ uint32_t cand_global(const uint32_t* s_pref, int chunks, const uint32_t* gkey,
-                                                uint32_t p) {
-  int lo = 0, hi = chunks - 1;  // last chunk with s_pref[cc] <= p
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (s_pref[mid] <= p) lo = mid;
-    else hi = mid - 1;
-  }
-  const int64_t at = (int64_t)lo * kChunk + (p - s_pref[lo]);
-  return gkey[at];
-}
-
 __global__ void __launch_bounds__(kSelT)
-sel_emit_kernel(int Lk, int window, int keep, int chunks, int spec, SelWs ws, int64_t* __restrict__ out_idx,
+sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __restrict__ out_idx,
                 float* __restrict__ pooled_out, CompactArgs ca) {
-  __shared__ uint32_t hist[kBins2 + kBins3];  // digit-2 and digit-3 histograms
-  __shared__ uint32_t small[128];  // scan partials [0, 32), bin / counts at 64.., max at 96..
-  __shared__ uint32_t lkey[kEmitCandLds];
-  __shared__ uint32_t s_pref[kMaxChunks + 1];
+  __shared__ uint32_t small[64];
   __shared__ int s_src[kChunk];
   __shared__ int s_dst[kChunk];
   const int tid = threadIdx.x;
   const int row = blockIdx.x / chunks;
   const int c = blockIdx.x % chunks;
-  uint32_t* wsum = small;
   const uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
   const float* pooled = ws.pooled + (int64_t)row * Lk;
-  const uint32_t* gkey = ws.cand_key + (int64_t)row * Lk;
-  const uint2* cnt = ws.cnt + (int64_t)row * chunks;
   const int prot = Lk - window;
 
-  // One round trip: the row words, this chunk's pooled values, every chunk's
-  // counts and, speculatively, the first `spec` candidates (a multiple of 4)
-  // of the first ncov = kEmitCandLds / spec chunk regions.
+  // One round trip: this chunk's pooled values, its offsets and the row words.
   const int j0 = c * kChunk + kPer * tid;
   float pv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) pv[i] = (j0 + i < Lk) ? pooled[j0 + i] : 0.f;
-  const uint32_t b1 = rw[kRowB1 + 0], k1 = rw[kRowB1 + 1];
+  const uint2 off = ws.cnt[(int64_t)row * chunks + c];
+  const uint32_t T = rw[kRowB1 + 0], take_eq = rw[kRowB1 + 1];
   const float big = key_float(rw[kRowB1 + 2]) + 1.0f;
   const uint32_t kbig = float_key(big);
-  const int seg = (chunks + kSelT - 1) / kSelT;  // chunk counts owned by each thread (<= kCntPer)
-  uint2 cv[kCntPer];
-#pragma unroll
-  for (int i = 0; i < kCntPer; ++i) {
-    if (i >= seg) break;
-    const int cc = tid * seg + i;
-    cv[i] = cc < chunks ? cnt[cc] : make_uint2(0u, 0u);
-  }
-  uint4 sk[kSpecPer];
-  const int nspec = min(chunks * spec, kEmitCandLds);
-#pragma unroll
-  for (int i = 0; i < kSpecPer; ++i) {
-    if (4 * i * kSelT >= nspec) break;
-    const int e = 4 * (tid + i * kSelT);
-    const int cc = e / spec, off = e - cc * spec;
-    const int64_t at = (int64_t)cc * kChunk + off;
-    if (cc < chunks && at + 4 <= Lk) {
-      sk[i] = *reinterpret_cast<const uint4*>(gkey + at);
-    } else {
-      sk[i] = make_uint4(0u, 0u, 0u, 0u);
-    }
-  }
-
-  // Candidate counts -> exclusive prefix s_pref (chunk-major list order);
-  // above-b1 keys of the chunks before this one.
-  const int ncov = kEmitCandLds / spec;
-  uint32_t tsum = 0u, g = 0u, e = 0u;
-  bool overflow = false;
-#pragma unroll
-  for (int i = 0; i < kCntPer; ++i) {
-    if (i >= seg) break;
-    const int cc = tid * seg + i;
-    if (cc < chunks) {
-      tsum += cv[i].y;
-      if (cc < c) g += cv[i].x;
-      overflow |= cv[i].y > (cc < ncov ? (uint32_t)spec : 0u);
-    }
-  }
-  uint32_t run, dummy, nc;
-  block_excl_scan2<kSelT>(tsum, 0u, &run, &dummy, &nc, nullptr, wsum);
-#pragma unroll
-  for (int i = 0; i < kCntPer; ++i) {
-    if (i >= seg) break;
-    const int cc = tid * seg + i;
-    if (cc < chunks) {
-      s_pref[cc] = run;
-      run += cv[i].y;
-    }
-  }
-  if (tid == 0) s_pref[chunks] = nc;
-  const bool any_overflow = __syncthreads_or(overflow);
-  const bool in_lds = nc <= (uint32_t)kEmitCandLds;
-
-  // Candidates into LDS: the speculative ones, then (rarely) the rest of any
-  // region longer than spec.
-  if (in_lds) {
-#pragma unroll
-    for (int i = 0; i < kSpecPer; ++i) {
-      if (4 * i * kSelT >= nspec) break;
-      const int e4 = 4 * (tid + i * kSelT);
-      const int cc = e4 / spec, off = e4 - cc * spec;
-      if (cc < chunks) {
-        const uint32_t n = s_pref[cc + 1] - s_pref[cc];
-        const uint32_t kk[4] = {sk[i].x, sk[i].y, sk[i].z, sk[i].w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if ((uint32_t)(off + q) < n) {
-            lkey[s_pref[cc] + off + q] = kk[q];
-          }
-      }
-    }
-    if (any_overflow) {
-      // Every list entry not covered by the speculative loads, 8 loads in
-      // flight per thread.
-      for (uint32_t p0 = tid; p0 < nc; p0 += 8 * kSelT) {
-        uint32_t kv[8];
-        int32_t dst[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const uint32_t p = p0 + q * kSelT;
-          dst[q] = -1;
-          if (p < nc) {
-            int lo = 0, hi = chunks - 1;  // chunk of entry p
-            while (lo < hi) {
-              const int mid = (lo + hi + 1) >> 1;
-              if (s_pref[mid] <= p) lo = mid;
-              else hi = mid - 1;
-            }
-            const uint32_t o = p - s_pref[lo];
-            if (o >= (lo < ncov ? (uint32_t)spec : 0u)) {
-              kv[q] = gkey[(int64_t)lo * kChunk + o];
-              dst[q] = (int32_t)p;
-            }
-          }
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-          if (dst[q] >= 0) lkey[dst[q]] = kv[q];
-      }
-    }
-  }
-  uint32_t* hist2 = hist;
-  uint32_t* hist3 = hist + kBins2;
-  for (int i = tid; i < kBins2 + kBins3; i += kSelT) hist[i] = 0u;
-  __syncthreads();
-
-  // Digit 2 (every candidate is in bin b1); the bin searches run on one wave.
-  uint32_t* fb = small + 64;
-  for (uint32_t p = tid; p < nc; p += kSelT) {
-    uint32_t kv;
-    if (in_lds) kv = lkey[p];
-    else kv = cand_global(s_pref, chunks, gkey, p);
-    atomicAdd(&hist2[(kv >> kShift2) & (kBins2 - 1)], 1u);
-  }
-  __syncthreads();
-  if (tid < 64) wave_find_bin<kBins2>(hist2, nullptr, k1, fb);
-  __syncthreads();
-  const uint32_t b2 = fb[0];
-  const uint32_t k2 = k1 - fb[1];
-  const uint32_t pre = (b1 << kBits2) | b2;
-  // Digit 3 over the candidates matching the first two digits.
-  for (uint32_t p = tid; p < nc; p += kSelT) {
-    uint32_t kv;
-    if (in_lds) kv = lkey[p];
-    else kv = cand_global(s_pref, chunks, gkey, p);
-    if ((kv >> kShift2) == pre) atomicAdd(&hist3[kv & (kBins3 - 1)], 1u);
-  }
-  __syncthreads();
-  if (tid < 64) wave_find_bin<kBins3>(hist3, nullptr, k2, fb + 4);
-  __syncthreads();
-  const uint32_t T = (pre << kBits3) | fb[4];
-  const uint32_t take_eq = k2 - fb[5];
-
-  // Output offsets of this chunk: kept keys > T and keys == T in earlier
-  // chunks (above-b1 keys per chunk, plus the candidates of those chunks,
-  // which are list entries [0, s_pref[c])).
-  const uint32_t lim = s_pref[c];
-  for (uint32_t p = tid; p < lim; p += kSelT) {
-    uint32_t kv;
-    if (in_lds) kv = lkey[p];
-    else kv = cand_global(s_pref, chunks, gkey, p);
-    g += kv > T ? 1u : 0u;
-    e += kv == T ? 1u : 0u;
-  }
-  uint32_t gt0, eq0;
-  block_sum2<kSelT>(g, e, &gt0, &eq0, wsum);
+  const uint32_t gt0 = off.x, eq0 = off.y;
 
   uint32_t keys[kPer];
   uint32_t ng = 0u, ne = 0u;
@@ -391,7 +334,7 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, int spec, SelWs ws, in
     }
   }
   uint32_t pg, pe, tg, te;
-  block_excl_scan2<kSelT>(ng, ne, &pg, &pe, &tg, &te, wsum);
+  block_excl_scan2<kSelT>(ng, ne, &pg, &pe, &tg, &te, small);
   const uint32_t start = gt0 + min(eq0, take_eq);  // first output slot of this chunk
   uint32_t g_before = gt0 + pg, e_before = eq0 + pe;
 #pragma unroll
@@ -427,9 +370,9 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, int spec, SelWs ws, in
       for (int q = 0; q < kG; ++q) {
         const int t = t0 + q * kSelT;
         if (t < total) {
-          const int64_t off = (int64_t)s_src[t / ca.units] * ca.sl + 16 * (t % ca.units);
-          kv[q] = *reinterpret_cast<const u32x4*>(kb + off);
-          vv[q] = *reinterpret_cast<const u32x4*>(vb + off);
+          const int64_t o = (int64_t)s_src[t / ca.units] * ca.sl + 16 * (t % ca.units);
+          kv[q] = *reinterpret_cast<const u32x4*>(kb + o);
+          vv[q] = *reinterpret_cast<const u32x4*>(vb + o);
         }
       }
 #pragma unroll
@@ -481,13 +424,10 @@ hipError_t launch_select_after_pool(const float* scores, int rows, int Lk, int k
   const SelWs ws = sel_layout(ws_base, rows, Lk, nullptr);
   const int chunks = (Lk + kChunk - 1) / kChunk;
   const dim3 grid((unsigned)(rows * chunks));
-  launch(sel_cand_kernel, grid, dim3(kSelT), 0, st, scores, Lk, ks, window, keep, chunks,
-                     SplitGeom{n_splits, kps}, ws);
-  // Speculative candidates per chunk region: a multiple of 4, at least 4,
-  // chunks * spec <= kEmitCandLds.
-  const int spec = std::max(4, std::min(kSpecMax, kEmitCandLds / chunks) & ~3);
-  launch(sel_emit_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, spec, ws, out_idx,
-                     pooled_out, compact_args(cp));
+  launch(sel_resolve_kernel, dim3((unsigned)rows), dim3(kResT), 0, st, scores, Lk, ks, window, keep, chunks,
+         SplitGeom{n_splits, kps}, ws);
+  launch(sel_emit_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, ws, out_idx, pooled_out,
+         compact_args(cp));
   return hipGetLastError();
 }
 

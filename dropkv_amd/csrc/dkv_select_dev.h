@@ -9,31 +9,26 @@
 //   threshold the lowest indices win (torch.topk leaves that order open).
 //
 // Floats are mapped to order-preserving uint32 keys and the keep-th largest
-// key T is found by a radix select over 11 + 11 + 10 bits, spread so that
-// every stage runs on all CUs:
-//   pool   (pass-2 epilogue, or the standalone pool kernel) pooled values of
-//          the keys whose window lies inside one workgroup's range, the row
-//          maximum and the top-digit histogram (device atomics);
-//   cand   (row, 1024-key chunk) workgroups: each first pools the few keys
-//          next to the scoring pass's split boundaries (redundantly), which
-//          completes the histogram and fixes the boundary bin b1; then its
-//          chunk's keys above b1 are counted and those inside b1 (the
-//          candidates) written to the chunk's own region of the candidate
-//          arrays, with the two counts;
-//   emit   (row, chunk) workgroups: each gathers the row's candidates (a few
-//          percent of the row) into LDS, resolves digits 2 and 3 from them,
-//          derives its chunk's output offsets, writes its kept indices in
-//          index order and copies the K/V rows they name.
-// Every stage issues all of its global loads in one round trip where the
-// data allow (emit loads the first kSpec candidates of every chunk region
-// before it knows the counts).
+// key T is found by a radix select over 11 + 11 + 10 bits:
+//   pool    (pass-2 epilogue, or the standalone pool kernel) pooled values of
+//           the keys whose window lies inside one workgroup's range, the row
+//           maximum and the top-digit histogram (device atomics);
+//   resolve (one workgroup per row) pools the few keys next to the scoring
+//           pass's split boundaries, which completes the histogram and fixes
+//           the top-digit bin b1; sweeps the row once for the keys above b1
+//           per chunk and the keys inside b1 (the candidates, a few percent
+//           of the row, kept in LDS); resolves digits 2 and 3 from the
+//           candidates; writes per 1024-key chunk the kept keys above T and
+//           the keys equal to T before it;
+//   emit    (row, chunk) workgroups write the chunk's kept indices in index
+//           order from those offsets and copy the K/V rows they name.
 #pragma once
 
 #include "dkv_common.h"
 
 namespace dkv {
 
-constexpr int kChunk = 1024;      // keys per cand/emit workgroup (offset granularity)
+constexpr int kChunk = 1024;      // keys per emit workgroup (offset granularity)
 constexpr int kBits1 = 11, kBits2 = 11, kBits3 = 10;  // radix digits, most significant first
 constexpr int kShift1 = 32 - kBits1;                // digit 1 = key >> kShift1
 constexpr int kShift2 = kBits3;                     // digit 2 = (key >> kShift2) & (kBins2 - 1)
@@ -46,17 +41,16 @@ constexpr int kBndLds = 4096;     // LDS words for the boundary keys' raw-score 
 constexpr int kBndPoolLds = 2048; // LDS words for the boundary keys' pooled values
 
 // Per-row words that must be zero on entry (the merge kernel or the zero
-// kernel clears them every call), then results of the cand stage:
+// kernel clears them every call), then results of the resolve stage:
 constexpr int kRowMax = 0;                 // max pooled key of the interiors
-constexpr int kRowB1 = 1;                  // b1, keep left in b1, max key of the row (cand stage)
+constexpr int kRowB1 = 1;                  // T, keys equal to T that are kept, max key of the row (resolve)
 constexpr int kRowHist1 = 4;               // top-digit histogram (unprotected interior keys), 16-byte aligned
 constexpr int kRowWords = kRowHist1 + kBins1;
 
 struct SelWs {
   uint32_t* rowws;     // [rows][kRowWords]
   float* pooled;       // [rows][Lk]
-  uint2* cnt;          // [rows][chunks] {keys above b1, candidates} of each chunk
-  uint32_t* cand_key;  // [rows][Lk]: chunk c's candidate keys at c*kChunk ..
+  uint2* cnt;          // [rows][chunks] {kept keys above T, keys equal to T} in the chunks before each
 };
 
 inline size_t sel_al256(size_t b) { return (b + 255) & ~size_t(255); }
@@ -73,7 +67,6 @@ inline SelWs sel_layout(char* base, int64_t rows, int64_t Lk, size_t* total) {
   w.rowws = reinterpret_cast<uint32_t*>(take((size_t)rows * kRowWords * 4));
   w.pooled = reinterpret_cast<float*>(take((size_t)rows * Lk * 4));
   w.cnt = reinterpret_cast<uint2*>(take((size_t)rows * chunks * 8));
-  w.cand_key = reinterpret_cast<uint32_t*>(take((size_t)rows * Lk * 4));
   if (total) *total = off;
   return w;
 }
@@ -85,9 +78,56 @@ struct SplitGeom {
   int n_splits, kps;
 };
 
-// Whether the cand stage can hold the boundary keys of this geometry in LDS.
+// Whether the resolve stage can hold the boundary keys of this geometry in LDS.
 __host__ __device__ constexpr bool boundary_fits(int64_t n_splits, int64_t h) {
   return (n_splits - 1) * 4 * h <= kBndLds && (n_splits - 1) * 2 * h <= kBndPoolLds;
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level scans and reductions on DPP (a few cycles per step, against an
+// LDS round trip per step for lane shuffles).
+// ---------------------------------------------------------------------------
+// DPP move of x with zeros where the source lane is out of the row or the
+// destination lane is masked off (row_mask / bank_mask).
+template <int kCtrl, int kRowMask, int kBankMask>
+__device__ __forceinline__ uint32_t dpp_z(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kCtrl, kRowMask, kBankMask, true);
+}
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr3 = 0x113, kDppRowShr4 = 0x114,
+              kDppRowShr8 = 0x118, kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+// Inclusive prefix sum over the 64 lanes: within each row of 16 lanes by row
+// shifts (1, 2, 3, then 4 into banks 1-3 and 8 into banks 2-3), then across
+// rows by broadcasting lane 15 into rows 1 and 3 and lane 31 into rows 2-3.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  uint32_t t = x + dpp_z<kDppRowShr1, 0xf, 0xf>(x);
+  t += dpp_z<kDppRowShr2, 0xf, 0xf>(x);
+  t += dpp_z<kDppRowShr3, 0xf, 0xf>(x);
+  t += dpp_z<kDppRowShr4, 0xf, 0xe>(t);
+  t += dpp_z<kDppRowShr8, 0xf, 0xc>(t);
+  t += dpp_z<kDppRowBcast15, 0xa, 0xf>(t);
+  t += dpp_z<kDppRowBcast31, 0xc, 0xf>(t);
+  return t;
+}
+
+// Sum and maximum over the 64 lanes (wave-uniform results).
+__device__ __forceinline__ uint32_t wave_reduce_add(uint32_t x) {
+  int v = (int)x;
+  v += dpp_i<kDppQuadSwap1>(v);
+  v += dpp_i<kDppQuadSwap2>(v);
+  v += dpp_i<kDppHalfMirror>(v);
+  v += dpp_i<kDppMirror>(v);
+  return (uint32_t)((__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+                    (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48)));
+}
+
+__device__ __forceinline__ uint32_t wave_reduce_max(uint32_t x) {
+  x = max(x, (uint32_t)dpp_i<kDppQuadSwap1>((int)x));
+  x = max(x, (uint32_t)dpp_i<kDppQuadSwap2>((int)x));
+  x = max(x, (uint32_t)dpp_i<kDppHalfMirror>((int)x));
+  x = max(x, (uint32_t)dpp_i<kDppMirror>((int)x));
+  return max(max((uint32_t)__builtin_amdgcn_readlane((int)x, 0), (uint32_t)__builtin_amdgcn_readlane((int)x, 16)),
+             max((uint32_t)__builtin_amdgcn_readlane((int)x, 32), (uint32_t)__builtin_amdgcn_readlane((int)x, 48)));
 }
 
 // ---------------------------------------------------------------------------
@@ -100,15 +140,7 @@ __device__ __forceinline__ void block_excl_scan2(uint32_t a, uint32_t b, uint32_
                                                  uint32_t* tb, uint32_t* wsum) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  uint32_t xa = a, xb = b;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t ya = __shfl_up((int)xa, o), yb = __shfl_up((int)xb, o);
-    if (lane >= o) {
-      xa += ya;
-      xb += yb;
-    }
-  }
+  const uint32_t xa = wave_incl_scan(a), xb = wave_incl_scan(b);
   __syncthreads();
   if (lane == 63) {
     wsum[w] = xa;
@@ -135,11 +167,8 @@ __device__ __forceinline__ void block_excl_scan2(uint32_t a, uint32_t b, uint32_
 template <int NT>
 __device__ __forceinline__ void block_sum2(uint32_t a, uint32_t b, uint32_t* ta, uint32_t* tb, uint32_t* wsum) {
   constexpr int NW = NT / 64;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    a += (uint32_t)__shfl_xor((int)a, o);
-    b += (uint32_t)__shfl_xor((int)b, o);
-  }
+  a = wave_reduce_add(a);
+  b = wave_reduce_add(b);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) {
     wsum[threadIdx.x >> 6] = a;
@@ -192,7 +221,7 @@ __device__ void find_bin(const uint32_t* hist, uint32_t k, int* s_bin, uint32_t*
 // bins of its segment (NB/64 consecutive bins, lane order = descending bins;
 // the reads are rotated per lane so that a wave's reads hit distinct banks),
 // the lane holding the k-th key is found by a scan over lanes, and its
-// segment is then scanned one bin per lane.
+// segment is then scanned one bin per lane (both scans on DPP).
 template <int NB>
 __device__ void wave_find_bin(const uint32_t* hist, const uint32_t* he, uint32_t k, uint32_t* out) {
   constexpr int per = NB / 64;
@@ -206,29 +235,14 @@ __device__ void wave_find_bin(const uint32_t* hist, const uint32_t* he, uint32_t
     th += hist[b];
     if (he) te += he[b];
   }
-  uint32_t ih = th, ie = te;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t yh = (uint32_t)__shfl_up((int)ih, o), ye = (uint32_t)__shfl_up((int)ie, o);
-    if (lane >= o) {
-      ih += yh;
-      ie += ye;
-    }
-  }
+  const uint32_t ih = wave_incl_scan(th), ie = he ? wave_incl_scan(te) : 0u;
   const uint64_t hit = __ballot(ih - th < k && ih >= k);
   const int lf = __ffsll((unsigned long long)hit) - 1;
-  const uint32_t run0 = (uint32_t)__shfl((int)(ih - th), lf), rune0 = (uint32_t)__shfl((int)(ie - te), lf);
+  const uint32_t run0 = (uint32_t)__builtin_amdgcn_readlane((int)(ih - th), lf);
+  const uint32_t rune0 = (uint32_t)__builtin_amdgcn_readlane((int)(ie - te), lf);
   const int b = NB - 1 - lf * per - lane;
   const uint32_t hv = lane < per ? hist[b] : 0u, ev = (lane < per && he) ? he[b] : 0u;
-  uint32_t jh = hv, je = ev;
-#pragma unroll
-  for (int o = 1; o < per; o <<= 1) {
-    const uint32_t yh = (uint32_t)__shfl_up((int)jh, o), ye = (uint32_t)__shfl_up((int)je, o);
-    if (lane >= o) {
-      jh += yh;
-      je += ye;
-    }
-  }
+  const uint32_t jh = wave_incl_scan(hv), je = he ? wave_incl_scan(ev) : 0u;
   if (lane < per && run0 + jh - hv < k && run0 + jh >= k) {
     out[0] = (uint32_t)b;
     out[1] = run0 + jh - hv;
@@ -238,8 +252,7 @@ __device__ void wave_find_bin(const uint32_t* hist, const uint32_t* he, uint32_t
 }
 
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t x, uint32_t* red) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x = max(x, (uint32_t)__shfl_xor((int)x, o));
+  x = wave_reduce_max(x);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
   __syncthreads();
