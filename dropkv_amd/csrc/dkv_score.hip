@@ -1273,6 +1273,274 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
 }
 
 // ---------------------------------------------------------------------------
+// Pass 2 for several row-chunks (3 <= n_mc <= 8: large GQA groups or
+// windows), in one sweep over K/V.  Workgroup = (head, key split) with 8
+// waves; wave w holds row-chunk w's Q / Y-hi / Y-lo operands and statistics
+// in registers (waves past n_mc only stage).  Each 32-key tile of K and V is
+// loaded once per workgroup into LDS (rows padded against bank conflicts,
+// with |v|^2 of each row), kG tiles per stage, double-buffered: the loads of
+// the next stage are in flight while the waves work on the current one.
+// Each wave's per-key sums over its 32 rows go to LDS, and after the stage's
+// one barrier the keys' totals are summed over the waves in wave order, so
+// the result does not depend on timing.  With one workgroup per row-chunk
+// group instead, K/V would be streamed once per group.
+// ---------------------------------------------------------------------------
+template <int CPR>
+__device__ __forceinline__ float sum_over_row_lanes(float x) {
+  x += dpp_f<kDppQuadSwap1>(x);
+  x += dpp_f<kDppQuadSwap2>(x);
+  if (CPR >= 8) x += dpp_f<kDppHalfMirror>(x);
+  if (CPR >= 16) x += dpp_f<kDppMirror>(x);
+  return x;
+}
+
+template <typename T, int D, int kG, bool PR>
+__global__ void __launch_bounds__(64 * kWideWaves, 1)
+pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int Hkv, int Lq, int Lk, int W, int g,
+              int M, int n_mc, int n_splits, int kps, float scale_log2, float eps, const u32x4* __restrict__ opblk,
+              const float* __restrict__ stblk, float* __restrict__ scores, SelFuse fz) {
+  typedef typename Elem<T>::v8 v8;
+  constexpr int KK = D / 32;
+  constexpr int OPS = kOpSlots * kMB * KK;
+  constexpr int NT = 64 * kWideWaves;
+  constexpr int RB = D * (int)sizeof(T);
+  constexpr int CPR = RB / 16;                // 16-byte chunks per row
+  constexpr int KCH = kTile * CPR;            // chunks per tile and tensor
+  static_assert(KCH <= NT && KCH % 64 == 0, "one K and one V chunk per thread, whole waves");
+  static_assert(CPR == 4 || CPR == 8 || CPR == 16, "a row's chunks in one DPP row");
+  constexpr int kRowPitch = D + 8;            // elements per padded row in LDS
+  constexpr int kTensorWords = kTile * kRowPitch / 2;
+  constexpr int kTileWords = 2 * kTensorWords + kTile;  // K rows, V rows, |v|^2
+  constexpr int kStage = kG * kTileWords;
+  __shared__ __attribute__((aligned(16))) uint32_t lds[2 * kStage > kPoolLdsWords ? 2 * kStage : kPoolLdsWords];
+  __shared__ float red[2][kWideWaves][kG * kTile];  // per-wave key sums of a stage, double-buffered
+  __shared__ __attribute__((aligned(16))) float sc_row[kScLds];
+  __shared__ uint32_t hist_l[kBins1 + 16];
+
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int split = lid % n_splits;
+  const int head = lid / n_splits;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wv = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int mc = wv;
+  const bool active = mc < n_mc;
+  const bool sc_lds = fz.enabled && fz.sc_lds;
+  if (sc_lds)
+    for (int i = tid; i < kBins1; i += NT) hist_l[i] = 0u;
+
+  const float out_scale = -2.0f * (1.0f / static_cast<float>(g));
+  const int k_begin = split * kps;
+  const int k_end = min(k_begin + kps, Lk);
+  const int64_t roff = ((int64_t)head * kv_ld + k_begin) * D;
+  const uint32_t range = (uint32_t)(k_end - k_begin) * RB;
+  const rsrc_t krs = make_rsrc(kp + roff, range), vrs = make_rsrc(vp + roff, range);
+  const int nrel = k_end - k_begin;
+  const int ntiles = (nrel + kTile - 1) / kTile;
+  const int ngroups = (ntiles + kG - 1) / kG;
+
+  // This wave's operands (merge wrote them in pass 2's LDS order) and row
+  // statistics: lse (log2 units), |y|^2, the row's dominant key and
+  // -dist2/2 there.
+  const int c = active ? mc : 0;
+  v8 qo[kMB][KK], yh[kMB][KK], yl[kMB][KK];
+  float lse2[kMB], nyh[kMB], snd2[kMB];
+  int skey[kMB];
+  {
+    const u32x4* ob = opblk + ((size_t)head * n_mc + c) * OPS * 64 + lane;
+    const float* st = stblk + ((size_t)head * n_mc + c) * kMB * kStatWords + li;
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb) {
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        qo[mb][kk] = __builtin_bit_cast(v8, ob[(size_t)((0 * kMB + mb) * KK + kk) * 64]);
+        yh[mb][kk] = __builtin_bit_cast(v8, ob[(size_t)((1 * kMB + mb) * KK + kk) * 64]);
+        yl[mb][kk] = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
+      }
+      lse2[mb] = st[mb * kStatWords];
+      nyh[mb] = -0.5f * st[mb * kStatWords + 16];
+      skey[mb] = __builtin_bit_cast(int, st[mb * kStatWords + 32]);
+      snd2[mb] = st[mb * kStatWords + 48];
+    }
+  }
+  const bool pad_chunk = mc * kRows + kRows > M;
+  const int unmasked_end = Lk - W + 1;
+
+  // Staging: thread tid < KCH owns chunk tid % CPR of row tid / CPR of each
+  // tile, of K and of V.
+  const int sr = tid / CPR, scn = tid % CPR;
+  const uint32_t s_off = (uint32_t)(sr * D + 8 * scn) * sizeof(T);
+  u32x4 kreg[kG], vreg[kG];
+  auto issue = [&](int grp) __attribute__((always_inline)) {
+#pragma unroll
+    for (int gt = 0; gt < kG; ++gt) {
+      const uint32_t base = (uint32_t)((grp * kG + gt) * kTile) * RB;
+      if (tid < KCH) {
+        kreg[gt] = buf_load16(krs, base + s_off);
+        vreg[gt] = buf_load16(vrs, base + s_off);
+      }
+    }
+  };
+  auto stage = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int gt = 0; gt < kG; ++gt) {
+      uint32_t* kl = lds + buf * kStage + gt * kTileWords;
+      uint32_t* vl = kl + kTensorWords;
+      float* vn = reinterpret_cast<float*>(vl + kTensorWords);
+      if (tid < KCH) {
+        *reinterpret_cast<u32x4*>(kl + (sr * kRowPitch + 8 * scn) / 2) = kreg[gt];
+        *reinterpret_cast<u32x4*>(vl + (sr * kRowPitch + 8 * scn) / 2) = vreg[gt];
+        // |v|^2 of the row: fp32 sum of the exact element values.
+        const float ss = sum_over_row_lanes<CPR>(sumsq8<T>(bitcast_u4<v8>(vreg[gt]), 0.f));
+        if (scn == 0) vn[sr] = ss;
+      }
+    }
+  };
+
+  // One tile: this wave's per-key sums over its rows into red[par][wv][gt * kTile ..].
+  auto tile = [&](const uint32_t* kl, int t0, int par, int gt) __attribute__((always_inline)) {
+    const uint32_t* vl = kl + kTensorWords;
+    const float* vn = reinterpret_cast<const float*>(vl + kTensorWords);
+    f32x4 sacc[2][kMB], gacc[2][kMB];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const f32x4 vn2 = *reinterpret_cast<const f32x4*>(vn + 16 * kb + 4 * lg);
+      v8 kop[KK], vop[KK];
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const int w = ((16 * kb + li) * kRowPitch + 32 * kk + 8 * lg) / 2;
+        kop[kk] = bitcast_u4<v8>(*reinterpret_cast<const u32x4*>(kl + w));
+        vop[kk] = bitcast_u4<v8>(*reinterpret_cast<const u32x4*>(vl + w));
+      }
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb) {
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f};
+        f32x4 ga;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ga[r] = fmaf(vn2[r], -0.5f, nyh[mb]);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) sa = Elem<T>::mfma(kop[kk], qo[mb][kk], sa);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          ga = Elem<T>::mfma(vop[kk], yh[mb][kk], ga);
+          ga = Elem<T>::mfma(vop[kk], yl[mb][kk], ga);
+        }
+        sacc[kb][mb] = sa;
+        gacc[kb][mb] = ga;
+      }
+    }
+    float sc[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[kb][r] = 0.f;
+    bool sink_here = false;
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb) sink_here |= (uint32_t)(skey[mb] - t0) < (uint32_t)kTile;
+    auto epilogue = [&](auto masked_c) __attribute__((always_inline)) {
+      constexpr bool kMasked = decltype(masked_c)::value;
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb) {
+        const int m = mc * kRows + mb * 16 + li;
+        const int bound = kMasked ? row_bound(m, M, W, Lk) : 0;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; r += 2) {
+            float p[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              p[e] = __builtin_amdgcn_exp2f(sacc[kb][mb][r + e] * scale_log2 - lse2[mb]);
+              if (kMasked) p[e] = (t0 + 16 * kb + 4 * lg + r + e) <= bound ? p[e] : 0.f;
+              p[e] = min_one_nonneg(p[e]);
+            }
+            if (PR) round_through2<T>(p[0], p[1]);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const float ratio = p[e] * __builtin_amdgcn_rcpf(1.0f - p[e] + eps);
+              float nd2 = min_zero(gacc[kb][mb][r + e]);  // -dist2/2, dist2 clamped at 0
+              if (kMasked) nd2 = (t0 + 16 * kb + 4 * lg + r + e) == skey[mb] ? snd2[mb] : nd2;
+              sc[kb][r + e] = fmaf(ratio * ratio, nd2, sc[kb][r + e]);
+            }
+          }
+      }
+    };
+    if (pad_chunk || t0 + kTile > unmasked_end || __any(sink_here))
+      epilogue(std::true_type{});
+    else
+      epilogue(std::false_type{});
+    // Sum over the 16 rows of lanes li = 0..15 (reduce-scatter): lane li
+    // with li % 4 == 0 then holds key 16kb + 4lg + li/4.
+    const bool h8 = li & 8, h4 = li & 4;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float k0 = h8 ? sc[kb][2] : sc[kb][0];
+      float k1 = h8 ? sc[kb][3] : sc[kb][1];
+      k0 += __shfl_xor(h8 ? sc[kb][0] : sc[kb][2], 8);
+      k1 += __shfl_xor(h8 ? sc[kb][1] : sc[kb][3], 8);
+      float v = h4 ? k1 : k0;
+      v += __shfl_xor(h4 ? k0 : k1, 4);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 1);
+      if ((li & 3) == 0) red[par][wv][gt * kTile + 16 * kb + 4 * lg + (li >> 2)] = v;
+    }
+  };
+
+  // The keys' totals of a stage over the active waves, in wave order, after
+  // the barrier that follows the stage's red writes.
+  auto finish = [&](int grp, int par) __attribute__((always_inline)) {
+    if (tid < kG * kTile) {
+      const int it = grp * kG + tid / kTile;
+      float v = red[par][0][tid];
+      for (int w = 1; w < n_mc; ++w) v += red[par][w][tid];
+      const int n = k_begin + it * kTile + tid % kTile;
+      if (it < ntiles && n < k_end) {
+        scores[(int64_t)head * Lk + n] = v * out_scale;
+        if (sc_lds) sc_row[n - k_begin] = v * out_scale;
+      }
+    }
+  };
+
+  auto group = [&](int grp, auto st_c) __attribute__((always_inline)) {
+    constexpr int st = decltype(st_c)::value;
+    if (grp + 1 < ngroups) issue(grp + 1);
+    if (active) {
+#pragma unroll
+      for (int gt = 0; gt < kG; ++gt) {
+        const int it = grp * kG + gt;
+        if (it < ntiles) tile(lds + st * kStage + gt * kTileWords, k_begin + it * kTile, grp & 1, gt);
+      }
+    }
+    if (grp + 1 < ngroups) stage(1 - st);
+    __syncthreads();
+    finish(grp, grp & 1);
+  };
+  issue(0);
+  stage(0);
+  __syncthreads();
+  for (int grp = 0; grp < ngroups; grp += 2) {
+    group(grp, std::integral_constant<int, 0>{});
+    if (grp + 1 < ngroups) group(grp + 1, std::integral_constant<int, 1>{});
+  }
+
+  if (fz.enabled) {
+    // The stage loop ended with a barrier, but the last stage's key totals
+    // (finish) were stored after it.
+    __syncthreads();
+    const int h = fz.ks / 2;
+    const int i0 = split == 0 ? 0 : k_begin + h;
+    const int i1 = k_end >= Lk ? Lk : k_end - h;
+    float* prow = fz.ws.pooled + (int64_t)head * Lk;
+    uint32_t* rw = fz.ws.rowws + (int64_t)head * kRowWords;
+    if (sc_lds)
+      pool_range_lds<NT>(sc_row, k_begin, prow, rw, Lk, h, Lk - fz.window, i0, i1, hist_l, hist_l + kBins1);
+    else
+      pool_range<NT>(scores + (int64_t)head * Lk, prow, rw, Lk, h, Lk - fz.window, i0, i1,
+                     reinterpret_cast<float*>(lds), lds + kSub + 2 * kMaxHalo, lds + kSub + 2 * kMaxHalo + kBins1);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host-side launch helpers (called from dkv_capi.hip).
 // ---------------------------------------------------------------------------
 
@@ -1296,6 +1564,9 @@ static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b)
 #endif
 #ifndef DKV_P1_WIDE_GROUP
 #define DKV_P1_WIDE_GROUP 1    // tiles per LDS stage of the wide pass 1 (1, 2 or 4)
+#endif
+#ifndef DKV_P2_WIDE_GROUP
+#define DKV_P2_WIDE_GROUP 3    // tiles per LDS stage of the wide pass 2 (1 to 3)
 #endif
 
 ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W,
@@ -1401,6 +1672,16 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
     lds2 = std::max(lds2, (size_t)kPoolLdsWords * 4);
   }
   const dim3 g2(p.heads * p.s2);
+  if (p.p1_wide) {
+    // One sweep over K/V for all row-chunks (pass2w); its LDS is static.
+    if (p_round)
+      launch((pass2w_kernel<T, D, DKV_P2_WIDE_GROUP, true>), g2, dim3(64 * kWideWaves), 0, st, kk, vv, kv_ld, Hkv, Lq,
+             Lk, W, p.g, p.M, p.n_mc, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
+    else
+      launch((pass2w_kernel<T, D, DKV_P2_WIDE_GROUP, false>), g2, dim3(64 * kWideWaves), 0, st, kk, vv, kv_ld, Hkv,
+             Lq, Lk, W, p.g, p.M, p.n_mc, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
+    return hipGetLastError();
+  }
   if (p_round)
     launch((pass2_kernel<T, D, 8, 1, true>), g2, dim3(512), lds2, st, kk, vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc,
            cg, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
