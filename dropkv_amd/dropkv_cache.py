@@ -26,7 +26,7 @@ from typing import Any, Iterable, Optional
 
 import torch
 
-from . import ops
+from . import ops, torch_ops
 from .hf_query import take_captured_query
 
 logger = logging.getLogger(__name__)
@@ -93,6 +93,8 @@ def _deployed_path_scores(query_states, key_states, value_states, window_size: i
     if Hq % Hkv != 0:
         raise ValueError(f"Query heads {Hq} must be divisible by KV heads {Hkv}")
     W = min(window_size, query_states.shape[2])
+    if torch_ops.compiling():
+        return torch.ops.dropkv.scores(query_states, key_states, value_states, W, 1e-6, True, True, 0)
     return ops.scores(query_states, key_states, value_states, W, eps=1e-6, p_round=True, y_round=True)
 
 
@@ -207,9 +209,13 @@ class DropKVCache(_LayerCache):
         fast = self._fast_path_ok(query_states, key_states, value_states)
         W = self.window_size if fast else min(self.window_size, query_states.shape[2])
         keep = self._keep_length(seq_len, total_tokens, max_keep_len)
-        _, key_c, value_c = ops.evict(query_states, key_states, value_states, W, self.kernel_size, keep,
-                                      protect_window=min(self.window_size, seq_len), eps=1e-6, p_round=True,
-                                      y_round=not fast)
+        protect = min(self.window_size, seq_len)
+        if torch_ops.compiling():
+            _, key_c, value_c = torch.ops.dropkv.evict(query_states, key_states, value_states, W, self.kernel_size,
+                                                       keep, protect, 1e-6, True, not fast, 0)
+        else:
+            _, key_c, value_c = ops.evict(query_states, key_states, value_states, W, self.kernel_size, keep,
+                                          protect_window=protect, eps=1e-6, p_round=True, y_round=not fast)
         return key_c, value_c
 
     @staticmethod

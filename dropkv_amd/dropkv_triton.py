@@ -15,7 +15,7 @@ import math
 
 import torch
 
-from . import ops
+from . import ops, torch_ops
 
 
 def _next_power_of_2(n: int) -> int:
@@ -98,4 +98,6 @@ def dropkv_scores_triton(
     operand split into two bf16/fp16 terms, which is at least as accurate.
     """
     check_scoring_inputs(Q, K, V, window_size)
+    if torch_ops.compiling():
+        return torch.ops.dropkv.scores(Q, K, V, window_size, eps, match_pytorch_precision, False, 0)
     return ops.scores(Q, K, V, window_size, eps=eps, p_round=match_pytorch_precision, y_round=False)

@@ -28,7 +28,7 @@ from typing import Any, Optional
 import torch
 from transformers.cache_utils import Cache, DynamicLayer
 
-from . import ops
+from . import ops, torch_ops
 from .dropkv_triton import check_scoring_inputs
 from .hf_query import query_capture, take_captured_query
 
@@ -61,6 +61,9 @@ def _evict(query_states: torch.Tensor, key_states: torch.Tensor, value_states: t
         except AssertionError:
             fast = False
     W = window_size if fast else min(window_size, query_states.shape[2])
+    if torch_ops.compiling():
+        return torch.ops.dropkv.evict(query_states, key_states, value_states, W, kernel_size, keep, window_size,
+                                      1e-6, True, not fast, 0)
     return ops.evict(query_states, key_states, value_states, W, kernel_size, keep, protect_window=window_size,
                      p_round=True, y_round=not fast)
 
