@@ -41,6 +41,21 @@ def test_select_ties_and_plateaus(gpu):
     _select_case(gpu, torch.zeros(1, 2, 3000), 11, 8, 300)
 
 
+def test_select_threshold_bin_beyond_lds(gpu):
+    """More than 4096 keys share the threshold's top-digit bin (here: the
+    threshold's exact value), so the threshold stage resolves its digits by
+    sweeping the row instead of from its LDS candidate list; the lowest
+    indices among the tied keys must still win, across chunks and sweep
+    rounds."""
+    g = torch.Generator().manual_seed(2)
+    scores = torch.randint(0, 3, (1, 3, 40000), generator=g).float()
+    _select_case(gpu, scores, 1, 8, 15000)
+    _select_case(gpu, scores, 11, 8, 39000)
+    near = 1.0 + torch.randint(0, 2048, (1, 2, 70000), generator=g).float() * 2.0 ** -20  # one top-digit bin
+    _select_case(gpu, near, 1, 8, 9000)
+    _select_case(gpu, near, 11, 8, 30000)
+
+
 def test_select_big_absorbed(gpu):
     """max >= 2^24: max + 1.0f == max, the protected tail ties with the maximum
     (dropkv_cache.py:465-467 semantics in fp32)."""
