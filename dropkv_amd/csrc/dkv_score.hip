@@ -79,14 +79,6 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
         s[kb][mb][r] = x;
         tmax = fmaxf(tmax, x);
       }
-#if defined(DKV_EXP_CAND) && DKV_EXP_CAND == 2
-    {
-      const bool up = tmax > lmax[mb];
-      lmax[mb] = up ? tmax : lmax[mb];
-      larg[mb] = up ? t0 + 4 * lg : larg[mb];
-    }
-#elif defined(DKV_EXP_CAND) && DKV_EXP_CAND == 0
-#else
     {
       // The lane's own maximum so far and the lowest of its keys holding it
       // (key t0 + 16 kb + 4 lg + r; scanned downwards so the lowest wins).
@@ -99,7 +91,6 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
       lmax[mb] = up ? tmax : lmax[mb];
       larg[mb] = up ? t0 + 4 * lg + off : larg[mb];
     }
-#endif
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const float mnew = fmaxf(m2[mb], tmax);
