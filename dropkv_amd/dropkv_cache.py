@@ -178,6 +178,8 @@ class DropKVCache(_LayerCache):
 
         keep_len = self._keep_length(seq_len, total_tokens, max_keep_len)
         protect = min(self.window_size, seq_len)
+        if torch_ops.compiling():
+            return torch.ops.dropkv.select(scores, self.kernel_size, protect, keep_len)[0]
         return ops.select(scores, self.kernel_size, protect, keep_len)
 
     def _fast_path_ok(self, query_states, key_states, value_states) -> bool:
@@ -222,6 +224,8 @@ class DropKVCache(_LayerCache):
     def _gather_compressed(key_states: torch.Tensor, value_states: torch.Tensor,
                            keep_idx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """Gather the retained rows (dropkv_cache.py:479-491), bit-exact."""
+        if torch_ops.compiling():
+            return torch.ops.dropkv.compact(key_states, value_states, keep_idx)
         return ops.compact(key_states, value_states, keep_idx)
 
     def update(self, query_states: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,

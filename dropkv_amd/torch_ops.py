@@ -8,12 +8,17 @@ instead of breaking the graph at the ctypes call:
 * ``torch.ops.dropkv.scores(q, k, v, window, eps, p_round, y_round, splits)``
   -> scores ``[B, Hkv, Lk]`` float32 (``dropkv_scores`` in the C ABI; the
   scoring of ``dropkv_scores_triton``, dropkv_triton.py:643-828);
+* ``torch.ops.dropkv.select(scores, kernel_size, window, keep)`` ->
+  ``(keep_idx [..., keep] int64 ascending, pooled)`` (``dropkv_select``: pool,
+  protect, top-k, sort, dropkv_cache.py:464-475);
+* ``torch.ops.dropkv.compact(k, v, keep_idx)`` -> ``(k_out, v_out)``
+  (``dropkv_compact``: ``_gather_compressed``, dropkv_cache.py:479-491);
 * ``torch.ops.dropkv.evict(q, k, v, window, kernel_size, keep, protect_window,
   eps, p_round, y_round, splits)`` -> ``(keep_idx [B, Hkv, keep] int64,
   k_out, v_out [B, Hkv, keep, D])`` (``dropkv_evict``: ``_compute_keep_indices``
-  then ``_gather_compressed``, dropkv_cache.py:355-491).
+  then ``_gather_compressed``, dropkv_cache.py:355-491, in one call).
 
-Both return fresh tensors.  ``dropkv_scores_triton`` and ``DropKVCache`` call
+All return fresh tensors.  ``dropkv_scores_triton`` and ``DropKVCache`` call
 them while ``torch.compile`` traces, and the ctypes wrappers of
 :mod:`dropkv_amd.ops` otherwise (no dispatcher overhead in eager code).
 """
@@ -52,6 +57,31 @@ def _evict_fake(q, k, v, window, kernel_size, keep, protect_window, eps=1e-6, p_
     B, Hkv, _, D = k.shape
     idx = q.new_empty((B, Hkv, keep), dtype=torch.int64)
     return idx, k.new_empty((B, Hkv, keep, D)), v.new_empty((B, Hkv, keep, D))
+
+
+@torch.library.custom_op("dropkv::select", mutates_args=())
+def select(scores: torch.Tensor, kernel_size: int, window: int, keep: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    idx, pooled = ops.select(scores, kernel_size, window, keep, return_pooled=True)
+    return idx, pooled
+
+
+@select.register_fake
+def _select_fake(scores, kernel_size, window, keep):
+    torch._check(scores.dtype == torch.float32)
+    return scores.new_empty((*scores.shape[:-1], keep), dtype=torch.int64), torch.empty_like(scores)
+
+
+@torch.library.custom_op("dropkv::compact", mutates_args=())
+def compact(k: torch.Tensor, v: torch.Tensor, keep_idx: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    return ops.compact(k, v, keep_idx)
+
+
+@compact.register_fake
+def _compact_fake(k, v, keep_idx):
+    torch._check(k.dim() == 4 and v.shape == k.shape and keep_idx.dim() == 3)
+    B, H, _, D = k.shape
+    keep = keep_idx.shape[-1]
+    return k.new_empty((B, H, keep, D)), v.new_empty((B, H, keep, D))
 
 
 def compiling() -> bool:

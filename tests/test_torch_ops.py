@@ -30,6 +30,10 @@ def test_fake_shapes_on_meta():
     idx, ko, vo = torch.ops.dropkv.evict(q, k, v, 8, 11, 100, 8)
     assert idx.shape == (1, 2, 100) and idx.dtype == torch.int64
     assert ko.shape == vo.shape == (1, 2, 100, 128) and ko.dtype == torch.bfloat16
+    sidx, pooled = torch.ops.dropkv.select(s, 11, 8, 100)
+    assert sidx.shape == (1, 2, 100) and sidx.dtype == torch.int64 and pooled.shape == s.shape
+    ck, cv = torch.ops.dropkv.compact(k, v, sidx)
+    assert ck.shape == cv.shape == (1, 2, 100, 128)
 
 
 def test_full_graph_trace_on_meta():
@@ -41,6 +45,25 @@ def test_full_graph_trace_on_meta():
     q, k, v = _meta_qkv()
     explanation = torch._dynamo.explain(fn)(q, k, v)
     assert explanation.graph_break_count == 0 and explanation.graph_count == 1
+
+
+@pytest.mark.gpu
+def test_operators_match_ops(gpu):
+    """Each operator returns what the ctypes wrapper returns, bit for bit."""
+    from dropkv_amd import ops
+    Q, K, V = make_qkv(dict(B=1, Hq=8, Hkv=2, D=128), 128, 2048, seed=5)
+    Q, K, V = Q.to(gpu), K.to(gpu), V.to(gpu)
+    s = torch.ops.dropkv.scores(Q, K, V, 8)
+    assert torch.equal(s, ops.scores(Q, K, V, 8))
+    idx, pooled = torch.ops.dropkv.select(s, 11, 8, 204)
+    ridx, rpooled = ops.select(s, 11, 8, 204, return_pooled=True)
+    assert torch.equal(idx, ridx) and torch.equal(pooled, rpooled)
+    ko, vo = torch.ops.dropkv.compact(K, V, idx)
+    rk, rv = ops.compact(K, V, idx)
+    assert torch.equal(ko, rk) and torch.equal(vo, rv)
+    e = torch.ops.dropkv.evict(Q, K, V, 8, 11, 204, 8)
+    r = ops.evict(Q, K, V, 8, 11, 204, protect_window=8)
+    assert all(torch.equal(a, b) for a, b in zip(e, r))
 
 
 @pytest.mark.gpu
