@@ -91,8 +91,7 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
       lmax[mb] = up ? tmax : lmax[mb];
       larg[mb] = up ? t0 + 4 * lg + off : larg[mb];
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    tmax = max_xor32(max_xor16(tmax));
     const float mnew = fmaxf(m2[mb], tmax);
     const bool empty = mnew == -INFINITY;
     const float alpha = empty ? 1.f : __builtin_amdgcn_exp2f(m2[mb] - mnew);
@@ -400,8 +399,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   // Row sums are per lane-group partials; fold the four groups.
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
-    lsum[mb] += __shfl_xor(lsum[mb], 16);
-    lsum[mb] += __shfl_xor(lsum[mb], 32);
+    lsum[mb] = add_xor32(add_xor16(lsum[mb]));
   }
 
   // Cross-wave merge in LDS (the V tiles are dead now): every wave stores
@@ -683,8 +681,7 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
   static_assert(kCand == 4, "one candidate per lane group");
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
-    lsum[mb] += __shfl_xor(lsum[mb], 16);
-    lsum[mb] += __shfl_xor(lsum[mb], 32);
+    lsum[mb] = add_xor32(add_xor16(lsum[mb]));
   }
   const int64_t slot = ((int64_t)head * n_mc + mc) * n_splits + split;
 #pragma unroll
@@ -1108,8 +1105,7 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
         float part = 0.f;
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) part = sumsq8<T>(vop[kb][kk], part);
-        part += __shfl_xor(part, 16);
-        part += __shfl_xor(part, 32);
+        part = add_xor32(add_xor16(part));
 #pragma unroll
         for (int r = 0; r < 4; ++r) vn2[kb][r] = __shfl(part, 4 * lg + r);
       }
@@ -1214,7 +1210,9 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
 
       // Sum over the 16 query rows held by lanes li = 0..15 as a
       // reduce-scatter: afterwards lane li holds the total of key r = li/4
-      // (for li % 4 == 0), so each key is stored by one lane.
+      // (for li % 4 == 0), so each key is stored by one lane.  (Lane
+      // shuffles here: the DPP form pass2w_kernel uses measured ~0.2 us
+      // slower at C2, where the shuffles' latency overlaps other waves.)
       const bool h8 = li & 8, h4 = li & 4;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
@@ -1460,19 +1458,21 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
       epilogue(std::true_type{});
     else
       epilogue(std::false_type{});
-    // Sum over the 16 rows of lanes li = 0..15 (reduce-scatter): lane li
+    // Sum over the 16 rows of lanes li = 0..15, a reduce-scatter on DPP
+    // (partners 15 - li, then 7 - li within each half, then li ^ 2 and
+    // li ^ 1: each step pairs lanes that keep complementary keys): lane li
     // with li % 4 == 0 then holds key 16kb + 4lg + li/4.
     const bool h8 = li & 8, h4 = li & 4;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       float k0 = h8 ? sc[kb][2] : sc[kb][0];
       float k1 = h8 ? sc[kb][3] : sc[kb][1];
-      k0 += __shfl_xor(h8 ? sc[kb][0] : sc[kb][2], 8);
-      k1 += __shfl_xor(h8 ? sc[kb][1] : sc[kb][3], 8);
+      k0 += dpp_f<kDppMirror>(h8 ? sc[kb][0] : sc[kb][2]);
+      k1 += dpp_f<kDppMirror>(h8 ? sc[kb][1] : sc[kb][3]);
       float v = h4 ? k1 : k0;
-      v += __shfl_xor(h4 ? k0 : k1, 4);
-      v += __shfl_xor(v, 2);
-      v += __shfl_xor(v, 1);
+      v += dpp_f<kDppHalfMirror>(h4 ? k0 : k1);
+      v += dpp_f<kDppQuadSwap2>(v);
+      v += dpp_f<kDppQuadSwap1>(v);
       if ((li & 3) == 0) red[par][wv][gt * kTile + 16 * kb + 4 * lg + (li >> 2)] = v;
     }
   };
