@@ -57,6 +57,7 @@ _SIGNATURES = {
                                  _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp, _c_size, _c_vp]),
     "dropkv_append": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "dropkv_set_resident": (_c_int, [_c_int, _c_i64]),
     "dropkv_timing_enable": (_c_int, [_c_int]),
     "dropkv_timing_read": (_c_int, [ctypes.POINTER(ctypes.c_double), _c_int]),
     "dropkv_selftest_mfma": (_c_int, [_c_vp, _c_vp]),
@@ -71,6 +72,10 @@ EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 # Size of the static per-GPU scratch of dropkv_evict_noalloc
 # (DROPKV_NOALLOC_SCRATCH_BYTES in include/dropkv_amd.h).
 NOALLOC_SCRATCH_BYTES = 32 << 20
+
+# Leading bytes of a dropkv_evict workspace that must be zero when the
+# workspace is first used (DROPKV_SYNC_BYTES in include/dropkv_amd.h).
+SYNC_BYTES = 4096
 
 _lib = None
 _lock = threading.Lock()

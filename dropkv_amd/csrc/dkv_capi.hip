@@ -119,6 +119,12 @@ int dropkv_scores(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64
   if (!workspace || workspace_bytes < p.total)
     return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", p.total, workspace_bytes);
   timing_start(static_cast<hipStream_t>(stream));
+  int rs = 0, rkpw = 0;
+  if (!dkv::scores_generic(dtype, D, p.M) && dkv::resident_plan(dtype, D, p.M, B * Hkv, Lk, splits, &rs, &rkpw))
+    return hip_status(dkv::launch_resident(p, dtype, rs, rkpw, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Lk, (int)Hkv,
+                                           (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, scores,
+                                           static_cast<char*>(workspace), nullptr, static_cast<hipStream_t>(stream)),
+                      "dropkv_scores launch");
   return hip_status(dkv::launch_scores(p, dtype, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Lk,
                                        (int)Hkv, (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, scores,
                                        static_cast<char*>(workspace), nullptr, 0, nullptr,
@@ -250,19 +256,31 @@ static int evict_impl(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, i
     return fail(DROPKV_E_UNSUPPORTED, "outputs with a row capacity need 16-byte aligned rows");
   timing_start(st);
   const dkv::SelectCompact cp{k, v, Hkv * kv_ld * D, kv_ld * D, D, eb, D, (int)Hkv, k_out, v_out, out_ld};
+  // The resident kernel (pass 1, merge and pass 2 in one, K/V streamed
+  // once) when the call fits on chip; otherwise the streaming passes.
   // Pooling runs in the tail of the scoring pass when the plan allows it
   // (the matrix-core kernels only); otherwise as the standalone selection's
   // pool kernel.
-  const bool fused = !dkv::scores_generic(dtype, D, p.M) && dkv::select_after_pool_ok(p.s2, p.kps2, Lk, kernel_size);
+  const bool mfma = !dkv::scores_generic(dtype, D, p.M);
+  int rs = 0, rkpw = 0;
+  const bool resident = mfma && dkv::resident_plan(dtype, D, p.M, B * Hkv, Lk, splits, &rs, &rkpw) &&
+                        dkv::select_after_pool_ok(rs, rkpw, Lk, kernel_size);
+  const bool fused = resident || (mfma && dkv::select_after_pool_ok(p.s2, p.kps2, Lk, kernel_size));
   const dkv::FuseSelect fs{sel_ws, (int)kernel_size, (int)protect_window};
-  hipError_t e = dkv::launch_scores(p, dtype, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)kv_ld,
-                                    (int)Hkv, (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc,
-                                    ws, reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv),
-                                    fused ? &fs : nullptr, st);
+  hipError_t e;
+  if (resident)
+    e = dkv::launch_resident(p, dtype, rs, rkpw, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)kv_ld, (int)Hkv, (int)Lq,
+                             (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws, &fs, st);
+  else
+    e = dkv::launch_scores(p, dtype, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)kv_ld, (int)Hkv, (int)Lq,
+                           (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws,
+                           reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv),
+                           fused ? &fs : nullptr, st);
   if (e != hipSuccess) return hip_status(e, "dropkv_evict scores");
   if (fused)
     e = dkv::launch_select_after_pool(sc, (int)(B * Hkv), (int)Lk, (int)kernel_size, (int)protect_window, (int)keep,
-                                      p.s2, p.kps2, keep_idx, nullptr, sel_ws, vec ? &cp : nullptr, st);
+                                      resident ? rs : p.s2, resident ? rkpw : p.kps2, keep_idx, nullptr, sel_ws,
+                                      vec ? &cp : nullptr, st);
   else
     e = dkv::launch_select(sc, (int)(B * Hkv), (int)Lk, (int)kernel_size, (int)protect_window, (int)keep, keep_idx,
                            nullptr, sel_ws, true, vec ? &cp : nullptr, st);
@@ -372,6 +390,15 @@ int dropkv_append(const void* k, const void* v, int64_t s_b, int64_t s_h, int64_
   return hip_status(dkv::launch_append(k, v, s_b, s_h, s_l, elem_bytes, B, H, L, D, k_dst, v_dst, dst_ld, row0,
                                        static_cast<hipStream_t>(stream)),
                     "dropkv_append launch");
+}
+
+static_assert(DROPKV_SYNC_BYTES == dkv::kResSyncBytes, "the header's sync area is the plan's");
+
+int dropkv_set_resident(int mode, int64_t spin_polls) {
+  if (mode != 0 && mode != 1) return fail(DROPKV_E_ARG, "mode must be 0 or 1");
+  if (spin_polls > INT32_MAX) return fail(DROPKV_E_ARG, "spin_polls too large");
+  dkv::set_resident(mode, spin_polls < 0 ? -1 : (int)spin_polls);
+  return DROPKV_OK;
 }
 
 int dropkv_timing_enable(int on) {

@@ -51,7 +51,7 @@ struct ScorePlan {
   int s2, kps2;  // pass 2: splits per head, keys per split
   int p1_waves, p2_waves;  // launch shapes
   int p1_wide;                     // pass 1 with all row-chunks of a head in one workgroup
-  size_t off_ml, off_y, off_cand, off_op, off_stb, off_stat, off_yf, total;
+  size_t off_sync, off_ml, off_y, off_cand, off_op, off_stb, off_stat, off_yf, total;
 };
 
 ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W, int64_t splits);
@@ -68,6 +68,25 @@ hipError_t launch_scores(const ScorePlan& p, int dtype, int D, const void* q, in
                          int64_t q_ss, int64_t q_sd, const void* k, const void* v, int kv_ld, int Hkv, int Lq,
                          int Lk, int W, float eps, int p_round, int y_round, float* scores, char* ws,
                          uint32_t* zero_ptr, int64_t zero_words, const FuseSelect* fuse, hipStream_t st);
+// The resident layer-call (dkv_resident.hip): pass 1, merge and pass 2 in one
+// kernel that keeps V and the logits on chip, for calls that fit (D = 128,
+// one row-chunk, bf16/fp16, at most kResKeys keys per workgroup and one
+// workgroup per CU).  resident_plan gives its split geometry (S workgroups
+// of kpw keys per head) or false; its counters live in the first
+// kResSyncBytes of the score workspace (ScorePlan::off_sync), which must be
+// zero when a workspace is first used and are zero again after every call.
+constexpr int kResKeys = 1024;
+constexpr int kResMaxHeads = 256;
+constexpr size_t kResSyncBytes = (size_t)kResMaxHeads * 16;
+bool resident_plan(int dtype, int64_t D, int64_t M, int64_t heads, int64_t Lk, int64_t splits, int* S, int* kpw);
+hipError_t launch_resident(const ScorePlan& p, int dtype, int S, int kpw, const void* q, int64_t q_sb,
+                           int64_t q_sh, int64_t q_ss, int64_t q_sd, const void* k, const void* v, int kv_ld,
+                           int Hkv, int Lq, int Lk, int W, float eps, int p_round, int y_round, float* scores,
+                           char* ws, const FuseSelect* fuse, hipStream_t st);
+// mode 0: never take the resident path, 1: whenever the call fits; spin1 >= 0
+// sets the polls a workgroup waits at its first barrier before it leaves the
+// head to the last one to arrive (tests use 0 to force that path).
+void set_resident(int mode, int spin1);
 hipError_t launch_debug_state(const ScorePlan& p, const char* ws, int D, float* lse_out, float* y_out,
                               hipStream_t st);
 // The generic scoring kernels (fp32 arithmetic on the vector ALUs) on the

@@ -26,9 +26,17 @@ def _workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
 
 
+def _evict_workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
+    """A new ``dropkv_scores`` / ``dropkv_evict`` workspace: its leading
+    counters (_lib.SYNC_BYTES) start at zero, and every call leaves them zero."""
+    ws = _workspace(nbytes, dev)
+    ws[: _lib.SYNC_BYTES].zero_()
+    return ws
+
+
 # One workspace per (device, stream), grown on demand and reused by every
-# ``evict`` call on that stream: calls on one stream run in order, so they
-# never use it at the same time.
+# ``scores`` / ``evict`` call on that stream: calls on one stream run in
+# order, so they never use it at the same time.
 _shared_ws: dict = {}
 _shared_ws_lock = threading.Lock()
 
@@ -37,12 +45,12 @@ def _stream_workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
     nbytes = max(int(nbytes), 1)
     stream = torch.cuda.current_stream(dev)
     if torch.cuda.is_current_stream_capturing():
-        return _workspace(nbytes, dev)  # a graph keeps its own (private-pool) workspace
+        return _evict_workspace(nbytes, dev)  # a graph keeps its own (private-pool) workspace
     key = (dev.index, stream.cuda_stream)
     with _shared_ws_lock:
         ws = _shared_ws.get(key)
         if ws is None or ws.numel() < nbytes:
-            ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            ws = _evict_workspace(nbytes, dev)
             _shared_ws[key] = ws
     return ws
 
@@ -81,7 +89,7 @@ def scores(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, window: int, eps: 
     V = _kv_operand(V)
     lib = _lib.load()
     ws_bytes = lib.dropkv_scores_workspace_bytes(B, Hq, Hkv, Lk, D, window, splits)
-    ws = _workspace(ws_bytes, dev)
+    ws = _evict_workspace(ws_bytes, dev) if return_workspace else _stream_workspace(ws_bytes, dev)
     out = torch.empty(B, Hkv, Lk, dtype=torch.float32, device=dev)
     rc = lib.dropkv_scores(Q.data_ptr(), *Q.stride(), K.data_ptr(), V.data_ptr(), _DTYPE_CODE[Q.dtype],
                            B, Hq, Hkv, Lq, Lk, D, window, float(eps), int(bool(p_round)), int(bool(y_round)),
@@ -214,7 +222,7 @@ def evict_ld(Q: torch.Tensor, k_buf: torch.Tensor, v_buf: torch.Tensor, Lk: int,
     B, Hq, Lq, D = Q.shape
     Hkv = k_buf.shape[1]
     lib = _lib.load()
-    ws = _workspace(lib.dropkv_evict_workspace_bytes(B, Hq, Hkv, Lk, D, window, 0), dev)
+    ws = _stream_workspace(lib.dropkv_evict_workspace_bytes(B, Hq, Hkv, Lk, D, window, 0), dev)
     idx = torch.empty(B, Hkv, keep, dtype=torch.int64, device=dev)
     pw = window if protect_window is None else protect_window
     rc = lib.dropkv_evict_ld(Q.data_ptr(), *Q.stride(), k_buf.data_ptr(), v_buf.data_ptr(), k_buf.shape[2],
@@ -257,6 +265,14 @@ def evict(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, window: int, kernel
     return idx, ko, vo
 
 
+def set_resident(enabled: bool = True, spin_polls: int = -1) -> None:
+    """``dropkv_set_resident``: whether layer-calls that fit on chip score in
+    the one resident kernel (off by default), and the polls a workgroup waits at its
+    first barrier before it leaves its KV head to the last one to arrive
+    (``spin_polls`` < 0: unchanged; 0 forces that path)."""
+    _lib.check(_lib.load().dropkv_set_resident(int(bool(enabled)), int(spin_polls)), "dropkv_set_resident")
+
+
 class EvictPlan:
     """Pre-sized workspace and outputs for repeated layer-calls of one shape
     (``dropkv_evict``); avoids per-call allocation in tight loops."""
@@ -273,7 +289,7 @@ class EvictPlan:
         self.protect_window = int(window if protect_window is None else protect_window)
         self.eps, self.p_round, self.y_round, self.splits = float(eps), int(p_round), int(y_round), int(splits)
         lib = _lib.load()
-        self.ws = _workspace(lib.dropkv_evict_workspace_bytes(B, Hq, Hkv, Lk, D, window, splits), dev)
+        self.ws = _evict_workspace(lib.dropkv_evict_workspace_bytes(B, Hq, Hkv, Lk, D, window, splits), dev)
         self.scores = torch.empty(B, Hkv, Lk, dtype=torch.float32, device=dev) if keep_scores else None
         self.keep_idx = torch.empty(B, Hkv, keep, dtype=torch.int64, device=dev)
         self.k_out = torch.empty(B, Hkv, keep, D, dtype=Q.dtype, device=dev)

@@ -68,6 +68,8 @@ int dropkv_supported_head_dims(int64_t* out, int cap);
  *   splits 0 = automatic split-K depth over keys, otherwise that many splits
  *          per (b, hkv, row-chunk)
  * Requires Hq % Hkv == 0, 1 <= W <= Lq <= Lk, 1 <= D <= 512.
+ * The first DROPKV_SYNC_BYTES of the workspace must be zero when a workspace
+ * is first used; every call leaves them zero (see dropkv_evict).
  * ------------------------------------------------------------------------ */
 size_t dropkv_scores_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk,
                                      int64_t D, int64_t W, int64_t splits);
@@ -134,8 +136,17 @@ int dropkv_compact2(const void* k0, const void* v0, int64_t s0_b, int64_t s0_h, 
  * deployed path).  `scores` may be NULL (then it lives in the workspace).
  * Pooling and the top-k threshold run in the tail of the scoring kernel
  * whenever the plan allows it (three kernels per call), otherwise as the
- * standalone selection kernels.
+ * standalone selection kernels.  Calls that fit on chip (D = 128, g*W <= 32,
+ * bf16/fp16, splits = 0, B*Hkv*ceil(Lk/1024) no more than the device's CUs)
+ * can score in one kernel that streams K/V once (dropkv_set_resident).
+ *
+ * The first DROPKV_SYNC_BYTES of the workspace hold that kernel's barrier
+ * counters: they must be zero when a workspace is first used (fill a new
+ * workspace with zeros), and every call leaves them zero.  The rest of the
+ * workspace needs no initialisation.  Calls that share a workspace must be
+ * serialised (one stream), as for every workspace here.
  * ------------------------------------------------------------------------ */
+#define DROPKV_SYNC_BYTES 4096
 size_t dropkv_evict_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk,
                                     int64_t D, int64_t W, int64_t splits);
 
@@ -163,8 +174,10 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
  * keys; the B4 Hq64 Hkv8 128K-key stress shape needs 77 MiB and is refused.
  * Every call on one GPU uses the same scratch and leaves its contents
  * behind: calls that overlap on one GPU (two streams, or two threads) race
- * and must be serialised by the caller.  No part of the scratch needs to be
- * zero on entry.  Arguments and results are those of dropkv_evict.
+ * and must be serialised by the caller.  The caller initialises nothing (the
+ * counters at the start of the scratch are zero when the library is loaded
+ * and every call leaves them zero).  Arguments and results are those of
+ * dropkv_evict.
  * ------------------------------------------------------------------------ */
 #define DROPKV_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 
@@ -206,6 +219,20 @@ int dropkv_evict_ld(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int
                     int64_t kernel_size, int64_t protect_window, int64_t keep,
                     float* scores, int64_t* keep_idx, void* k_out, void* v_out, int64_t out_ld,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * The one-kernel (resident) scoring of dropkv_evict / dropkv_evict_ld /
+ * dropkv_evict_noalloc (no counterpart in the reference, whose Triton path
+ * always launches its kernels in sequence).  mode 1 takes it for every call
+ * that fits; mode 0 (the default) never does.  Its workgroups wait for one
+ * another twice per call; a workgroup that has waited spin_polls polls at
+ * the first wait (spin_polls < 0: unchanged; default 65536, a few tens of
+ * milliseconds) leaves its KV head to the last workgroup of the head to
+ * arrive, which finishes that head alone with the same results.  That only
+ * happens when other work holds CUs; spin_polls = 0 forces it (tests).
+ * Process-wide; not synchronised with calls in flight.
+ * ------------------------------------------------------------------------ */
+int dropkv_set_resident(int mode, int64_t spin_polls);
 
 /* Kernel timing with HIP events (no counterpart in the reference, which has
  * no timers).  dropkv_timing_enable(1) makes every later dropkv_scores /
