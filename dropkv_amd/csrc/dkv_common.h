@@ -102,6 +102,21 @@ __device__ __forceinline__ V bitcast_u4(u32x4 x) {
   return __builtin_bit_cast(V, x);
 }
 
+// Stores that are coherent across the whole device when they complete
+// (agent-scope relaxed atomic stores: write-through to the memory-side
+// cache), for data that workgroups on other XCDs read within the same
+// kernel after a counter handshake.  A release then needs only the wait for
+// the stores, not a write-back of the XCD's L2.
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Order-preserving map float -> uint32 (larger float => larger key).
 // -0.0 is folded onto +0.0 so that the two compare equal, as in torch.
 __device__ __forceinline__ uint32_t float_key(float f) {

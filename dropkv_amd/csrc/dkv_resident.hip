@@ -26,9 +26,12 @@
 // resolve stage, as after pass 2.
 //
 // Barriers: per head, counters in the caller's workspace (zero on entry,
-// zero again when the call ends).  A workgroup publishes with an agent-scope
-// release and an atomic add; the others poll with agent-scope atomic loads
-// and acquire.  Every workgroup of the grid is resident at once when the
+// zero again when the call ends).  What a workgroup publishes (its partial,
+// its merged rows, the cleared selection words) it writes with
+// device-coherent stores (st_dev), waits for them and adds its arrival; the
+// others poll with agent-scope atomic loads and acquire.  (An agent-scope
+// release fence would write back the XCD's whole L2 instead; those
+// write-backs queue up per XCD and cost 2-8 us per barrier.)  Every workgroup of the grid is resident at once when the
 // GPU runs nothing else (one workgroup per CU, grid <= CUs), but nothing
 // guarantees it: a workgroup that waits at barrier 1 longer than `spin1`
 // polls marks the head abandoned (a flag bit in the counter, set by
@@ -78,12 +81,13 @@ __device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Every wave's global stores done, then one agent-scope release by thread 0
-// (the caller adds its arrival right after).
+// Every wave's device-coherent stores complete (the caller adds its arrival
+// right after).  On the other side one acquire by thread 0 followed by a
+// workgroup barrier covers the workgroup's later loads (the fence
+// invalidates the CU's and the XCD's caches, which every wave shares).
 __device__ __forceinline__ void publish() {
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (threadIdx.x == 0) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
 }
 
 // Thread 0 at barrier 1: arrival, then the wait (see the file comment).
@@ -240,6 +244,131 @@ __device__ __forceinline__ void score_tile(const f32x4 (&sacc)[2][kMB], const ty
   }
 }
 
+// Two tiles of the score pass at once (tiles u = 0, 1 starting at keys
+// t0[u]), in one basic block so that their dependency chains interleave: with
+// one wave per SIMD nothing else hides the latencies.  The operands are read
+// from LDS once for both.  kMasked: the causal bound and the rows' dominant
+// keys are applied (chosen for the pair by the caller).  Keys at or past
+// k_end are computed but not stored.
+template <typename T, bool PR, bool kMasked>
+__device__ __forceinline__ void score_pair(const f32x4 (&sacc)[2][2][kMB],
+                                           const typename Elem<T>::v8 (&vA)[2][kResD / 32],
+                                           const typename Elem<T>::v8 (&vB)[2][kResD / 32], const u32x4* opnd,
+                                           const float* stat, const int (&t0)[2], int k_begin, int k_end, int M,
+                                           int W, int Lk, float scale_log2, float eps, float out_scale,
+                                           float* __restrict__ srow, float* sc) {
+  typedef typename Elem<T>::v8 v8;
+  constexpr int KK = kResD / 32;
+  const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  auto both = [&](auto&& f) __attribute__((always_inline)) {
+    f(std::integral_constant<int, 0>{});
+    f(std::integral_constant<int, 1>{});
+  };
+  auto vop = [&](auto uc, int kb, int kk) __attribute__((always_inline)) -> v8 {
+    if constexpr (decltype(uc)::value == 0)
+      return vA[kb][kk];
+    else
+      return vB[kb][kk];
+  };
+  const float* cst = stat + li;
+  float vn2[2][2][4];
+  both([&](auto uc) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float part = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) part = sumsq8<T>(vop(uc, kb, kk), part);
+      part = add_xor32(add_xor16(part));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vn2[u][kb][r] = __shfl(part, 4 * lg + r);
+    }
+  });
+  f32x4 gacc[2][2][kMB];
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    const float nyh = -0.5f * cst[mb * kStatWords + 16];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) gacc[u][kb][mb][r] = fmaf(vn2[u][kb][r], -0.5f, nyh);
+  }
+  const u32x4* ob = opnd + lane;
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const v8 yh = __builtin_bit_cast(v8, ob[(size_t)((1 * kMB + mb) * KK + kk) * 64]);
+      const v8 yl = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
+      both([&](auto uc) __attribute__((always_inline)) {
+        constexpr int u = decltype(uc)::value;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          gacc[u][kb][mb] = Elem<T>::mfma(vop(uc, kb, kk), yh, gacc[u][kb][mb]);
+          gacc[u][kb][mb] = Elem<T>::mfma(vop(uc, kb, kk), yl, gacc[u][kb][mb]);
+        }
+      });
+    }
+  float sc2[2][2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc2[u][kb][r] = 0.f;
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb) {
+    const int m = mb * 16 + li;
+    const int bound = kMasked ? row_bound(m, M, W, Lk) : 0;
+    const int skey = kMasked ? __builtin_bit_cast(int, cst[mb * kStatWords + 32]) : -1;
+    const float snd2 = kMasked ? cst[mb * kStatWords + 48] : 0.f;
+    const float lse2 = cst[mb * kStatWords];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+          float p[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            p[e] = __builtin_amdgcn_exp2f(sacc[u][kb][mb][r + e] * scale_log2 - lse2);
+            if (kMasked) p[e] = (t0[u] + 16 * kb + 4 * lg + r + e) <= bound ? p[e] : 0.f;
+            p[e] = min_one_nonneg(p[e]);
+          }
+          if (PR) round_through2<T>(p[0], p[1]);
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float ratio = p[e] * __builtin_amdgcn_rcpf(1.0f - p[e] + eps);
+            float nd2 = min_zero(gacc[u][kb][mb][r + e]);  // -dist2/2, dist2 clamped at 0
+            if (kMasked) nd2 = (t0[u] + 16 * kb + 4 * lg + r + e) == skey ? snd2 : nd2;
+            sc2[u][kb][r + e] = fmaf(ratio * ratio, nd2, sc2[u][kb][r + e]);
+          }
+        }
+  }
+  const bool h8 = li & 8, h4 = li & 4;
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float k0 = h8 ? sc2[u][kb][2] : sc2[u][kb][0];
+      float k1 = h8 ? sc2[u][kb][3] : sc2[u][kb][1];
+      k0 += __shfl_xor(h8 ? sc2[u][kb][0] : sc2[u][kb][2], 8);
+      k1 += __shfl_xor(h8 ? sc2[u][kb][1] : sc2[u][kb][3], 8);
+      float v = h4 ? k1 : k0;
+      v += __shfl_xor(h4 ? k0 : k1, 4);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 1);
+      const int n = t0[u] + 16 * kb + 4 * lg + (li >> 2);
+      if ((li & 3) == 0 && n < k_end) {
+        srow[n] = v * out_scale;
+        if (sc) sc[n - k_begin] = v * out_scale;
+      }
+    }
+}
+
 // Operand block and statistics of `head` (written by merge_row) into LDS.
 __device__ __forceinline__ void stage_operands(const ResArgs& a, int head, u32x4* opnd, float* stat) {
   const u32x4* gop = a.opblk + (size_t)head * kResOps * 64;
@@ -268,11 +397,12 @@ __device__ void finish_alone(const ResArgs& a, int head, unsigned char* lds) {
   const T* kp = static_cast<const T*>(a.k);
   const int heads_rows = (int)(gridDim.x / a.S) * kRows;  // every head's padded rows
   for (int r = wv; r < kRows; r += kResWaves)
-    merge_row<T, D>(head * kRows + r, a.part_ml, a.part_y, a.part_cand, 1, a.S, a.M, heads_rows, a.p_round,
-                    a.y_round, q, a.q_sb, a.q_sh, a.q_ss, a.q_sd, vp, a.kv_ld, a.Lk, a.Hkv, a.g, a.W, a.Lq, a.opblk,
-                    a.stblk, a.ystat, a.yf32);
+    merge_row<T, D, true>(head * kRows + r, a.part_ml, a.part_y, a.part_cand, 1, a.S, a.M, heads_rows, a.p_round,
+                          a.y_round, q, a.q_sb, a.q_sh, a.q_ss, a.q_sd, vp, a.kv_ld, a.Lk, a.Hkv, a.g, a.W, a.Lq,
+                          a.opblk, a.stblk, a.ystat, a.yf32);
   publish();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (threadIdx.x == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  __syncthreads();
   unsigned char* aux = lds + kLogitBytes;
   u32x4* opnd = reinterpret_cast<u32x4*>(aux + kAuxOps);
   float* stat = reinterpret_cast<float*>(aux + kAuxStat);
@@ -513,33 +643,39 @@ __global__ void __launch_bounds__(kResNT, 1) resident_kernel(ResArgs a) {
       const float mw = sm_m[w * kRows + row];
       l += sm_l[w * kRows + row] * ((mw == -INFINITY) ? 0.f : exp2f(mw - mx));
     }
-    a.part_ml[(slot * kRows + row) * 2 + 0] = mx;
-    a.part_ml[(slot * kRows + row) * 2 + 1] = l;
+    st_dev(reinterpret_cast<uint64_t*>(a.part_ml + (slot * kRows + row) * 2), __builtin_bit_cast(uint64_t, f32x2{mx, l}));
     float cs[kCand];
     int ck[kCand];
     merge_wave_cands<kResWaves>(sm_cs, sm_ck, row, cs, ck);
 #pragma unroll
     for (int j = 0; j < kCand; ++j)
-      a.part_cand[(slot * kRows + row) * kCand + j] = make_int2(ck[j], __float_as_int(cs[j]));
+      st_dev(reinterpret_cast<uint64_t*>(a.part_cand + (slot * kRows + row) * kCand + j),
+             __builtin_bit_cast(uint64_t, i32x2{ck[j], __float_as_int(cs[j])}));
   }
   float* py = a.part_y + slot * kRows * D;
-  for (int i = threadIdx.x; i < kRows * D; i += kResNT) py[i] = ybuf[(i / D) * kYPitchR + i % D];
+  for (int i = 2 * threadIdx.x; i < kRows * D; i += 2 * kResNT) {
+    const float* yr = ybuf + (i / D) * kYPitchR + i % D;
+    st_dev(reinterpret_cast<uint64_t*>(py + i), __builtin_bit_cast(uint64_t, f32x2{yr[0], yr[1]}));
+  }
   // The selection's per-row words start at zero (the pooling tail adds to them).
   if (a.fz.enabled && split == 0)
-    for (int i = threadIdx.x; i < kRowWords; i += kResNT) a.fz.ws.rowws[(int64_t)head * kRowWords + i] = 0u;
+    for (int i = threadIdx.x; i < kRowWords; i += kResNT) st_dev(a.fz.ws.rowws + (int64_t)head * kRowWords + i, 0u);
 
   // ---- Barrier 1 ----------------------------------------------------------
   uint32_t* sy = a.sync + (size_t)head * 4;
   int* s_state = reinterpret_cast<int*>(aux + kAuxState);
   publish();
-  if (threadIdx.x == 0) s_state[0] = barrier1(sy, a.S, a.spin1);
+  if (threadIdx.x == 0) {
+    const int st = barrier1(sy, a.S, a.spin1);
+    if (st != kStLeave) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // for the whole workgroup
+    s_state[0] = st;
+  }
   __syncthreads();
   const int st1 = s_state[0];
   if (st1 == kStLeave) {
     if (threadIdx.x == 0) atomicAdd(sy + 2, 1u);
     return;
   }
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (st1 == kStAlone) {
     __syncthreads();  // s_state read by every thread before the LDS is reused
     finish_alone<T, PR>(a, head, lds);
@@ -549,9 +685,9 @@ __global__ void __launch_bounds__(kResNT, 1) resident_kernel(ResArgs a) {
   // ---- Merge: this workgroup's rows of the head, one wave each --------------
   const int heads_rows = (int)(gridDim.x / a.S) * kRows;
   for (int r = split + a.S * wv; r < kRows; r += a.S * kResWaves)
-    merge_row<T, D>(head * kRows + r, a.part_ml, a.part_y, a.part_cand, 1, a.S, M, heads_rows, a.p_round, a.y_round,
-                    q, a.q_sb, a.q_sh, a.q_ss, a.q_sd, vp, a.kv_ld, Lk, a.Hkv, a.g, a.W, a.Lq, a.opblk, a.stblk,
-                    a.ystat, a.yf32);
+    merge_row<T, D, true>(head * kRows + r, a.part_ml, a.part_y, a.part_cand, 1, a.S, M, heads_rows, a.p_round,
+                          a.y_round, q, a.q_sb, a.q_sh, a.q_ss, a.q_sd, vp, a.kv_ld, Lk, a.Hkv, a.g, a.W, a.Lq,
+                          a.opblk, a.stblk, a.ystat, a.yf32);
 
   // ---- Barrier 2 ----------------------------------------------------------
   publish();
@@ -572,11 +708,11 @@ __global__ void __launch_bounds__(kResNT, 1) resident_kernel(ResArgs a) {
       st_agent(sy + 1, 0u);
       st_agent(sy + 2, 0u);
     }
+    if (st == kStGo) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // for the whole workgroup
     s_state[0] = st;
   }
   __syncthreads();
   if (s_state[0] == kStFail) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
   // ---- Phase 3: the scores of this workgroup's keys ------------------------
   u32x4* opnd = reinterpret_cast<u32x4*>(aux + kAuxOps);
@@ -586,17 +722,33 @@ __global__ void __launch_bounds__(kResNT, 1) resident_kernel(ResArgs a) {
   __syncthreads();
   const float out_scale = -2.0f * (1.0f / static_cast<float>(a.g));
   float* srow = a.scores + (int64_t)head * Lk;
+  // Tiles in pairs (i, i+1); a pair whose second tile lies past the range
+  // computes it on stale logits and zero V rows and stores none of it.
+  const float* cst = stat + li;
 #pragma unroll
-  for (int i = 0; i < kResTiles; ++i) {
-    const int tr0 = trel(i);
-    if (tr0 >= nrel) break;
-    f32x4 s[2][kMB];
+  for (int i = 0; i < kResTiles; i += 2) {
+    if (trel(i) >= nrel) break;
+    const int t0[2] = {k_begin + trel(i), k_begin + trel(i + 1)};
+    f32x4 s[2][2][kMB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int mb = 0; mb < kMB; ++mb) s[kb][mb] = logit[(i * 2 * kMB + kb * kMB + mb) * 64];
-    score_tile<T, PR>(s, vres[i], opnd, stat, k_begin + tr0, k_begin, k_end, M, a.W, Lk, pad_rows, a.scale_log2,
-                      a.eps, out_scale, srow, a.fz.enabled ? sc : nullptr);
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb) s[u][kb][mb] = logit[((i + u) * 2 * kMB + kb * kMB + mb) * 64];
+    bool sink_here = false;
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb) {
+      const int sk = __builtin_bit_cast(int, cst[mb * kStatWords + 32]);
+      sink_here |= (uint32_t)(sk - t0[0]) < (uint32_t)kTile || (uint32_t)(sk - t0[1]) < (uint32_t)kTile;
+    }
+    float* scp = a.fz.enabled ? sc : nullptr;
+    if (pad_rows || t0[1] + kTile > unmasked_end || __any(sink_here))
+      score_pair<T, PR, true>(s, vres[i], vres[i + 1], opnd, stat, t0, k_begin, k_end, M, a.W, Lk, a.scale_log2,
+                              a.eps, out_scale, srow, scp);
+    else
+      score_pair<T, PR, false>(s, vres[i], vres[i + 1], opnd, stat, t0, k_begin, k_end, M, a.W, Lk, a.scale_log2,
+                               a.eps, out_scale, srow, scp);
   }
   if (a.fz.enabled) {
     __syncthreads();  // scores in LDS; the logits are dead

@@ -297,7 +297,9 @@ constexpr float kCorrMinP = 1.0f / 4096.0f;
 constexpr float kCorrMinLog2P = -12.0f;  // log2(kCorrMinP)
 constexpr int kCorrKeys = 8;  // candidates corrected per row (the largest p)
 
-template <typename T, int D>
+// kCoherent: every result is written with device-coherent stores (st_dev),
+// for readers in the same kernel (the resident layer-call).
+template <typename T, int D, bool kCoherent = false>
 __device__ __forceinline__ void merge_row(int rid, const float* __restrict__ part_ml, const float* __restrict__ part_y,
                                           const int2* __restrict__ part_cand, int n_mc, int n_splits, int M,
                                           int n_rows, int p_round, int y_round, const T* __restrict__ q,
@@ -501,38 +503,69 @@ __device__ __forceinline__ void merge_row(int rid, const float* __restrict__ par
   const int64_t rbase = (int64_t)head * mpad + gr;
   T* ob = reinterpret_cast<T*>(opblk + ((int64_t)head * n_mc + mc) * OPS * 64);
   const int mb = row / 16, li = row % 16;
+  float ye[DPL];
+  T qe[DPL], he[DPL], le[DPL];
 #pragma unroll
   for (int e = 0; e < DPL; ++e) {
-    const int d = d0 + e;
-    if (!col) break;
     float y = valid ? acc[e] / l + corr[e] : 0.f;
     const T hi = static_cast<T>(y);
     if (y_round) y = static_cast<float>(hi);
     const T lo = static_cast<T>(y - static_cast<float>(hi));
-    ysq += y * y;
-    const float dv = vk[e] - y;
-    dsq += dv * dv;
-    yf32[rbase * D + d] = y;
-    // Operand block of this head: per row-chunk, the Q, Y-hi and Y-lo
-    // MFMA operands in per-lane order (slot (which, mb, kk), lane li + 16*lg,
-    // element e8), so that pass 2 stages them with one contiguous copy.
+    if (col) {
+      ysq += y * y;
+      const float dv = vk[e] - y;
+      dsq += dv * dv;
+    }
+    ye[e] = y;
+    qe[e] = gr < M ? qv[e] : static_cast<T>(0.f);
+    he[e] = hi;
+    le[e] = lo;
+  }
+  // Operand block of this head: per row-chunk, the Q, Y-hi and Y-lo MFMA
+  // operands in per-lane order (slot (which, mb, kk), lane li + 16*lg,
+  // element e8), so that pass 2 stages them with one contiguous copy.
+  auto op_at = [&](int which, int d) __attribute__((always_inline)) {
     const int kk = d / 32, lg = (d % 32) / 8, e8 = d % 8;
-    const int word = li + 16 * lg;
-    ob[((size_t)((0 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = gr < M ? qv[e] : static_cast<T>(0.f);
-    ob[((size_t)((1 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = hi;
-    ob[((size_t)((2 * kMB + mb) * KK + kk) * 64 + word) * 8 + e8] = lo;
+    return ob + ((size_t)((which * kMB + mb) * KK + kk) * 64 + li + 16 * lg) * 8 + e8;
+  };
+  if (col) {
+    if constexpr (kCoherent) {
+      static_assert(DPL == 2, "coherent stores pack two columns per word");
+      typedef T t2 __attribute__((ext_vector_type(2)));
+      st_dev(reinterpret_cast<uint64_t*>(yf32 + rbase * D + d0), __builtin_bit_cast(uint64_t, f32x2{ye[0], ye[1]}));
+      st_dev(reinterpret_cast<uint32_t*>(op_at(0, d0)), __builtin_bit_cast(uint32_t, t2{qe[0], qe[1]}));
+      st_dev(reinterpret_cast<uint32_t*>(op_at(1, d0)), __builtin_bit_cast(uint32_t, t2{he[0], he[1]}));
+      st_dev(reinterpret_cast<uint32_t*>(op_at(2, d0)), __builtin_bit_cast(uint32_t, t2{le[0], le[1]}));
+    } else {
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        yf32[rbase * D + d0 + e] = ye[e];
+        *op_at(0, d0 + e) = qe[e];
+        *op_at(1, d0 + e) = he[e];
+        *op_at(2, d0 + e) = le[e];
+      }
+    }
   }
   const float yn2 = wave_sum_dpp(ysq);
   const float nd2_top = -0.5f * wave_sum_dpp(dsq);
   if (lane == 0) {
     const float lse_row = valid ? lse2 : INFINITY;
-    ystat[rbase * 2 + 0] = lse_row;
-    ystat[rbase * 2 + 1] = yn2;
     float* sb = stblk + (((int64_t)head * n_mc + mc) * kMB + row / 16) * kStatWords + (row % 16);
-    sb[0] = lse_row;
-    sb[16] = yn2;
-    sb[32] = __builtin_bit_cast(float, k_top);
-    sb[48] = nd2_top;
+    if constexpr (kCoherent) {
+      st_dev(ystat + rbase * 2 + 0, lse_row);
+      st_dev(ystat + rbase * 2 + 1, yn2);
+      st_dev(sb + 0, lse_row);
+      st_dev(sb + 16, yn2);
+      st_dev(sb + 32, __builtin_bit_cast(float, k_top));
+      st_dev(sb + 48, nd2_top);
+    } else {
+      ystat[rbase * 2 + 0] = lse_row;
+      ystat[rbase * 2 + 1] = yn2;
+      sb[0] = lse_row;
+      sb[16] = yn2;
+      sb[32] = __builtin_bit_cast(float, k_top);
+      sb[48] = nd2_top;
+    }
   }
 }
 

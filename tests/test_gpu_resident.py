@@ -149,3 +149,33 @@ def test_resident_against_streaming(gpu, resident):
     assert rel.max().item() <= 1e-4
     worst, unexcused = R.index_overlap(idx_r.cpu(), idx_s.cpu(), pooled)
     assert worst >= 0.999, (worst, unexcused)
+
+
+def test_new_inputs_on_a_used_workspace(gpu, resident):
+    """A plan's workspace still holds the previous call's partials and merged
+    rows: a call on other inputs must read only what its own workgroups
+    published (scores equal to a fresh streaming run's up to summation order,
+    p unrounded), in both orders of two input sets."""
+    cfg, Lq, Lk, W, dtype = SHAPES[2]
+    ks = 11
+    keep = R.keep_length(0.1, Lk, W)
+    sets = [tuple(t.to(gpu) for t in make_qkv(cfg, Lq, Lk, dtype=dtype, seed=s, k_scale="lognormal"))
+            for s in (80, 81)]
+    ref = []
+    resident.set_resident(False)
+    try:
+        for Q, K, V in sets:
+            plan = resident.EvictPlan(Q, K, W, ks, keep, keep_scores=True, p_round=False)
+            plan(Q, K, V)
+            ref.append(plan.scores.clone())
+    finally:
+        resident.set_resident(True)
+    plan = resident.EvictPlan(sets[0][0], sets[0][1], W, ks, keep, keep_scores=True, p_round=False)
+    for order in ((0, 1), (1, 0), (0, 1)):
+        for i in order:
+            print(f"[resident reuse] inputs {i}", flush=True)
+            plan(*sets[i])
+            torch.cuda.synchronize()
+            got, exp = plan.scores.double(), ref[i].double()
+            rel = ((got - exp).abs() / exp.abs().clamp_min(1e-30)).max().item()
+            assert rel <= 1e-4, (i, rel)
