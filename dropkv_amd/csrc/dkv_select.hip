@@ -40,30 +40,38 @@ sel_pool_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
 }
 
 // ---------------------------------------------------------------------------
-// resolve: one workgroup per row.
-//   A. Pools the keys next to the scoring pass's split boundaries (their
-//      windows straddle two workgroup ranges), which completes the row's
-//      top-digit histogram and maximum; finds the top-digit bin b1 of the
-//      keep-th largest key.
-//   B. One sweep over the pooled row: per chunk, the keys above b1; the keys
-//      inside b1 (the candidates, a few percent of the row) into LDS.
-//   C. Digits 2 and 3 over the candidates: the threshold key T and how many
-//      keys equal to T are kept (the lowest indices).
-//   D. Per chunk, the kept keys above T and the keys equal to T in the
-//      chunks before it (exclusive prefix sums), for emit.
+// resolve: grid = rows * parts; part p of a row sweeps its chunks
+// [p*cpp, (p+1)*cpp).
+//   A. (every part) Pools the keys next to the scoring pass's split
+//      boundaries (their windows straddle two workgroup ranges; the part
+//      writes those in its chunks to the pooled row), which completes the
+//      row's top-digit histogram and maximum in LDS; finds the top-digit bin
+//      b1 of the keep-th largest key.
+//   B. (every part) One sweep of its chunks: per chunk the keys above b1
+//      (into cnt[].x), the keys inside b1 (the candidates) appended to the
+//      row's list in the workspace; then its arrival on the row's counter.
+//      What B and A publish is written with device-coherent stores, so an
+//      arrival needs only the wait for them.
+//   C. (the row's last part to arrive) Digits 2 and 3 over the candidates:
+//      the threshold key T and how many keys equal to T are kept (the lowest
+//      indices).
+//   D. (the same) Per chunk, the kept keys above T and the keys equal to T
+//      in the chunks before it (exclusive prefix sums), for emit.
 // Past kResCandCap candidates (near-constant rows), C and D sweep the row
-// again instead of reading the list.
+// instead of reading the list.  No part waits for another: the last one to
+// arrive finishes the row, whenever the others ran.  A row of one part
+// keeps its candidates and chunk counts in LDS (no publishing round trips).
 // ---------------------------------------------------------------------------
 constexpr int kResT = 1024;
-constexpr int kResWaves = kResT / 64;
-constexpr int kWaveKeys = 2 * kChunk;              // keys per wave and sweep round: 8 x 4 per lane
-constexpr int kRoundKeys = kResWaves * kWaveKeys;  // keys per sweep round
-constexpr int kResCandCap = 4096;                  // candidates held in LDS as (key, index)
+constexpr int kResMaxParts = 8;
+constexpr int kResPartMinChunks = 32;  // shorter rows are resolved by one workgroup (measured crossover)
+constexpr int kRoundKeys = 4 * kResT;             // keys per sweep round: 4 per thread, 256 per wave
+constexpr int kRoundsInFlight = 4;                // sweep rounds whose loads are issued together
 constexpr int kResUnion = kBndLds > 2 * kResCandCap ? kBndLds : 2 * kResCandCap;
-constexpr int kBndPer = kBndLds / kResT;           // boundary raw scores per thread (at most)
-constexpr int kCntPer = kMaxChunks / kResT;        // chunk counters per thread (at most)
+constexpr int kBndPer = kBndLds / kResT;          // boundary raw scores per thread (at most)
+constexpr int kCntPer = kMaxChunks / kResT;       // chunk counters per thread (at most)
 static_assert(kBins1 == 2 * kResT, "two top-digit histogram words per thread");
-static_assert(kWaveKeys == 2 * kChunk, "a wave's share of a round is two whole chunks");
+static_assert(kChunk % 256 == 0, "a wave's 256 keys of a round lie in one chunk");
 
 // Sort key of a pooled value given as its bits (the buffer load's integer
 // lanes), with the protected tail mapped to kbig.
@@ -74,18 +82,19 @@ __device__ __forceinline__ uint32_t pooled_key(uint32_t bits, int j, int prot, u
 }
 
 __global__ void __launch_bounds__(kResT)
-sel_resolve_kernel(const float* __restrict__ scores, int Lk, int ks, int window, int keep, int chunks,
-                   SplitGeom geom, SelWs ws) {
+sel_resolve_kernel(const float* __restrict__ scores, int Lk, int ks, int window, int keep, int chunks, int parts,
+                   int cpp, SplitGeom geom, SelWs ws) {
   __shared__ __attribute__((aligned(16))) uint32_t hist1[kBins1];
   __shared__ uint32_t hist2[kBins2];
   __shared__ uint32_t hist3[kBins3];
   __shared__ uint32_t gtc[kMaxChunks];  // per chunk: keys above b1, then kept keys above T
   __shared__ uint32_t eqc[kMaxChunks];  // per chunk: keys equal to T
-  __shared__ float bpool[kBndPoolLds];
   __shared__ __attribute__((aligned(16))) uint32_t un[kResUnion];  // boundary raw scores, then candidates
-  __shared__ uint32_t small[128];  // scan partials [0, 32), bin / counts at 64.., max at 96.., count at 112
+  __shared__ uint32_t small[128];  // scan partials [0, 32), bin / counts at 64.., max at 96.., flag at 112
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int row = blockIdx.x;
+  const int row = blockIdx.x / parts, part = blockIdx.x % parts;
+  const int c_begin = part * cpp, c_end = min(c_begin + cpp, chunks);
+  const int kb = c_begin * kChunk, ke = min(c_end * kChunk, Lk);
   const int h = ks / 2;
   const int prot = Lk - window;
   uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
@@ -110,10 +119,9 @@ sel_resolve_kernel(const float* __restrict__ scores, int Lk, int ks, int window,
       if (u >= 0 && u < Lk) bv[i] = srow[u];
     }
   }
-  for (int i = tid; i < chunks; i += kResT) eqc[i] = 0u;
-  for (int i = tid; i < kBins2; i += kResT) hist2[i] = 0u;
-  for (int i = tid; i < kBins3; i += kResT) hist3[i] = 0u;
-  if (tid == 0) small[112] = 0u;
+  const bool solo = parts == 1;
+  for (int i = tid; i < cpp; i += kResT) gtc[i] = 0u;
+  if (tid == 0) small[113] = 0u;  // candidates of a one-part row
   reinterpret_cast<uint2*>(hist1)[tid] = hv;
   float* bxs = reinterpret_cast<float*>(un);
 #pragma unroll
@@ -127,16 +135,17 @@ sel_resolve_kernel(const float* __restrict__ scores, int Lk, int ks, int window,
   for (int t = tid; t < nb * w2; t += kResT) {
     const int bi = t / w2, k = t % w2;
     const int j = (bi + 1) * geom.kps - h + k;
-    float m = -INFINITY;
     if (j < Lk) {
       const float* w = bxs + bi * w4 + k;
+      float m = -INFINITY;
       for (int u = 0; u <= 2 * h; ++u) m = fmaxf(m, w[u]);
       const uint32_t key = float_key(m);
       bmax = max(bmax, key);
       if (j < prot) atomicAdd(&hist1[key >> kShift1], 1u);
-      prow[j] = m;  // read back by this workgroup's sweep (after the barriers below) and by emit
+      // read back by this part's sweep (after the barriers below), by the
+      // last part's fallback sweep and by emit
+      if (j >= kb && j < ke) st_dev(reinterpret_cast<uint32_t*>(prow + j), __float_as_uint(m));
     }
-    bpool[t] = m;
   }
   const uint32_t gmax = block_max_u32(max(bmax, rmax), small + 96);
   const uint32_t kbig = float_key(key_float(gmax) + 1.0f);
@@ -148,63 +157,87 @@ sel_resolve_kernel(const float* __restrict__ scores, int Lk, int ks, int window,
   const uint32_t b1 = fb[0];
   const uint32_t k1 = (uint32_t)keep - fb[1];
 
-  // B. Sweep: wave w of round r reads keys r*kRoundKeys + w*kWaveKeys + ..,
-  // lane l the 4-key groups l + 64 i; groups i < 4 lie in the wave's first
-  // chunk, the rest in its second.  Past Lk the loads return zeros (masked).
+  // B. Sweep of [kb, ke): round r, wave w, lane l reads keys
+  // r + 256w + 4l .. +3 (past Lk the loads return zeros, masked).  The
+  // candidates of a batch of rounds take their slots with one atomic add per
+  // wave on the row's counter.
   const rsrc_t prs = make_rsrc(prow, (uint32_t)Lk * 4u);
-  uint2* cl = reinterpret_cast<uint2*>(un);
-  for (int r0 = 0; r0 < Lk; r0 += kRoundKeys) {
-    const int base = r0 + wv * kWaveKeys;
-    if (base >= Lk) break;
-    u32x4 x[8];
+  uint2* gl = ws.cand + (int64_t)row * kResCandCap;
+  uint2* cl = reinterpret_cast<uint2*>(un);  // the boundary raw scores are dead
+  for (int r0 = kb; r0 < ke; r0 += kRoundsInFlight * kRoundKeys) {
+    u32x4 x[kRoundsInFlight];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = buf_load16(prs, (uint32_t)(base + 4 * (lane + 64 * i)) * 4u);
-    uint32_t keys[8][4];
-    uint32_t na0 = 0u, na1 = 0u, nc = 0u;
+    for (int i = 0; i < kRoundsInFlight; ++i)
+      x[i] = buf_load16(prs, (uint32_t)(r0 + i * kRoundKeys + 256 * wv + 4 * lane) * 4u);
+    uint32_t nc = 0u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < kRoundsInFlight; ++i) {
+      const int base = r0 + i * kRoundKeys + 256 * wv;
+      uint32_t na = 0u;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int j = base + 4 * (lane + 64 * i) + e;
-        const uint32_t key = pooled_key(x[i][e], j, prot, kbig);
-        keys[i][e] = key;
-        const uint32_t d = key >> kShift1;
-        const bool valid = j < Lk;
-        const uint32_t above = (valid && d > b1) ? 1u : 0u;
-        if (i < 4) na0 += above;
-        else na1 += above;
+        const int j = base + 4 * lane + e;
+        const uint32_t d = pooled_key(x[i][e], j, prot, kbig) >> kShift1;
+        const bool valid = j < ke;
+        na += (valid && d > b1) ? 1u : 0u;
         nc += (valid && d == b1) ? 1u : 0u;
       }
-    const uint32_t s0 = wave_reduce_add(na0), s1 = wave_reduce_add(na1);
-    const int c0 = base / kChunk;
-    if (lane == 0) {
-      gtc[c0] = s0;
-      if (base + kChunk < Lk) gtc[c0 + 1] = s1;
+      const uint32_t s = wave_reduce_add(na);
+      if (lane == 0 && base < ke && s) atomicAdd(&gtc[base / kChunk - c_begin], s);
     }
-    // Candidate slots: a wave-wide exclusive scan of the lanes' counts and
-    // one LDS atomic per wave.
     const uint32_t incl = wave_incl_scan(nc);
     const uint32_t wtot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
     uint32_t wbase = 0u;
-    if (lane == 0 && wtot) wbase = atomicAdd(&small[112], wtot);
+    if (lane == 0 && wtot) wbase = solo ? atomicAdd(&small[113], wtot) : atomicAdd(rw + kRowNcand, wtot);
     wbase = (uint32_t)__builtin_amdgcn_readfirstlane((int)wbase);
     if (nc) {
       uint32_t pos = wbase + incl - nc;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < kRoundsInFlight; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int j = base + 4 * (lane + 64 * i) + e;
-          if (j < Lk && (keys[i][e] >> kShift1) == b1) {
-            if (pos < (uint32_t)kResCandCap) cl[pos] = make_uint2(keys[i][e], (uint32_t)j);
+          const int j = r0 + i * kRoundKeys + 256 * wv + 4 * lane + e;
+          const uint32_t key = pooled_key(x[i][e], j, prot, kbig);
+          if (j < ke && (key >> kShift1) == b1) {
+            if (pos < (uint32_t)kResCandCap) {
+              if (solo)
+                cl[pos] = make_uint2(key, (uint32_t)j);
+              else
+                st_dev(reinterpret_cast<uint64_t*>(gl + pos), (uint64_t)key | ((uint64_t)(uint32_t)j << 32));
+            }
             ++pos;
           }
         }
     }
   }
   __syncthreads();
-  const uint32_t ncand = small[112];
+  uint32_t ncand;
+  if (solo) {
+    ncand = small[113];
+  } else {
+    for (int c = c_begin + tid; c < c_end; c += kResT)
+      st_dev(reinterpret_cast<uint32_t*>(ws.cnt + (int64_t)row * chunks + c), gtc[c - c_begin]);
+    // Arrival: the stores above complete first; the last part continues.
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      const bool last = atomicAdd(rw + kRowArrive, 1u) == (uint32_t)parts - 1u;
+      if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      small[112] = last ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!small[112]) return;
+    // The row's candidates and per-chunk counts, as the parts left them.
+    ncand = __hip_atomic_load(rw + kRowNcand, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (ncand <= (uint32_t)kResCandCap)
+      for (uint32_t p = tid; p < ncand; p += kResT) cl[p] = gl[p];
+    for (int c = tid; c < chunks; c += kResT) gtc[c] = ws.cnt[(int64_t)row * chunks + c].x;
+  }
   const bool in_lds = ncand <= (uint32_t)kResCandCap;
+  for (int c = tid; c < chunks; c += kResT) eqc[c] = 0u;
+  for (int i = tid; i < kBins2; i += kResT) hist2[i] = 0u;
+  for (int i = tid; i < kBins3; i += kResT) hist3[i] = 0u;
+  __syncthreads();
 
   // Every candidate (key, index): from the LDS list, or by sweeping the row.
   auto for_cands = [&](auto&& f) __attribute__((always_inline)) {
@@ -424,8 +457,12 @@ hipError_t launch_select_after_pool(const float* scores, int rows, int Lk, int k
   const SelWs ws = sel_layout(ws_base, rows, Lk, nullptr);
   const int chunks = (Lk + kChunk - 1) / kChunk;
   const dim3 grid((unsigned)(rows * chunks));
-  launch(sel_resolve_kernel, dim3((unsigned)rows), dim3(kResT), 0, st, scores, Lk, ks, window, keep, chunks,
-         SplitGeom{n_splits, kps}, ws);
+  // Rows of kResPartMinChunks chunks or more in up to kResMaxParts parts,
+  // each a whole number of chunks; shorter rows in one.
+  const int cpp = chunks < kResPartMinChunks ? chunks : (chunks + kResMaxParts - 1) / kResMaxParts;
+  const int parts = (chunks + cpp - 1) / cpp;
+  launch(sel_resolve_kernel, dim3((unsigned)(rows * parts)), dim3(kResT), 0, st, scores, Lk, ks, window, keep,
+         chunks, parts, cpp, SplitGeom{n_splits, kps}, ws);
   launch(sel_emit_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, ws, out_idx, pooled_out,
          compact_args(cp));
   return hipGetLastError();

@@ -13,13 +13,14 @@
 //   pool    (pass-2 epilogue, or the standalone pool kernel) pooled values of
 //           the keys whose window lies inside one workgroup's range, the row
 //           maximum and the top-digit histogram (device atomics);
-//   resolve (one workgroup per row) pools the few keys next to the scoring
-//           pass's split boundaries, which completes the histogram and fixes
-//           the top-digit bin b1; sweeps the row once for the keys above b1
-//           per chunk and the keys inside b1 (the candidates, a few percent
-//           of the row, kept in LDS); resolves digits 2 and 3 from the
-//           candidates; writes per 1024-key chunk the kept keys above T and
-//           the keys equal to T before it;
+//   resolve (up to 8 workgroups per row, each sweeping a part of it) pools
+//           the few keys next to the scoring pass's split boundaries, which
+//           completes the histogram and fixes the top-digit bin b1; sweeps
+//           its part for the keys above b1 per chunk and the keys inside b1
+//           (the candidates, a few percent of the row, appended to a list in
+//           the workspace); the row's last part to finish resolves digits 2
+//           and 3 from the candidates and writes per 1024-key chunk the kept
+//           keys above T and the keys equal to T before it;
 //   emit    (row, chunk) workgroups write the chunk's kept indices in index
 //           order from those offsets and copy the K/V rows they name.
 #pragma once
@@ -44,13 +45,17 @@ constexpr int kBndPoolLds = 2048; // LDS words for the boundary keys' pooled val
 // kernel clears them every call), then results of the resolve stage:
 constexpr int kRowMax = 0;                 // max pooled key of the interiors
 constexpr int kRowB1 = 1;                  // T, keys equal to T that are kept, max key of the row (resolve)
-constexpr int kRowHist1 = 4;               // top-digit histogram (unprotected interior keys), 16-byte aligned
+constexpr int kRowArrive = 4;              // resolve parts of the row that have swept their chunks
+constexpr int kRowNcand = 5;               // candidates the parts have found (may exceed kResCandCap)
+constexpr int kRowHist1 = 8;               // top-digit histogram (unprotected interior keys), 16-byte aligned
 constexpr int kRowWords = kRowHist1 + kBins1;
+constexpr int kResCandCap = 4096;          // candidates (key, index) kept per row, in the workspace and in LDS
 
 struct SelWs {
   uint32_t* rowws;     // [rows][kRowWords]
   float* pooled;       // [rows][Lk]
   uint2* cnt;          // [rows][chunks] {kept keys above T, keys equal to T} in the chunks before each
+  uint2* cand;         // [rows][kResCandCap] the resolve parts' candidates (key, index)
 };
 
 inline size_t sel_al256(size_t b) { return (b + 255) & ~size_t(255); }
@@ -67,6 +72,7 @@ inline SelWs sel_layout(char* base, int64_t rows, int64_t Lk, size_t* total) {
   w.rowws = reinterpret_cast<uint32_t*>(take((size_t)rows * kRowWords * 4));
   w.pooled = reinterpret_cast<float*>(take((size_t)rows * Lk * 4));
   w.cnt = reinterpret_cast<uint2*>(take((size_t)rows * chunks * 8));
+  w.cand = reinterpret_cast<uint2*>(take((size_t)rows * kResCandCap * 8));
   if (total) *total = off;
   return w;
 }
