@@ -798,7 +798,7 @@ bool resident_plan(int dtype, int64_t D, int64_t M, int64_t heads, int64_t Lk, i
   if (heads < 1 || heads > kResMaxHeads || Lk < 1) return false;
   const int64_t s = (Lk + kResKeys - 1) / kResKeys;
   const int cus = device_cus();
-  if (cus <= 0 || heads * s > cus) return false;
+  if (cus <= 0 || heads * s > cus || heads * s > kResMaxHeads) return false;  // the plan sized its partials for this
   *S = (int)s;
   *kpw = kResKeys;
   return true;

@@ -1079,8 +1079,12 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   // The counters of the resident layer-call first, at a fixed offset, so
   // that no other layout ever writes over them.
   p.off_sync = take(kResSyncBytes);
-  // Partials: pass 1's splits, or the resident kernel's workgroups per head.
-  const int s_part = p.n_mc == 1 ? std::max(p.s1, ceil_div(Lk, kResKeys)) : p.s1;
+  // Partials: pass 1's splits, or the resident kernel's workgroups per head
+  // when the call could fit it (one row-chunk, at most kResMaxHeads
+  // workgroups in all).
+  const int s_res = ceil_div(Lk, kResKeys);
+  const bool res_fit = p.n_mc == 1 && (int64_t)p.heads * s_res <= kResMaxHeads;
+  const int s_part = res_fit ? std::max(p.s1, s_res) : p.s1;
   const size_t slots = (size_t)p.heads * p.n_mc * s_part;
   p.off_ml = take(slots * kRows * 2 * sizeof(float));
   p.off_y = take(slots * kRows * D * sizeof(float));

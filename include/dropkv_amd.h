@@ -170,8 +170,8 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
  * first call outside graph capture); no call allocates or frees anything.
  * Calls whose dropkv_evict_workspace_bytes exceeds the maximum return
  * DROPKV_E_UNSUPPORTED: 32 MiB covers a Llama-3.1-8B layer (Hq 32, Hkv 8,
- * D 128) up to about 470K keys and a Qwen2-0.5B layer up to about 1.9M
- * keys; the B4 Hq64 Hkv8 128K-key stress shape needs 77 MiB and is refused.
+ * D 128) up to about 470K keys and a Qwen2-0.5B layer up to about 2.0M
+ * keys; the B4 Hq64 Hkv8 128K-key stress shape needs 78 MiB and is refused.
  * Every call on one GPU uses the same scratch and leaves its contents
  * behind: calls that overlap on one GPU (two streams, or two threads) race
  * and must be serialised by the caller.  The caller initialises nothing (the
