@@ -45,10 +45,14 @@ HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
 # kernels of one dropkv_evict call, in launch order: with the selection fused
 # into the scoring pass's tail, and with the standalone selection kernels
+# (the selection in pass 2's tail; in two kernels after pass 2's pooling; in
+# three kernels after pass 2)
+STAGES_TAIL = ("pass1_partials", "merge", "pass2_scores_select")
 STAGES_FUSED = ("pass1_partials", "merge", "pass2_scores_pool", "select_resolve", "emit_compact")
 STAGES_UNFUSED = ("pass1_partials", "merge", "pass2_scores", "select_pool", "select_resolve", "emit_compact")
+STAGE_NAMES = {len(t): t for t in (STAGES_TAIL, STAGES_FUSED, STAGES_UNFUSED)}
 # kernels that stream all of K and V
-STREAM_STAGES = ("pass1_partials", "pass2_scores", "pass2_scores_pool")
+STREAM_STAGES = ("pass1_partials", "pass2_scores", "pass2_scores_pool", "pass2_scores_select")
 
 WORKLOADS = {
     "llama8b_layer_32k": dict(B=1, Hq=32, Hkv=8, D=128, Lq=32768, Lk=32768, window=8, kernel=11, ratio=0.1,
@@ -438,8 +442,7 @@ def kernel_times(lib, fn, steps):
                 sums[i] += buf[i]
     finally:
         lib.dropkv_timing_enable(0)
-    names = {len(STAGES_FUSED): STAGES_FUSED, len(STAGES_UNFUSED): STAGES_UNFUSED}.get(
-        nk, tuple(f"kernel{i}" for i in range(nk)))
+    names = STAGE_NAMES.get(nk, tuple(f"kernel{i}" for i in range(nk)))
     return {names[i]: 1e3 * sums[i] / steps for i in range(nk)}, nk
 
 
@@ -478,8 +481,7 @@ def cold_steps(lib, fn, steps, dev):
     finally:
         lib.dropkv_timing_enable(0)
     del flush
-    names = {len(STAGES_FUSED): STAGES_FUSED, len(STAGES_UNFUSED): STAGES_UNFUSED}.get(
-        nk, tuple(f"kernel{i}" for i in range(nk)))
+    names = STAGE_NAMES.get(nk, tuple(f"kernel{i}" for i in range(nk)))
     return total / steps, {names[i]: 1e3 * sums[i] / steps for i in range(nk)}
 
 

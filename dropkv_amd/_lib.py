@@ -58,6 +58,7 @@ _SIGNATURES = {
     "dropkv_append": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "dropkv_set_resident": (_c_int, [_c_int, _c_i64]),
+    "dropkv_set_tail_select": (_c_int, [_c_int, _c_i64]),
     "dropkv_timing_enable": (_c_int, [_c_int]),
     "dropkv_timing_read": (_c_int, [ctypes.POINTER(ctypes.c_double), _c_int]),
     "dropkv_selftest_mfma": (_c_int, [_c_vp, _c_vp]),

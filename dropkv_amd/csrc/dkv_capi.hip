@@ -266,7 +266,11 @@ static int evict_impl(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, i
   const bool resident = mfma && dkv::resident_plan(dtype, D, p.M, B * Hkv, Lk, splits, &rs, &rkpw) &&
                         dkv::select_after_pool_ok(rs, rkpw, Lk, kernel_size);
   const bool fused = resident || (mfma && dkv::select_after_pool_ok(p.s2, p.kps2, Lk, kernel_size));
-  const dkv::FuseSelect fs{sel_ws, (int)kernel_size, (int)protect_window};
+  // With the resident kernel, and where pass 2 cannot run it in its tail,
+  // the selection continues in its own kernels after the scores.
+  int tail_done = 0;
+  const dkv::FuseSelect fs{sel_ws,   (int)kernel_size,        (int)protect_window, (int)keep,
+                           keep_idx, vec ? &cp : nullptr, resident ? nullptr : &tail_done};
   hipError_t e;
   if (resident)
     e = dkv::launch_resident(p, dtype, rs, rkpw, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)kv_ld, (int)Hkv, (int)Lq,
@@ -277,7 +281,9 @@ static int evict_impl(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, i
                            reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv),
                            fused ? &fs : nullptr, st);
   if (e != hipSuccess) return hip_status(e, "dropkv_evict scores");
-  if (fused)
+  if (tail_done)
+    e = hipSuccess;
+  else if (fused)
     e = dkv::launch_select_after_pool(sc, (int)(B * Hkv), (int)Lk, (int)kernel_size, (int)protect_window, (int)keep,
                                       resident ? rs : p.s2, resident ? rkpw : p.kps2, keep_idx, nullptr, sel_ws,
                                       vec ? &cp : nullptr, st);
@@ -398,6 +404,13 @@ int dropkv_set_resident(int mode, int64_t spin_polls) {
   if (mode != 0 && mode != 1) return fail(DROPKV_E_ARG, "mode must be 0 or 1");
   if (spin_polls > INT32_MAX) return fail(DROPKV_E_ARG, "spin_polls too large");
   dkv::set_resident(mode, spin_polls < 0 ? -1 : (int)spin_polls);
+  return DROPKV_OK;
+}
+
+int dropkv_set_tail_select(int mode, int64_t spin_polls) {
+  if (mode != 0 && mode != 1) return fail(DROPKV_E_ARG, "mode must be 0 or 1");
+  if (spin_polls > INT32_MAX) return fail(DROPKV_E_ARG, "spin_polls too large");
+  dkv::set_tail_select(mode, spin_polls < 0 ? -1 : (int)spin_polls);
   return DROPKV_OK;
 }
 

@@ -55,6 +55,7 @@ struct ScorePlan {
 };
 
 ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W, int64_t splits);
+struct SelectCompact;
 // Pooling fused into the scoring pass: the selection workspace (its per-row
 // words are cleared by the merge kernel through zero_ptr) and the pooling
 // parameters.  The selection then continues with launch_select_after_pool
@@ -62,6 +63,14 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
 struct FuseSelect {
   char* ws;
   int ks, window;
+  // The whole selection in the scoring pass's tail (threshold, ordered emit
+  // and the gather through `cp`), when the plan and the GPU allow it: the
+  // scoring launch then sets *tail_done and the caller skips
+  // launch_select_after_pool.  keep_idx null: never.
+  int keep;
+  int64_t* keep_idx;
+  const SelectCompact* cp;
+  int* tail_done;
 };
 // K/V: [B*Hkv, kv_ld, D] with rows 0 .. Lk-1 of each head used (kv_ld = Lk: contiguous).
 hipError_t launch_scores(const ScorePlan& p, int dtype, int D, const void* q, int64_t q_sb, int64_t q_sh,
@@ -137,6 +146,13 @@ struct SelectCompact {
   void* v_out;
   int64_t out_ld;  // rows per head in k_out / v_out ([B, H, out_ld, D]; keep: contiguous)
 };
+struct CompactArgs;
+CompactArgs compact_args(const SelectCompact* cp);
+// mode 0: the selection always runs as its own kernels after the scoring
+// pass; 1: in the scoring pass's tail whenever the call allows it.  spin >= 0
+// sets the polls a workgroup waits at the tail's first barrier before it
+// leaves the row to the last one to arrive (tests use 0 to force that path).
+void set_tail_select(int mode, int spin);
 hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int window, int keep, int64_t* out_idx,
                          float* pooled_out, char* ws, bool pre_zeroed, const SelectCompact* cp, hipStream_t st);
 // The resolve and emit stages after a pooling stage that pooled every key

@@ -24,9 +24,11 @@
 #include "dkv_internal.h"
 #include "dkv_score_dev.h"
 #include "dkv_select_dev.h"
+#include "dkv_tail_dev.h"
 
 #include <algorithm>
 #include <climits>
+#include <mutex>
 #include <type_traits>
 
 namespace dkv {
@@ -725,6 +727,10 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
   }
   if (fz.enabled) {
     __syncthreads();  // this workgroup's score stores are done; the LDS operands are dead
+    if (fz.full) {
+      fused_tail<NT>(fz, sc_row, hist_l, head, split, n_splits, kps, Lk);
+      return;
+    }
     const int h = fz.ks / 2;
     const int i0 = split == 0 ? 0 : k_begin + h;
     const int i1 = k_end >= Lk ? Lk : k_end - h;
@@ -1066,7 +1072,9 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   s1 = max(1, min(min(s1, max_by_work), kMaxSplits));
   p.kps1 = ceil_div(ceil_div(Lk, s1), kTile) * kTile;
   p.s1 = ceil_div(Lk, p.kps1);
-  int s2 = splits > 0 ? (int)splits : ceil_div(target, p.heads);
+  // Pass 2: at most one workgroup per CU in all (rounded down), so that the
+  // grid runs in one wave and the selection tail's barriers can hold.
+  int s2 = splits > 0 ? (int)splits : max(1, target / p.heads);
   s2 = max(1, min(s2, max_by_work));
   p.kps2 = ceil_div(ceil_div(Lk, s2), kTile) * kTile;
   p.s2 = ceil_div(Lk, p.kps2);
@@ -1095,6 +1103,46 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
   p.off_yf = take((size_t)p.heads * p.mpad * D * sizeof(float));
   p.total = off;
   return p;
+}
+
+namespace {
+int g_tail_mode = 1;         // 1: selection in pass 2's tail whenever the call allows it
+int g_tail_spin = 1 << 16;   // polls at the tail's barrier A before a workgroup gives up
+
+// Whether `grid` workgroups of `fn` (threads, dynamic LDS bytes) fit on the
+// current GPU at once: the tail's barriers need every workgroup of a row
+// running.  Looked up once per (device, kernel, LDS size).
+bool tail_fits(const void* fn, int threads, size_t lds, int64_t grid) {
+  struct Entry {
+    int dev;
+    const void* fn;
+    size_t lds;
+    int64_t cap;
+  };
+  static std::mutex mu;
+  static Entry cache[64];
+  static int n_cache = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n_cache; ++i)
+    if (cache[i].dev == dev && cache[i].fn == fn && cache[i].lds == lds) return grid <= cache[i].cap;
+  int per_cu = 0, cus = 0, max_lds = 0;
+  int64_t cap = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+      lds <= (size_t)max_lds)
+    cap = (int64_t)per_cu * cus;
+  (void)hipGetLastError();
+  if (n_cache < 64) cache[n_cache++] = Entry{dev, fn, lds, cap};
+  return grid <= cap;
+}
+}  // namespace
+
+void set_tail_select(int mode, int spin) {
+  g_tail_mode = mode;
+  if (spin >= 0) g_tail_spin = spin;
 }
 
 template <typename T, int D>
@@ -1160,12 +1208,24 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
              Lq, Lk, W, p.g, p.M, p.n_mc, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
     return hipGetLastError();
   }
-  if (p_round)
-    launch((pass2_kernel<T, D, 8, 1, true>), g2, dim3(512), lds2, st, kk, vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc,
-           cg, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
-  else
-    launch((pass2_kernel<T, D, 8, 1, false>), g2, dim3(512), lds2, st, kk, vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc,
-           cg, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
+  const auto k2 = p_round ? pass2_kernel<T, D, 8, 1, true> : pass2_kernel<T, D, 8, 1, false>;
+  // The whole selection in pass 2's tail: needs the scores in LDS, an
+  // output to emit into, and every workgroup of the grid running at once.
+  if (fuse && fz.sc_lds && fuse->keep_idx && fuse->cp && g_tail_mode && p.s2 <= kFuseMaxSplits) {
+    const size_t lds_t = (size_t)cg * kOpSlots * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * kStatWords * 4 +
+                         (size_t)p.kps2 * 4 + (size_t)tail_lds_words(512, p.kps2) * 4;
+    if (tail_fits(reinterpret_cast<const void*>(k2), 512, lds_t, (int64_t)p.heads * p.s2)) {
+      fz.full = 1;
+      fz.keep = fuse->keep;
+      fz.spin = g_tail_spin;
+      fz.out_idx = fuse->keep_idx;
+      fz.ca = compact_args(fuse->cp);
+      lds2 = std::max(lds2, lds_t);
+      if (fuse->tail_done) *fuse->tail_done = 1;
+    }
+  }
+  launch(k2, g2, dim3(512), lds2, st, kk, vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2,
+         eps, opblk, stblk, scores, fz);
   return hipGetLastError();
 }
 

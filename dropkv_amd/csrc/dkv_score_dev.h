@@ -585,6 +585,12 @@ struct SelFuse {
   int enabled;
   int ks, window;
   int sc_lds;  // the workgroup's scores are also kept in LDS (kps <= kScLds)
+  // The whole selection in the tail (dkv_tail_dev.h) instead of pooling only.
+  int full;
+  int keep;
+  int spin;    // polls at the tail's barrier A before a workgroup gives up
+  int64_t* out_idx;
+  CompactArgs ca;
 };
 constexpr int kScLds = 4096;  // longest split range whose scores pass 2 keeps in LDS
 

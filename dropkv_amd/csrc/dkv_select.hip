@@ -73,14 +73,6 @@ constexpr int kCntPer = kMaxChunks / kResT;       // chunk counters per thread (
 static_assert(kBins1 == 2 * kResT, "two top-digit histogram words per thread");
 static_assert(kChunk % 256 == 0, "a wave's 256 keys of a round lie in one chunk");
 
-// Sort key of a pooled value given as its bits (the buffer load's integer
-// lanes), with the protected tail mapped to kbig.
-__device__ __forceinline__ uint32_t pooled_key(uint32_t bits, int j, int prot, uint32_t kbig) {
-  if (bits == 0x80000000u) bits = 0u;
-  const uint32_t k = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-  return j >= prot ? kbig : k;
-}
-
 __global__ void __launch_bounds__(kResT)
 sel_resolve_kernel(const float* __restrict__ scores, int Lk, int ks, int window, int keep, int chunks, int parts,
                    int cpp, SplitGeom geom, SelWs ws) {
@@ -319,17 +311,6 @@ sel_resolve_kernel(const float* __restrict__ scores, int Lk, int ks, int window,
 // order from the chunk's offsets (resolve), then (when ko is given) their
 // K/V rows are copied.
 // ---------------------------------------------------------------------------
-struct CompactArgs {
-  const uint8_t* k;
-  const uint8_t* v;
-  int64_t sb, sh, sl;  // source byte strides
-  int H;
-  int units;           // 16-byte units per row
-  uint8_t* ko;
-  uint8_t* vo;
-  int64_t out_ld;      // rows per head in ko / vo
-};
-
 __global__ void __launch_bounds__(kSelT)
 sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __restrict__ out_idx,
                 float* __restrict__ pooled_out, CompactArgs ca) {
@@ -434,7 +415,7 @@ int64_t select_zero_words(int64_t rows) { return rows * kRowWords; }
 
 int64_t select_max_len() { return (int64_t)kMaxChunks * kChunk; }
 
-static CompactArgs compact_args(const SelectCompact* cp) {
+CompactArgs compact_args(const SelectCompact* cp) {
   CompactArgs ca{};
   if (cp) {
     ca.k = static_cast<const uint8_t*>(cp->k);

@@ -47,15 +47,25 @@ constexpr int kRowMax = 0;                 // max pooled key of the interiors
 constexpr int kRowB1 = 1;                  // T, keys equal to T that are kept, max key of the row (resolve)
 constexpr int kRowArrive = 4;              // resolve parts of the row that have swept their chunks
 constexpr int kRowNcand = 5;               // candidates the parts have found (may exceed kResCandCap)
-constexpr int kRowHist1 = 8;               // top-digit histogram (unprotected interior keys), 16-byte aligned
+constexpr int kRowBarA = 8;                // selection in the scoring tail: arrivals at barrier A (| poison bit)
+constexpr int kRowBarB = 9;                //   arrivals at barrier B
+constexpr int kRowStatus = 10;             //   nonzero: barrier B's hang guard gave up
+constexpr int kRowHist1 = 16;              // top-digit histogram (unprotected interior keys), 16-byte aligned
 constexpr int kRowWords = kRowHist1 + kBins1;
 constexpr int kResCandCap = 4096;          // candidates (key, index) kept per row, in the workspace and in LDS
+constexpr int kFuseMaxSplits = 256;        // scoring splits per row the selection tail takes
+constexpr int kPeekTotal = 4096;           // candidates of a row the tail reads without knowing the counts
+constexpr int kScandPad = 4096;            // entries past Lk in a row's candidate regions (the last split's peek)
 
 struct SelWs {
   uint32_t* rowws;     // [rows][kRowWords]
   float* pooled;       // [rows][Lk]
   uint2* cnt;          // [rows][chunks] {kept keys above T, keys equal to T} in the chunks before each
   uint2* cand;         // [rows][kResCandCap] the resolve parts' candidates (key, index)
+  // The selection in the scoring tail (dkv_tail_dev.h):
+  float* edge;         // [rows][kBndLds] raw scores around each split boundary
+  uint2* shdr;         // [rows][kFuseMaxSplits] per split {keys above the top-digit bin, candidates}
+  uint2* scand;        // [rows][Lk + kScandPad] per split's key range: its candidates (key, index)
 };
 
 inline size_t sel_al256(size_t b) { return (b + 255) & ~size_t(255); }
@@ -73,9 +83,33 @@ inline SelWs sel_layout(char* base, int64_t rows, int64_t Lk, size_t* total) {
   w.pooled = reinterpret_cast<float*>(take((size_t)rows * Lk * 4));
   w.cnt = reinterpret_cast<uint2*>(take((size_t)rows * chunks * 8));
   w.cand = reinterpret_cast<uint2*>(take((size_t)rows * kResCandCap * 8));
+  w.edge = reinterpret_cast<float*>(take((size_t)rows * kBndLds * 4));
+  w.shdr = reinterpret_cast<uint2*>(take((size_t)rows * kFuseMaxSplits * 8));
+  w.scand = reinterpret_cast<uint2*>(take((size_t)rows * (Lk + kScandPad) * 8));
   if (total) *total = off;
   return w;
 }
+
+// Sort key of a pooled value given as its bits (the buffer load's integer
+// lanes), with the protected tail mapped to kbig.
+__device__ __forceinline__ uint32_t pooled_key(uint32_t bits, int j, int prot, uint32_t kbig) {
+  if (bits == 0x80000000u) bits = 0u;
+  const uint32_t k = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+  return j >= prot ? kbig : k;
+}
+
+// The K/V gather of the emit stage: kept rows of the [B, H, L, D] sources go
+// to rows of [B, H, out_ld, D] outputs, in 16-byte units.
+struct CompactArgs {
+  const uint8_t* k;
+  const uint8_t* v;
+  int64_t sb, sh, sl;  // source byte strides
+  int H;
+  int units;           // 16-byte units per row
+  uint8_t* ko;
+  uint8_t* vo;
+  int64_t out_ld;      // rows per head in ko / vo
+};
 
 // Split geometry of the pooling stage: keys within h of j = i*kps
 // (1 <= i < n_splits) were not pooled by it (their window straddles two

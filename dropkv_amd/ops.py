@@ -273,6 +273,16 @@ def set_resident(enabled: bool = True, spin_polls: int = -1) -> None:
     _lib.check(_lib.load().dropkv_set_resident(int(bool(enabled)), int(spin_polls)), "dropkv_set_resident")
 
 
+def set_tail_select(enabled: bool = True, spin_polls: int = -1) -> None:
+    """``dropkv_set_tail_select``: whether layer-calls finish their selection
+    (threshold, ordered emit, K/V gather) in the scoring kernel's tail when
+    the call allows it (on by default) or always in two further kernels, and
+    the polls a workgroup waits at the tail's first barrier before it leaves
+    its row to the last one to arrive (``spin_polls`` < 0: unchanged; 0
+    forces that path).  Same results either way."""
+    _lib.check(_lib.load().dropkv_set_tail_select(int(bool(enabled)), int(spin_polls)), "dropkv_set_tail_select")
+
+
 class EvictPlan:
     """Pre-sized workspace and outputs for repeated layer-calls of one shape
     (``dropkv_evict``); avoids per-call allocation in tight loops."""

@@ -234,6 +234,22 @@ int dropkv_evict_ld(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int
  * ------------------------------------------------------------------------ */
 int dropkv_set_resident(int mode, int64_t spin_polls);
 
+/* Where the layer-calls' selection runs (no counterpart in the reference,
+ * whose pooling, top-k and gather are separate torch ops).  mode 1 (the
+ * default): dropkv_evict / dropkv_evict_ld / dropkv_evict_noalloc finish the
+ * selection (threshold, ordered emit of keep_idx, K/V gather) in the tail of
+ * the scoring kernel whenever the call allows it (matrix-core scoring with at
+ * most two 32-row query chunks per KV head, each split's scores in LDS, and
+ * every workgroup of the scoring grid running at once on the GPU); its
+ * workgroups then wait for one another twice per call.  mode 0: the
+ * selection always runs as two further kernels.  Both give the same
+ * results.  A workgroup that has waited spin_polls polls at the first wait
+ * (spin_polls < 0: unchanged; default 65536, a few tens of milliseconds)
+ * leaves its row to the row's last workgroup to arrive, which finishes the
+ * row alone; spin_polls = 0 forces that (tests).  Process-wide; not
+ * synchronised with calls in flight. */
+int dropkv_set_tail_select(int mode, int64_t spin_polls);
+
 /* Kernel timing with HIP events (no counterpart in the reference, which has
  * no timers).  dropkv_timing_enable(1) makes every later dropkv_scores /
  * dropkv_select / dropkv_compact / dropkv_compact2 / dropkv_evict /

@@ -36,10 +36,18 @@ def test_timing_per_kernel(gpu):
         ms = _read(lib, buf)
         torch.cuda.synchronize()
         wall = start.elapsed_time(end)
-        # score pass 1, merge, score pass 2 (+ pooling), candidates, emit + gather
-        assert len(ms) == 5
+        # score pass 1, merge, score pass 2 with the whole selection in its tail
+        assert len(ms) == 3
         assert all(0.0 < t < wall for t in ms), (ms, wall)
         assert sum(ms) <= wall * 1.001, (ms, wall)
+        # the selection as its own kernels: pass 2 (+ pooling), threshold, emit + gather
+        ops.set_tail_select(False)
+        try:
+            plan(Q, K, V)
+            ms = _read(lib, buf)
+        finally:
+            ops.set_tail_select(True)
+        assert len(ms) == 5 and all(t > 0.0 for t in ms), ms
 
         # decode: partials and merge
         B, Hq, Hkv, D, C = 1, 32, 8, 128, 256
