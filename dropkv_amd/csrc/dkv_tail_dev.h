@@ -115,6 +115,47 @@ __device__ __forceinline__ int tail_barrier_a(uint32_t* c, int S, int spin) {
   }
 }
 
+// Exclusive prefix sums of a and b over the threads of the block with their
+// totals, and the totals of c and d, in one pass (two barriers).  wsum: 4*NT/64
+// words of LDS.
+template <int NT>
+__device__ __forceinline__ void block_scan2_sum2(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t* pa,
+                                                 uint32_t* pb, uint32_t* ta, uint32_t* tb, uint32_t* tc,
+                                                 uint32_t* td, uint32_t* wsum) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint32_t xa = wave_incl_scan(a), xb = wave_incl_scan(b);
+  const uint32_t sc = wave_reduce_add(c), sd = wave_reduce_add(d);
+  __syncthreads();
+  if (lane == 63) {
+    wsum[w] = xa;
+    wsum[NW + w] = xb;
+  }
+  if (lane == 0) {
+    wsum[2 * NW + w] = sc;
+    wsum[3 * NW + w] = sd;
+  }
+  __syncthreads();
+  uint32_t oa = 0, ob = 0, sa = 0, sb = 0, s3 = 0, s4 = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    if (i < w) {
+      oa += wsum[i];
+      ob += wsum[NW + i];
+    }
+    sa += wsum[i];
+    sb += wsum[NW + i];
+    s3 += wsum[2 * NW + i];
+    s4 += wsum[3 * NW + i];
+  }
+  *pa = oa + xa - a;
+  *pb = ob + xb - b;
+  *ta = sa;
+  *tb = sb;
+  *tc = s3;
+  *td = s4;
+}
+
 // Copies nk kept rows (source row s_src[i] to output row s_dst[i]) of one
 // (batch, head) row with 16-byte units spread over the block.
 template <int NT>
@@ -162,6 +203,35 @@ __device__ __forceinline__ void tail_digits(ForCands&& for_cands, uint32_t b1, u
   const uint32_t b2 = fb[0];
   const uint32_t k2 = k1 - fb[1];
   const uint32_t pre = (b1 << kBits2) | b2;
+  const uint32_t m = hist2[b2];  // candidates left in the two top digits
+  if (m <= 64u) {
+    // Few: rank them directly (one wave, one key per lane) against each
+    // other; the k2-th largest is T.  hist3 serves as their list.
+    if (threadIdx.x == 0) fb[7] = 0u;
+    __syncthreads();
+    for_cands([&](uint32_t key, int) {
+      if ((key >> kShift2) == pre) hist3[atomicAdd(&fb[7], 1u)] = key;
+    });
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      const int l = threadIdx.x;
+      const uint32_t mine = (uint32_t)l < m ? hist3[l] : 0u;
+      uint32_t g = 0u, e = 0u;
+      for (uint32_t i = 0; i < m; ++i) {
+        const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)mine, (int)i);  // lane i's key
+        g += o > mine ? 1u : 0u;
+        e += o == mine ? 1u : 0u;
+      }
+      if ((uint32_t)l < m && g < k2 && k2 <= g + e) {
+        fb[4] = mine;
+        fb[5] = k2 - g;
+      }
+    }
+    __syncthreads();
+    *T = fb[4];
+    *take_eq = fb[5];
+    return;
+  }
   for_cands([&](uint32_t key, int) {
     if ((key >> kShift2) == pre) atomicAdd(&hist3[key & (kBins3 - 1)], 1u);
   });
@@ -264,6 +334,7 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
   // the row histogram and maximum.  Boundary i (between splits i and i+1)
   // keeps raw scores [(i+1)*kps - 2h, (i+1)*kps + 2h) (past Lk: -inf).
   for (int i = tid; i < kBins1; i += NT) hist1[i] = 0u;
+  if (tid == 0) small[127] = 0u;
   if (split > 0)
     for (int t = tid; t < w2; t += NT) {
       const int u = k_begin + t;
@@ -295,8 +366,10 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
       if (j + 1 < prot) atomicAdd(&hist1[key1 >> kShift1], 1u);
     }
   }
-  kmax = block_max_u32(kmax, small + 96);
-  if (tid == 0 && i0 < i1) atomicMax(rw + kRowMax, kmax);
+  kmax = wave_reduce_max(kmax);
+  if ((tid & 63) == 0 && kmax) atomicMax(&small[127], kmax);
+  __syncthreads();  // every wave's histogram adds and maximum are in
+  if (tid == 0 && small[127]) atomicMax(rw + kRowMax, small[127]);
   for (int i = tid; i < kBins1; i += NT)
     if (hist1[i]) atomicAdd(rw + kRowHist1 + i, hist1[i]);
 
@@ -324,7 +397,11 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
 #pragma unroll
     for (int k = 0; k < kEdge4; ++k)
       if (tid + k * NT < n4) reinterpret_cast<u32x4*>(U)[tid + k * NT] = ev[k];
-    if (tid == 0) small[121] = rm;
+    if (tid == 0) {
+      small[121] = rm;   // row maximum, then with the boundary keys
+      small[124] = 0u;   // slots taken in the candidate regions / in s_pot
+      small[125] = 0u;
+    }
   }
   __syncthreads();
   const uint32_t rmax = small[121];
@@ -344,11 +421,16 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
       if (own || alone) st_dev(reinterpret_cast<uint32_t*>(prow + j), __float_as_uint(m));
     }
   }
-  const uint32_t gmax = block_max_u32(max(bmax, rmax), small + 96);
-  const uint32_t kbig = float_key(key_float(gmax) + 1.0f);
-  if (tid == 0) hist1[kbig >> kShift1] += (uint32_t)fz.window;
+  bmax = wave_reduce_max(bmax);
+  if ((tid & 63) == 0 && bmax > rmax) atomicMax(&small[121], bmax);
   __syncthreads();
-  if (tid < 64) wave_find_bin<kBins1>(hist1, nullptr, (uint32_t)fz.keep, small + 64);
+  const uint32_t gmax = small[121];
+  const uint32_t kbig = float_key(key_float(gmax) + 1.0f);
+  if (tid < 64) {
+    // (one wave: its own LDS operations stay in order)
+    if (tid == 0) hist1[kbig >> kShift1] += (uint32_t)fz.window;
+    wave_find_bin<kBins1>(hist1, nullptr, (uint32_t)fz.keep, small + 64);
+  }
   __syncthreads();
   const uint32_t b1 = small[64];
   const uint32_t k1 = (uint32_t)fz.keep - small[65];
@@ -395,8 +477,20 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
     na += d > b1 ? 1u : 0u;
     nc += d == b1 ? 1u : 0u;
   }
-  uint32_t pc, pp, nc_all, np_all;
-  block_excl_scan2<NT>(nc, na + nc, &pc, &pp, &nc_all, &np_all, small);
+  // Slots: a wave-wide prefix, then one LDS atomic per wave.
+  uint32_t pc, pp;
+  {
+    const uint32_t ic = wave_incl_scan(nc), ip = wave_incl_scan(na + nc);
+    const uint32_t tc = (uint32_t)__builtin_amdgcn_readlane((int)ic, 63);
+    const uint32_t tp = (uint32_t)__builtin_amdgcn_readlane((int)ip, 63);
+    uint32_t bc = 0u, bp = 0u;
+    if ((tid & 63) == 0) {
+      if (tc) bc = atomicAdd(&small[124], tc);
+      if (tp) bp = atomicAdd(&small[125], tp);
+    }
+    pc = (uint32_t)__builtin_amdgcn_readfirstlane((int)bc) + ic - nc;
+    pp = (uint32_t)__builtin_amdgcn_readfirstlane((int)bp) + ip - (na + nc);
+  }
   if (na + nc) {
     for (int j = k_begin + tid; j < k_end; j += NT) {
       const uint32_t key = j >= prot ? kbig : float_key(pl[j - k_begin]);
@@ -408,14 +502,17 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
       }
     }
   }
-  if (tid == 0)
-    st_dev(reinterpret_cast<uint64_t*>(hdr + split), (uint64_t)(np_all - nc_all) | ((uint64_t)nc_all << 32));
 
   // B.  The K/V rows of the first keys of s_pot are loaded into registers
   // right after the arrival (workgroup barriers do not wait for them).
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (tid == 0) atomicAdd(rw + kRowBarB, 1u);
+  const uint32_t nc_all = small[124], np_all = small[125];
+  if (tid == 0) {
+    st_dev(reinterpret_cast<uint64_t*>(hdr + split), (uint64_t)(np_all - nc_all) | ((uint64_t)nc_all << 32));
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    atomicAdd(rw + kRowBarB, 1u);
+  }
   const CompactArgs& ca = fz.ca;
   const int units = ca.units;
   const int pre_rows = min((int)np_all, kPre * NT / units);
@@ -446,36 +543,65 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
   // 3. One round trip: every split's header and its first `peek`
   // candidates (read blindly; kPeekTotal entries in all, the region is
   // padded for the last split).
-  const int peek = min(kps, kPeekTotal / S);
-  const uint2 hv = tid < S ? ld_dev(hdr + tid) : make_uint2(0u, 0u);
+  const int lpeek = 31 - __clz(min(kps, kPeekTotal / S));  // peek: a power of two
+  const int peek = 1 << lpeek;
+  constexpr int kHdrPer = kFuseMaxSplits / 64;  // split headers per lane of wave 0
+  uint2 hv[kHdrPer];
+  if (tid < 64) {
+#pragma unroll
+    for (int q = 0; q < kHdrPer; ++q) {
+      const int sp = kHdrPer * tid + q;
+      hv[q] = sp < S ? ld_dev(hdr + sp) : make_uint2(0u, 0u);
+    }
+  }
   uint2 pk[kPeekPer];
   const int npk = S * peek;
 #pragma unroll
   for (int k = 0; k < kPeekPer; ++k) {
     const int e = tid + k * NT;
-    if (e < npk) pk[k] = ld_dev(cregion + (e / peek) * kps + e % peek);
+    if (e < npk) pk[k] = ld_dev(cregion + (e >> lpeek) * kps + (e & (peek - 1)));
   }
-  if (tid < S) {
-    abv[tid] = hv.x;
-    ncs[tid] = hv.y;
-  }
-  uint32_t off, unused2, ncand, unused3;
-  block_excl_scan2<NT>(tid < S ? hv.y : 0u, 0u, &off, &unused2, &ncand, &unused3, small);
-  if (tid < S) {
-    soff[tid] = off;
-    if (hv.y > (uint32_t)peek) small[122] = 1u;
+  if (tid < 64) {
+    // Split counts -> first slots, by one wave (splits kHdrPer*lane ..).
+    uint32_t n = 0u;
+    bool over = false;
+#pragma unroll
+    for (int q = 0; q < kHdrPer; ++q) {
+      n += hv[q].y;
+      over |= hv[q].y > (uint32_t)peek;
+    }
+    const uint32_t inc = wave_incl_scan(n);
+    uint32_t run = inc - n;
+#pragma unroll
+    for (int q = 0; q < kHdrPer; ++q) {
+      const int sp = kHdrPer * tid + q;
+      if (sp < S) {
+        abv[sp] = hv[q].x;
+        ncs[sp] = hv[q].y;
+        soff[sp] = run;
+      }
+      run += hv[q].y;
+    }
+    if (tid == 63) small[126] = inc;
+    if (__ballot(over)) small[122] = 1u;
   }
   __syncthreads();
+  const uint32_t ncand = small[126];
   const bool in_lds = ncand <= (uint32_t)kFuseCandCap;
   uint2* cl = reinterpret_cast<uint2*>(U);  // the boundary raw scores are dead
   if (in_lds) {
+    uint32_t pn[kPeekPer], po[kPeekPer];
+#pragma unroll
+    for (int k = 0; k < kPeekPer; ++k) {
+      const int sp = min((tid + k * NT) >> lpeek, S - 1);
+      pn[k] = ncs[sp];
+      po[k] = soff[sp];
+    }
 #pragma unroll
     for (int k = 0; k < kPeekPer; ++k) {
       const int e = tid + k * NT;
-      if (e < npk) {
-        const int sp = e / peek, i = e % peek;
-        if ((uint32_t)i < ncs[sp]) cl[soff[sp] + i] = pk[k];
-      }
+      const uint32_t i = (uint32_t)(e & (peek - 1));
+      if (e < npk && i < pn[k]) cl[po[k] + i] = pk[k];
     }
     // Splits with more candidates than were peeked: the rest (a second round trip).
     if (small[122])
@@ -509,8 +635,8 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
     }
   });
   for (int sp = tid; sp < split; sp += NT) cgt += abv[sp];
-  uint32_t gt0, eq0;
-  block_sum2<NT>(cgt, ceq, &gt0, &eq0, small);
+  // (their block totals come out of the first emit round's scan)
+  uint32_t gt0 = 0u, eq0 = 0u;
   // Output rows of this split's keys (pos_of), then the prefetched rows
   // stored where they go and the rest of the kept rows copied.
   const uint32_t keep = (uint32_t)fz.keep;
@@ -529,7 +655,10 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
       }
     }
     uint32_t pg, pe, tg, te;
-    block_excl_scan2<NT>(ng, ne, &pg, &pe, &tg, &te, small);
+    if (r0 == k_begin)
+      block_scan2_sum2<NT>(ng, ne, cgt, ceq, &pg, &pe, &tg, &te, &gt0, &eq0, small);
+    else
+      block_excl_scan2<NT>(ng, ne, &pg, &pe, &tg, &te, small);
     uint32_t g_before = gt0 + pg, e_before = eq0 + pe;
 #pragma unroll
     for (int i = 0; i < kEmitPer; ++i) {
