@@ -280,7 +280,12 @@ def main():
     bytes_alg = 2 * B * Hkv * Lk * D * 2
     value = bytes_alg / (ms_per_step * 1e-3) / 1e9
     dom = max((s for s in STREAM_STAGES if s in kernel_us), key=lambda s: kernel_us[s])
-    achieved = bytes_alg / (kernel_us[dom] * 1e-6) / 1e9
+    # The longest kernel's own algorithmic bytes: K and V once; with the
+    # selection in its tail also the kept K/V rows it gathers (read and
+    # written: 4 * keep * D * 2 bytes per head).
+    gather_bytes = 4 * B * Hkv * keep * D * 2
+    dom_bytes = bytes_alg + (gather_bytes if dom == "pass2_scores_select" else 0)
+    achieved = dom_bytes / (kernel_us[dom] * 1e-6) / 1e9
     # Each stream kernel does two GEMM-equivalents of 2*M*D flop per key and
     # head (QK^T and P.V in pass 1; QK^T and Y.V^T in pass 2): arithmetic
     # intensity 2*M flop per K/V byte against the ridge peak_mfma / peak_hbm.
@@ -324,7 +329,7 @@ def main():
                          "runtime), mean over the steps",
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "bytes_per_launch": bytes_alg},
+                     "bytes_per_launch": dom_bytes},
     }
 
     # The drop-in cache itself: DropKVCache(keep_ratio, window, kernel).update
@@ -340,7 +345,8 @@ def main():
         print("[bench] cold steps", file=sys.stderr, flush=True)
         cold_ms, cold_kus = cold_steps(lib, lambda: plan(Qg, Kg, Vg), min(args.steps, 50), dev)
         cold_dom = max((s for s in STREAM_STAGES if s in cold_kus), key=lambda s: cold_kus[s])
-        cold_ach = bytes_alg / (cold_kus[cold_dom] * 1e-6) / 1e9
+        cold_ach = (bytes_alg + (gather_bytes if cold_dom == "pass2_scores_select" else 0)) / (
+            cold_kus[cold_dom] * 1e-6) / 1e9
         out["cold"] = {"ms_per_step": round(cold_ms, 5), "value": round(bytes_alg / (cold_ms * 1e-3) / 1e9, 2),
                        "unit": "GB/s", "pct_hbm_peak": round(100.0 * bytes_alg / (cold_ms * 1e-3) / 1e9
                                                              / HBM_PEAK_GBPS, 2),
@@ -396,7 +402,7 @@ def main():
                            "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
                            "traffic": traffic, "flops_per_launch": flops_kernel,
                            "hbm": {"achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                                   "frac": round(achieved / HBM_PEAK_GBPS, 4), "bytes_per_launch": bytes_alg}}
+                                   "frac": round(achieved / HBM_PEAK_GBPS, 4), "bytes_per_launch": dom_bytes}}
 
     # The other BASELINE configurations, measured in the same run (skipped
     # with --no-extras): C3's chunked-prefill cache flow, C4's Qwen2 layer
