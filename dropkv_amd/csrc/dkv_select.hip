@@ -14,8 +14,12 @@
 
 namespace dkv {
 
-constexpr int kSelT = 1024;           // threads per workgroup, all stages
-constexpr int kPer = kChunk / kSelT;  // keys per thread
+constexpr int kSelT = 1024;           // threads per workgroup: zero, pool
+#ifndef DKV_EMIT_T
+#define DKV_EMIT_T 256
+#endif
+constexpr int kEmitT = DKV_EMIT_T;    // threads per emit workgroup (one 1024-key chunk; 256: C5 emit 67 -> 41 us)
+constexpr int kPer = kChunk / kEmitT;  // keys per emit thread
 
 __global__ void __launch_bounds__(kSelT)
 sel_zero_kernel(uint32_t* __restrict__ p, int64_t n) {
@@ -311,7 +315,7 @@ sel_resolve_kernel(const float* __restrict__ scores, int Lk, int ks, int window,
 // order from the chunk's offsets (resolve), then (when ko is given) their
 // K/V rows are copied.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(kSelT)
+__global__ void __launch_bounds__(kEmitT)
 sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __restrict__ out_idx,
                 float* __restrict__ pooled_out, CompactArgs ca) {
   __shared__ uint32_t small[64];
@@ -348,7 +352,7 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __r
     }
   }
   uint32_t pg, pe, tg, te;
-  block_excl_scan2<kSelT>(ng, ne, &pg, &pe, &tg, &te, small);
+  block_excl_scan2<kEmitT>(ng, ne, &pg, &pe, &tg, &te, small);
   const uint32_t start = gt0 + min(eq0, take_eq);  // first output slot of this chunk
   uint32_t g_before = gt0 + pg, e_before = eq0 + pe;
 #pragma unroll
@@ -378,11 +382,11 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __r
     const uint8_t* kb = ca.k + b * ca.sb + h * ca.sh;
     const uint8_t* vb = ca.v + b * ca.sb + h * ca.sh;
     constexpr int kG = 8;  // 16-byte units of K and of V in flight per thread
-    for (int t0 = tid; t0 < total; t0 += kG * kSelT) {
+    for (int t0 = tid; t0 < total; t0 += kG * kEmitT) {
       u32x4 kv[kG], vv[kG];
 #pragma unroll
       for (int q = 0; q < kG; ++q) {
-        const int t = t0 + q * kSelT;
+        const int t = t0 + q * kEmitT;
         if (t < total) {
           const int64_t o = (int64_t)s_src[t / ca.units] * ca.sl + 16 * (t % ca.units);
           kv[q] = *reinterpret_cast<const u32x4*>(kb + o);
@@ -391,7 +395,7 @@ sel_emit_kernel(int Lk, int window, int keep, int chunks, SelWs ws, int64_t* __r
       }
 #pragma unroll
       for (int q = 0; q < kG; ++q) {
-        const int t = t0 + q * kSelT;
+        const int t = t0 + q * kEmitT;
         if (t < total) {
           const int64_t o = ((int64_t)row * ca.out_ld + s_dst[t / ca.units]) * ca.units * 16 + 16 * (t % ca.units);
           *reinterpret_cast<u32x4*>(ca.ko + o) = kv[q];
@@ -444,7 +448,7 @@ hipError_t launch_select_after_pool(const float* scores, int rows, int Lk, int k
   const int parts = (chunks + cpp - 1) / cpp;
   launch(sel_resolve_kernel, dim3((unsigned)(rows * parts)), dim3(kResT), 0, st, scores, Lk, ks, window, keep,
          chunks, parts, cpp, SplitGeom{n_splits, kps}, ws);
-  launch(sel_emit_kernel, grid, dim3(kSelT), 0, st, Lk, window, keep, chunks, ws, out_idx, pooled_out,
+  launch(sel_emit_kernel, grid, dim3(kEmitT), 0, st, Lk, window, keep, chunks, ws, out_idx, pooled_out,
          compact_args(cp));
   return hipGetLastError();
 }
