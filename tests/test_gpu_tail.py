@@ -22,6 +22,10 @@ the oracle's selection rule.
 * Repeated calls, and HIP graph replays with eager calls in between, give
   the same bits (the barrier words are cleared by the merge kernel of every
   call).
+* Edge cases of the pooling and protection geometry: a 33-wide pooling
+  window, no pooling (kernel 1), a protected tail longer than a split,
+  keep = Lk - 1, keep = 1 with nothing protected, and one KV head split 128
+  ways; each against the oracle's rule, the gather and the separate kernels.
 """
 
 import ctypes
@@ -170,3 +174,40 @@ def test_tail_repeats_and_graph_replays(gpu, tail):
         assert all(torch.equal(u, v) for u, v in zip(a, got))
         _, y = _run(tail, Q2g, K2g, V2g, W, ks, keep, plan=plan)
         assert all(torch.equal(u, v) for u, v in zip(b, y))
+
+
+EDGE_CASES = [
+    # (cfg, Lk, W, kernel_size, protect_window, keep)
+    (LLAMA_CFG, 8192, 8, 33, 8, 819),                      # wide pooling: 4h = 64 raw scores per boundary
+    (LLAMA_CFG, 8192, 8, 1, 8, 819),                       # no pooling (h = 0): no boundary keys
+    (LLAMA_CFG, 8192, 8, 11, 600, 819),                    # protected tail longer than a 256-key split
+    (LLAMA_CFG, 4096, 8, 11, 8, 4095),                     # almost every key kept
+    (LLAMA_CFG, 4096, 8, 11, 0, 1),                        # one key, nothing protected
+    (dict(B=1, Hq=8, Hkv=1, D=128), 32768, 8, 11, 8, 3276),  # one row in 128 splits
+]
+
+
+@pytest.mark.parametrize("case", range(len(EDGE_CASES)))
+def test_tail_edge_cases(gpu, tail, case):
+    cfg, Lk, W, ks, pw, keep = EDGE_CASES[case]
+    Q, K, V = make_qkv(cfg, Lk, Lk, seed=110 + case, k_scale="lognormal")
+    Qg, Kg, Vg = Q.to(gpu), K.to(gpu), V.to(gpu)
+    print(f"[tail edge] case {case} Lk {Lk} ks {ks} protect {pw} keep {keep}", flush=True)
+
+    def run():
+        plan = tail.EvictPlan(Qg, Kg, W, ks, keep, protect_window=pw, keep_scores=True)
+        idx, ko, vo = plan(Qg, Kg, Vg)
+        torch.cuda.synchronize()
+        return plan, (idx.clone(), ko.clone(), vo.clone(), plan.scores.clone())
+
+    plan, a = run()
+    assert _kernels_of(lambda: plan(Qg, Kg, Vg)) == 3
+    pooled = R.pool_protect(a[3].cpu().clone(), ks, pw)
+    assert torch.equal(a[0].cpu(), R.topk_sorted(pooled, keep))
+    rk, rv = R.gather_compressed(K, V, a[0].cpu())
+    assert torch.equal(a[1].cpu(), rk) and torch.equal(a[2].cpu(), rv)
+    tail.set_tail_select(False)
+    _, b = run()
+    tail.set_tail_select(True)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
