@@ -544,7 +544,11 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
     const bool first = c0 == 0, last = c0 + cn >= n_mc;
     // Operands of row-chunks c0 .. c0+cn-1 (written by the merge kernel in
     // LDS order): issue their loads, then the first tile's K/V loads, so both
-    // round trips overlap; the LDS writes wait only for the former.
+    // round trips overlap; the LDS writes wait only for the former.  Every
+    // wave issues its operand loads before any wave issues K/V loads (the
+    // barrier between them): otherwise the later waves' operand loads queue
+    // behind the earlier waves' 16 KB of K/V each, and the operand block
+    // reaches LDS ~2 us later.
     constexpr int SPW = (2 * OPS * 64 + NT - 1) / NT;
     const int nw = cn * OPS * 64, ns = cn * kMB * kStatWords;
     static_assert(4 * kMB * kStatWords <= NT, "one statistics word per thread");
@@ -559,9 +563,9 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
     // key's score is computed by one wave in a fixed order, so the results do
     // not depend on the assignment.
     const int tw = wv;
+    __syncthreads();  // the previous group's LDS operands and s_next are dead
     load_rows_op<T, D>(kop, krs, k_lane, tw * kTile);
     load_rows_op<T, D>(vop, vrs, k_lane, tw * kTile);
-    __syncthreads();  // the previous group's LDS operands and s_next are dead
     if (threadIdx.x == 0) s_next = WAVES;
 #pragma unroll
     for (int i = 0; i < SPW; ++i)
