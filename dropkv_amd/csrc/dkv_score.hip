@@ -33,6 +33,11 @@
 
 namespace dkv {
 
+// Makes a kernel argument live in scalar registers at this point, so that the
+// compiler issues every argument load of the prologue at once instead of one
+// dependent round trip per branch that first needs an argument.
+#define DKV_ARG_NOW(x) __asm__ volatile("" ::"s"(x))
+
 // ---------------------------------------------------------------------------
 // Pass 1: split-K flash partials.  Workgroup = (head, row-chunk, key split);
 // each of its WAVES waves streams its own 32-key tiles, issuing the loads of
@@ -476,16 +481,29 @@ merge_kernel(const float* __restrict__ part_ml, const float* __restrict__ part_y
              int Hkv, int g, int W, int Lq, u32x4* __restrict__ opblk, float* __restrict__ stblk,
              float* __restrict__ ystat, float* __restrict__ yf32, uint32_t* __restrict__ zero_ptr,
              int64_t zero_words) {
-  if (zero_ptr)
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_words;
-         i += (int64_t)gridDim.x * blockDim.x)
-      zero_ptr[i] = 0u;
+  DKV_ARG_NOW(gridDim.x);
+  DKV_ARG_NOW(part_ml);
+  DKV_ARG_NOW(part_y);
+  DKV_ARG_NOW(part_cand);
+  DKV_ARG_NOW(n_splits);
+  DKV_ARG_NOW(n_mc);
+  DKV_ARG_NOW(n_rows);
+  DKV_ARG_NOW(q);
+  DKV_ARG_NOW(q_sb);
+  DKV_ARG_NOW(q_sh);
+  DKV_ARG_NOW(q_ss);
+  DKV_ARG_NOW(M);
   // (head, padded row); a head's rows on the XCD whose pass-1 workgroups
   // wrote its partials (pass 1 maps heads to XCDs the same way).
   const int rid =
       __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x) * kMergeRows + (threadIdx.x >> 6));
   merge_row<T, D>(rid, part_ml, part_y, part_cand, n_mc, n_splits, M, n_rows, p_round, y_round, q, q_sb, q_sh,
                   q_ss, q_sd, vp, kv_ld, Lk, Hkv, g, W, Lq, opblk, stblk, ystat, yf32);
+  // Last, so that the argument loads it needs do not delay the row's first loads.
+  if (zero_ptr)
+    for (int64_t i = (int64_t)blockIdx.x * (64 * kMergeRows) + threadIdx.x; i < zero_words;
+         i += (int64_t)gridDim.x * (64 * kMergeRows))
+      zero_ptr[i] = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -515,9 +533,19 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
   float* sc_row = stat + cg * kMB * kStatWords;  // [kps] this workgroup's scores (fused pooling only)
   // Top-digit histogram of the fused pooling (after sc_row), zeroed now.
   uint32_t* hist_l = reinterpret_cast<uint32_t*>(sc_row + kps);
-  if (fz.enabled && fz.sc_lds)
-    for (int i = threadIdx.x; i < kBins1; i += NT) hist_l[i] = 0u;
 
+  DKV_ARG_NOW(gridDim.x);
+  DKV_ARG_NOW(kp);
+  DKV_ARG_NOW(vp);
+  DKV_ARG_NOW(opblk);
+  DKV_ARG_NOW(stblk);
+  DKV_ARG_NOW(n_splits);
+  DKV_ARG_NOW(kps);
+  DKV_ARG_NOW(kv_ld);
+  DKV_ARG_NOW(Lk);
+  DKV_ARG_NOW(n_mc);
+  DKV_ARG_NOW(cg);
+  DKV_ARG_NOW(g);
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   const int split = lid % n_splits;
   const int head = lid / n_splits;
@@ -567,6 +595,9 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
     load_rows_op<T, D>(kop, krs, k_lane, tw * kTile);
     load_rows_op<T, D>(vop, vrs, k_lane, tw * kTile);
     if (threadIdx.x == 0) s_next = WAVES;
+    // The pooling histogram, zeroed once the first loads are out.
+    if (first && fz.enabled && fz.sc_lds)
+      for (int i = threadIdx.x; i < kBins1; i += NT) hist_l[i] = 0u;
 #pragma unroll
     for (int i = 0; i < SPW; ++i)
       if ((int)threadIdx.x + i * NT < nw) opnd[threadIdx.x + i * NT] = sv[i];
