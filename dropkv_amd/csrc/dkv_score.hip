@@ -228,6 +228,9 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
       *reinterpret_cast<f32x4*>(wbuf + ((size_t)wv * kRows + 16 * mb + li) * kYPitch + 16 * dt + 4 * lg) =
           yacc[dt][mb];
   __syncthreads();
+  // The partials go out with write-through stores (st_dev): none of them is
+  // left dirty in the L2 for the write-back at the end of the kernel, which
+  // the merge kernel's start waits for.
   const int64_t slot = ((int64_t)head * n_mc + mc) * n_splits + split;
   if (threadIdx.x < kRows) {
     const int row = threadIdx.x;
@@ -240,14 +243,15 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
       sm_f[w * kRows + row] = f;
       l += sm_l[w * kRows + row] * f;
     }
-    part_ml[(slot * kRows + row) * 2 + 0] = mx;
-    part_ml[(slot * kRows + row) * 2 + 1] = l;
+    st_dev(&part_ml[(slot * kRows + row) * 2 + 0], mx);
+    st_dev(&part_ml[(slot * kRows + row) * 2 + 1], l);
     float cs[kCand];
     int ck[kCand];
     merge_wave_cands<WAVES>(sm_cs, sm_ck, row, cs, ck);
 #pragma unroll
     for (int j = 0; j < kCand; ++j)
-      part_cand[(slot * kRows + row) * kCand + j] = make_int2(ck[j], __float_as_int(cs[j]));
+      st_dev(reinterpret_cast<uint64_t*>(&part_cand[(slot * kRows + row) * kCand + j]),
+             ((uint64_t)(uint32_t)__float_as_int(cs[j]) << 32) | (uint32_t)ck[j]);
   }
   __syncthreads();
   float* py = part_y + slot * kRows * D;
@@ -256,7 +260,7 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     float y = 0.f;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) y += wbuf[((size_t)w * kRows + row) * kYPitch + d] * sm_f[w * kRows + row];
-    py[i] = y;
+    st_dev(py + i, y);
   }
 }
 

@@ -157,7 +157,10 @@ __device__ __forceinline__ void block_scan2_sum2(uint32_t a, uint32_t b, uint32_
 }
 
 // Copies nk kept rows (source row s_src[i] to output row s_dst[i]) of one
-// (batch, head) row with 16-byte units spread over the block.
+// (batch, head) row with 16-byte units spread over the block.  The outputs
+// here and in fused_tail are written with non-temporal stores: they stream
+// to memory instead of waiting, dirty in the L2, for the write-back at the
+// end of the kernel.
 template <int NT>
 __device__ __forceinline__ void tail_gather(const CompactArgs& ca, int row, int nk, const int* s_src,
                                             const int* s_dst) {
@@ -182,8 +185,8 @@ __device__ __forceinline__ void tail_gather(const CompactArgs& ca, int row, int 
       const int t = t0 + q * NT;
       if (t < total) {
         const int64_t o = ((int64_t)row * ca.out_ld + s_dst[t / ca.units]) * ca.units * 16 + 16 * (t % ca.units);
-        *reinterpret_cast<u32x4*>(ca.ko + o) = kv[q];
-        *reinterpret_cast<u32x4*>(ca.vo + o) = vv[q];
+        __builtin_nontemporal_store(kv[q], reinterpret_cast<u32x4*>(ca.ko + o));
+        __builtin_nontemporal_store(vv[q], reinterpret_cast<u32x4*>(ca.vo + o));
       }
     }
   }
@@ -669,7 +672,7 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
         if (gt || (eq && e_before < take_eq)) {
           const uint32_t p = g_before + min(e_before, take_eq);
           if (p < keep) {
-            fz.out_idx[(int64_t)row * keep + p] = j;
+            __builtin_nontemporal_store((int64_t)j, &fz.out_idx[(int64_t)row * keep + p]);
             pos = (int)p;
           }
         }
@@ -690,8 +693,8 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
       const int p = pos_of[s_pot[u / units] - k_begin];
       if (p >= 0) {
         const int64_t o = (orow + p) * units * 16 + 16 * (u % units);
-        *reinterpret_cast<u32x4*>(ca.ko + o) = kpre[q];
-        *reinterpret_cast<u32x4*>(ca.vo + o) = vpre[q];
+        __builtin_nontemporal_store(kpre[q], reinterpret_cast<u32x4*>(ca.ko + o));
+        __builtin_nontemporal_store(vpre[q], reinterpret_cast<u32x4*>(ca.vo + o));
       }
     }
   }
@@ -701,8 +704,8 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
     if (p >= 0) {
       const int64_t os = (int64_t)j * ca.sl + 16 * (u % units);
       const int64_t o = (orow + p) * units * 16 + 16 * (u % units);
-      *reinterpret_cast<u32x4*>(ca.ko + o) = *reinterpret_cast<const u32x4*>(kbase + os);
-      *reinterpret_cast<u32x4*>(ca.vo + o) = *reinterpret_cast<const u32x4*>(vbase + os);
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(kbase + os), reinterpret_cast<u32x4*>(ca.ko + o));
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(vbase + os), reinterpret_cast<u32x4*>(ca.vo + o));
     }
   }
 }
