@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libdropkv_amd.so")
-SOURCES = ["dkv_score.hip", "dkv_resident.hip", "dkv_generic.hip", "dkv_select.hip", "dkv_compact.hip", "dkv_decode.hip", "dkv_capi.hip"]
+SOURCES = ["dkv_score.hip", "dkv_generic.hip", "dkv_select.hip", "dkv_compact.hip", "dkv_decode.hip", "dkv_capi.hip"]
 ARCH = os.environ.get("DROPKV_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

@@ -57,8 +57,7 @@ _SIGNATURES = {
                                  _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp, _c_size, _c_vp]),
     "dropkv_append": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
-    "dropkv_set_resident": (_c_int, [_c_int, _c_i64]),
-    "dropkv_set_tail_select": (_c_int, [_c_int, _c_i64]),
+    "dropkv_set_tail_select": (_c_int, [_c_int, _c_i64, _c_i64]),
     "dropkv_timing_enable": (_c_int, [_c_int]),
     "dropkv_timing_read": (_c_int, [ctypes.POINTER(ctypes.c_double), _c_int]),
     "dropkv_selftest_mfma": (_c_int, [_c_vp, _c_vp]),
@@ -77,6 +76,10 @@ NOALLOC_SCRATCH_BYTES = 32 << 20
 # Leading bytes of a dropkv_evict workspace that must be zero when the
 # workspace is first used (DROPKV_SYNC_BYTES in include/dropkv_amd.h).
 SYNC_BYTES = 4096
+
+# Largest head dimension the scoring kernels take (the generic kernels'
+# limit; include/dropkv_amd.h, dropkv_scores).
+MAX_HEAD_DIM = 4096
 
 _lib = None
 _lock = threading.Lock()
@@ -113,8 +116,9 @@ _head_dims = None
 
 def supported_head_dims() -> tuple[int, ...]:
     """Head dimensions of the matrix-core scoring kernels (asked once; the
-    library does not change while loaded).  Other head dimensions up to 512
-    and fp32 inputs are scored by the library's generic kernels."""
+    library does not change while loaded).  Other head dimensions up to
+    ``MAX_HEAD_DIM`` and fp32 inputs are scored by the library's generic
+    kernels."""
     global _head_dims
     if _head_dims is None:
         buf = (_c_i64 * 16)()

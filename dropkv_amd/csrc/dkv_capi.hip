@@ -42,6 +42,15 @@ int64_t elem_size(int dtype) { return dtype == DROPKV_FP32 ? 4 : 2; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Whether the plan's 32-bit counts hold: query rows B*Hq*W (the generic
+// grid, g*W as the plan's M) and keys B*Hkv*Lk (grids and row offsets of the
+// selection).  Larger shapes (K/V of 512 GB and more, or billions of window
+// rows) are refused, not wrapped around.
+bool shape_counts_fit(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t W) {
+  const double rows = (double)B * (double)Hq * (double)W, keys = (double)B * (double)Hkv * (double)Lk;
+  return rows <= (double)INT32_MAX && keys <= (double)INT32_MAX;
+}
+
 int check_score_args(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
                      int64_t Lq, int64_t Lk, int64_t D, int64_t W) {
   if (!q || !k || !v) return fail(DROPKV_E_ARG, "null q/k/v pointer");
@@ -55,6 +64,8 @@ int check_score_args(const void* q, const void* k, const void* v, int dtype, int
   if (Lk < W) return fail(DROPKV_E_ARG, "Lk (%lld) must be >= window_size (%lld)", (long long)Lk, (long long)W);
   if (Lq > Lk) return fail(DROPKV_E_ARG, "Lq (%lld) must be <= Lk (%lld)", (long long)Lq, (long long)Lk);
   if (Lk > kMaxLk) return fail(DROPKV_E_UNSUPPORTED, "Lk (%lld) too large", (long long)Lk);
+  if (!shape_counts_fit(B, Hq, Hkv, Lk, W))
+    return fail(DROPKV_E_UNSUPPORTED, "B*Hq*W or B*Hkv*Lk above %d", INT32_MAX);
   if (D < 1) return fail(DROPKV_E_ARG, "head dim must be positive");
   if (dkv::scores_generic(dtype, D, (Hq / Hkv) * W) && D > dkv::generic_max_head_dim())
     return fail(DROPKV_E_UNSUPPORTED, "head dim %lld above %lld", (long long)D, (long long)dkv::generic_max_head_dim());
@@ -104,6 +115,7 @@ int dropkv_supported_head_dims(int64_t* out, int cap) {
 size_t dropkv_scores_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_t D, int64_t W,
                                      int64_t splits) {
   if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || W < 1 || Lk < 1 || D < 1) return 0;
+  if (Lk > kMaxLk || !shape_counts_fit(B, Hq, Hkv, Lk, W)) return 0;
   return dkv::make_score_plan(B, Hq, Hkv, Lk, D, W, splits).total;
 }
 
@@ -119,12 +131,6 @@ int dropkv_scores(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64
   if (!workspace || workspace_bytes < p.total)
     return fail(DROPKV_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", p.total, workspace_bytes);
   timing_start(static_cast<hipStream_t>(stream));
-  int rs = 0, rkpw = 0;
-  if (!dkv::scores_generic(dtype, D, p.M) && dkv::resident_plan(dtype, D, p.M, B * Hkv, Lk, splits, &rs, &rkpw))
-    return hip_status(dkv::launch_resident(p, dtype, rs, rkpw, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Lk, (int)Hkv,
-                                           (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, scores,
-                                           static_cast<char*>(workspace), nullptr, static_cast<hipStream_t>(stream)),
-                      "dropkv_scores launch");
   return hip_status(dkv::launch_scores(p, dtype, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)Lk,
                                        (int)Hkv, (int)Lq, (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, scores,
                                        static_cast<char*>(workspace), nullptr, 0, nullptr,
@@ -145,7 +151,7 @@ int dropkv_scores_debug_state(const void* workspace, int64_t B, int64_t Hq, int6
 }
 
 size_t dropkv_select_workspace_bytes(int64_t rows, int64_t Lk) {
-  if (rows < 1 || Lk < 1) return 0;
+  if (rows < 1 || Lk < 1 || Lk > kMaxLk || (double)rows * (double)Lk > (double)INT32_MAX) return 0;
   return dkv::select_workspace_bytes(rows, Lk);
 }
 
@@ -154,9 +160,10 @@ static int check_select_args(const float* scores, int64_t rows, int64_t Lk, int6
   if (!scores || !keep_idx) return fail(DROPKV_E_ARG, "null scores/keep_idx pointer");
   if (rows < 1 || Lk < 1) return fail(DROPKV_E_ARG, "rows and Lk must be positive");
   if (rows > 65535 * 64) return fail(DROPKV_E_UNSUPPORTED, "too many rows");
+  if ((double)rows * (double)Lk > (double)INT32_MAX) return fail(DROPKV_E_UNSUPPORTED, "rows*Lk above %d", INT32_MAX);
   if (Lk > dkv::select_max_len()) return fail(DROPKV_E_UNSUPPORTED, "Lk (%lld) too large", (long long)Lk);
   if (ks < 1 || ks % 2 == 0) return fail(DROPKV_E_ARG, "kernel_size must be a positive odd integer");
-  if (ks > 129) return fail(DROPKV_E_UNSUPPORTED, "kernel_size above 129 is not supported");
+  if (ks > INT32_MAX) return fail(DROPKV_E_UNSUPPORTED, "kernel_size too large");
   if (window < 0 || window > Lk) return fail(DROPKV_E_ARG, "window must be in [0, Lk]");
   if (keep < 1 || keep > Lk) return fail(DROPKV_E_ARG, "keep (%lld) must be in [1, Lk=%lld]", (long long)keep,
                                          (long long)Lk);
@@ -256,37 +263,25 @@ static int evict_impl(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, i
     return fail(DROPKV_E_UNSUPPORTED, "outputs with a row capacity need 16-byte aligned rows");
   timing_start(st);
   const dkv::SelectCompact cp{k, v, Hkv * kv_ld * D, kv_ld * D, D, eb, D, (int)Hkv, k_out, v_out, out_ld};
-  // The resident kernel (pass 1, merge and pass 2 in one, K/V streamed
-  // once) when the call fits on chip; otherwise the streaming passes.
   // Pooling runs in the tail of the scoring pass when the plan allows it
   // (the matrix-core kernels only); otherwise as the standalone selection's
-  // pool kernel.
-  const bool mfma = !dkv::scores_generic(dtype, D, p.M);
-  int rs = 0, rkpw = 0;
-  const bool resident = mfma && dkv::resident_plan(dtype, D, p.M, B * Hkv, Lk, splits, &rs, &rkpw) &&
-                        dkv::select_after_pool_ok(rs, rkpw, Lk, kernel_size);
-  const bool fused = resident || (mfma && dkv::select_after_pool_ok(p.s2, p.kps2, Lk, kernel_size));
-  // With the resident kernel, and where pass 2 cannot run it in its tail,
+  // pool kernel.  Where pass 2 cannot run the whole selection in its tail,
   // the selection continues in its own kernels after the scores.
+  const bool mfma = !dkv::scores_generic(dtype, D, p.M);
+  const bool fused = mfma && dkv::select_after_pool_ok(p.s2, p.kps2, Lk, kernel_size);
   int tail_done = 0;
   const dkv::FuseSelect fs{sel_ws,   (int)kernel_size,        (int)protect_window, (int)keep,
-                           keep_idx, vec ? &cp : nullptr, resident ? nullptr : &tail_done};
-  hipError_t e;
-  if (resident)
-    e = dkv::launch_resident(p, dtype, rs, rkpw, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)kv_ld, (int)Hkv, (int)Lq,
-                             (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws, &fs, st);
-  else
-    e = dkv::launch_scores(p, dtype, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)kv_ld, (int)Hkv, (int)Lq,
-                           (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws,
-                           reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv),
-                           fused ? &fs : nullptr, st);
+                           keep_idx, vec ? &cp : nullptr, &tail_done};
+  hipError_t e = dkv::launch_scores(p, dtype, (int)D, q, q_sb, q_sh, q_ss, q_sd, k, v, (int)kv_ld, (int)Hkv, (int)Lq,
+                                    (int)Lk, (int)W, eps, p_round ? 1 : 0, y_round ? 1 : 0, sc, ws,
+                                    reinterpret_cast<uint32_t*>(sel_ws), dkv::select_zero_words(B * Hkv),
+                                    fused ? &fs : nullptr, st);
   if (e != hipSuccess) return hip_status(e, "dropkv_evict scores");
   if (tail_done)
     e = hipSuccess;
   else if (fused)
     e = dkv::launch_select_after_pool(sc, (int)(B * Hkv), (int)Lk, (int)kernel_size, (int)protect_window, (int)keep,
-                                      resident ? rs : p.s2, resident ? rkpw : p.kps2, keep_idx, nullptr, sel_ws,
-                                      vec ? &cp : nullptr, st);
+                                      p.s2, p.kps2, keep_idx, nullptr, sel_ws, vec ? &cp : nullptr, st);
   else
     e = dkv::launch_select(sc, (int)(B * Hkv), (int)Lk, (int)kernel_size, (int)protect_window, (int)keep, keep_idx,
                            nullptr, sel_ws, true, vec ? &cp : nullptr, st);
@@ -398,19 +393,12 @@ int dropkv_append(const void* k, const void* v, int64_t s_b, int64_t s_h, int64_
                     "dropkv_append launch");
 }
 
-static_assert(DROPKV_SYNC_BYTES == dkv::kResSyncBytes, "the header's sync area is the plan's");
+static_assert(DROPKV_SYNC_BYTES == dkv::kSyncBytes, "the header's sync area is the plan's");
 
-int dropkv_set_resident(int mode, int64_t spin_polls) {
+int dropkv_set_tail_select(int mode, int64_t spin_polls, int64_t spin_polls_b) {
   if (mode != 0 && mode != 1) return fail(DROPKV_E_ARG, "mode must be 0 or 1");
-  if (spin_polls > INT32_MAX) return fail(DROPKV_E_ARG, "spin_polls too large");
-  dkv::set_resident(mode, spin_polls < 0 ? -1 : (int)spin_polls);
-  return DROPKV_OK;
-}
-
-int dropkv_set_tail_select(int mode, int64_t spin_polls) {
-  if (mode != 0 && mode != 1) return fail(DROPKV_E_ARG, "mode must be 0 or 1");
-  if (spin_polls > INT32_MAX) return fail(DROPKV_E_ARG, "spin_polls too large");
-  dkv::set_tail_select(mode, spin_polls < 0 ? -1 : (int)spin_polls);
+  if (spin_polls > INT32_MAX || spin_polls_b > INT32_MAX) return fail(DROPKV_E_ARG, "spin_polls too large");
+  dkv::set_tail_select(mode, spin_polls < 0 ? -1 : (int)spin_polls, spin_polls_b < 0 ? -1 : (int)spin_polls_b);
   return DROPKV_OK;
 }
 

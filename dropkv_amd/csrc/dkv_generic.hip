@@ -24,11 +24,14 @@
 namespace dkv {
 
 constexpr int kGenThreads = 256;
-constexpr int kGenMaxD = 512;
-constexpr int kGenLdsRowFloats = 4096;  // q + y rows staged per pass of the score kernel: 32 KiB of LDS
+constexpr int kGenMaxD = 4096;
+constexpr int kGenCols = kGenMaxD / kGenThreads;  // y columns per thread of the stats kernel (at most)
 
-// Query rows per pass of the score kernel: as many as fit kGenLdsRowFloats.
-constexpr int gen_rows(int D) { return D <= 64 ? 32 : D <= 128 ? 16 : D <= 256 ? 8 : 4; }
+// Query rows per pass of the score kernel: R rows of q and of y in 4096
+// floats of LDS (16 KiB), at least one (2*D floats for D above 2048).
+constexpr int gen_rows(int D) {
+  return D <= 64 ? 32 : D <= 128 ? 16 : D <= 256 ? 8 : D <= 512 ? 4 : D <= 1024 ? 2 : 1;
+}
 
 template <typename T>
 __device__ __forceinline__ float ld(const T* p) {
@@ -90,7 +93,9 @@ gen_stats_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_
   const float lse = mr + __logf(s);
 
   // Sweep 2: y = sum_j p_j v_j with the final p, 256 keys at a time.
-  float y0 = 0.f, y1 = 0.f;  // columns tid and tid + 256
+  float y[kGenCols];  // columns tid + 256 c
+#pragma unroll
+  for (int c = 0; c < kGenCols; ++c) y[c] = 0.f;
   for (int j0 = 0; j0 <= bound; j0 += kGenThreads) {
     const int j = j0 + tid;
     float p = 0.f;
@@ -105,17 +110,15 @@ gen_stats_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_
     for (int u = 0; u < n; ++u) {
       const float pu = ps[u];
       const T* vr = vh + (int64_t)(j0 + u) * D;
-      if (tid < D) y0 = fmaf(pu, ld(vr + tid), y0);
-      if (tid + kGenThreads < D) y1 = fmaf(pu, ld(vr + tid + kGenThreads), y1);
+#pragma unroll
+      for (int c = 0; c < kGenCols; ++c)
+        if (tid + c * kGenThreads < D) y[c] = fmaf(pu, ld(vr + tid + c * kGenThreads), y[c]);
     }
   }
-  if (y_round) {
-    y0 = round_through<T>(y0);
-    y1 = round_through<T>(y1);
-  }
   const int64_t rbase = (int64_t)head * mpad + m;
-  if (tid < D) yf32[rbase * D + tid] = y0;
-  if (tid + kGenThreads < D) yf32[rbase * D + tid + kGenThreads] = y1;
+#pragma unroll
+  for (int c = 0; c < kGenCols; ++c)
+    if (tid + c * kGenThreads < D) yf32[rbase * D + tid + c * kGenThreads] = y_round ? round_through<T>(y[c]) : y[c];
   if (tid == 0) {
     ystat[rbase * 2 + 0] = lse * 1.4426950408889634f;  // log2 units, as the matrix-core merge stores it
     ystat[rbase * 2 + 1] = lse;                         // natural units, read by gen_score_kernel
@@ -128,9 +131,11 @@ gen_score_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_
                  const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int Hkv, int Lq, int Lk, int D, int W,
                  int g, int M, int mpad, float scale, float eps, int p_round, const float* __restrict__ ystat,
                  const float* __restrict__ yf32, float* __restrict__ scores) {
-  __shared__ float qs[kGenLdsRowFloats / 2];  // R query rows of D
-  __shared__ float ys[kGenLdsRowFloats / 2];  // R y rows of D
-  __shared__ float ls[R];                     // their lse
+  // R query rows of D, then R y rows of D (dynamic LDS).
+  extern __shared__ float gen_lds[];
+  float* qs = gen_lds;
+  float* ys = gen_lds + R * D;
+  __shared__ float ls[R];  // their lse
   const int tid = threadIdx.x;
   const int tiles = (Lk + kGenThreads - 1) / kGenThreads;
   const int head = blockIdx.x / tiles;
@@ -196,15 +201,18 @@ static hipError_t launch_generic_t(const ScorePlan& p, int D, const void* q, int
   launch(gen_stats_kernel<T>, dim3(p.heads * p.M), dim3(kGenThreads), 0, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv,
          kv_ld, Hkv, Lq, Lk, D, W, p.g, p.M, p.mpad, scale, p_round, y_round, ystat, yf, zero_ptr, zero_words);
   const int tiles = (Lk + kGenThreads - 1) / kGenThreads;
+  const size_t lds = (size_t)2 * gen_rows(D) * D * sizeof(float);
   auto score = [&](auto kern) {
-    launch(kern, dim3(p.heads * tiles), dim3(kGenThreads), 0, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, kv_ld, Hkv,
+    launch(kern, dim3(p.heads * tiles), dim3(kGenThreads), lds, st, qq, q_sb, q_sh, q_ss, q_sd, kk, vv, kv_ld, Hkv,
            Lq, Lk, D, W, p.g, p.M, p.mpad, scale, eps, p_round, ystat, yf, scores);
   };
   switch (gen_rows(D)) {
     case 32: score(gen_score_kernel<T, 32>); break;
     case 16: score(gen_score_kernel<T, 16>); break;
     case 8: score(gen_score_kernel<T, 8>); break;
-    default: score(gen_score_kernel<T, 4>); break;
+    case 4: score(gen_score_kernel<T, 4>); break;
+    case 2: score(gen_score_kernel<T, 2>); break;
+    default: score(gen_score_kernel<T, 1>); break;
   }
   return hipGetLastError();
 }

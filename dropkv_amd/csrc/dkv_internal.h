@@ -77,25 +77,10 @@ hipError_t launch_scores(const ScorePlan& p, int dtype, int D, const void* q, in
                          int64_t q_ss, int64_t q_sd, const void* k, const void* v, int kv_ld, int Hkv, int Lq,
                          int Lk, int W, float eps, int p_round, int y_round, float* scores, char* ws,
                          uint32_t* zero_ptr, int64_t zero_words, const FuseSelect* fuse, hipStream_t st);
-// The resident layer-call (dkv_resident.hip): pass 1, merge and pass 2 in one
-// kernel that keeps V and the logits on chip, for calls that fit (D = 128,
-// one row-chunk, bf16/fp16, at most kResKeys keys per workgroup and one
-// workgroup per CU).  resident_plan gives its split geometry (S workgroups
-// of kpw keys per head) or false; its counters live in the first
-// kResSyncBytes of the score workspace (ScorePlan::off_sync), which must be
-// zero when a workspace is first used and are zero again after every call.
-constexpr int kResKeys = 1024;
-constexpr int kResMaxHeads = 256;
-constexpr size_t kResSyncBytes = (size_t)kResMaxHeads * 16;
-bool resident_plan(int dtype, int64_t D, int64_t M, int64_t heads, int64_t Lk, int64_t splits, int* S, int* kpw);
-hipError_t launch_resident(const ScorePlan& p, int dtype, int S, int kpw, const void* q, int64_t q_sb,
-                           int64_t q_sh, int64_t q_ss, int64_t q_sd, const void* k, const void* v, int kv_ld,
-                           int Hkv, int Lq, int Lk, int W, float eps, int p_round, int y_round, float* scores,
-                           char* ws, const FuseSelect* fuse, hipStream_t st);
-// mode 0: never take the resident path, 1: whenever the call fits; spin1 >= 0
-// sets the polls a workgroup waits at its first barrier before it leaves the
-// head to the last one to arrive (tests use 0 to force that path).
-void set_resident(int mode, int spin1);
+// Counters at the start of every score / evict workspace
+// (ScorePlan::off_sync): zero when a workspace is first used, and zero again
+// after every call (the DROPKV_SYNC_BYTES contract of the C ABI).
+constexpr size_t kSyncBytes = 4096;
 hipError_t launch_debug_state(const ScorePlan& p, const char* ws, int D, float* lse_out, float* y_out,
                               hipStream_t st);
 // The generic scoring kernels (fp32 arithmetic on the vector ALUs) on the
@@ -151,8 +136,10 @@ CompactArgs compact_args(const SelectCompact* cp);
 // mode 0: the selection always runs as its own kernels after the scoring
 // pass; 1: in the scoring pass's tail whenever the call allows it.  spin >= 0
 // sets the polls a workgroup waits at the tail's first barrier before it
-// leaves the row to the last one to arrive (tests use 0 to force that path).
-void set_tail_select(int mode, int spin);
+// leaves the row to the last one to arrive, spin_b >= 0 the polls at the
+// second barrier before it finishes the row alone (tests use 0 to force
+// those paths).
+void set_tail_select(int mode, int spin, int spin_b);
 hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int window, int keep, int64_t* out_idx,
                          float* pooled_out, char* ws, bool pre_zeroed, const SelectCompact* cp, hipStream_t st);
 // The resolve and emit stages after a pooling stage that pooled every key

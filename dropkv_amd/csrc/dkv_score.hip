@@ -28,6 +28,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -1123,16 +1124,10 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
     off += (bytes + 255) & ~size_t(255);
     return o;
   };
-  // The counters of the resident layer-call first, at a fixed offset, so
-  // that no other layout ever writes over them.
-  p.off_sync = take(kResSyncBytes);
-  // Partials: pass 1's splits, or the resident kernel's workgroups per head
-  // when the call could fit it (one row-chunk, at most kResMaxHeads
-  // workgroups in all).
-  const int s_res = ceil_div(Lk, kResKeys);
-  const bool res_fit = p.n_mc == 1 && (int64_t)p.heads * s_res <= kResMaxHeads;
-  const int s_part = res_fit ? std::max(p.s1, s_res) : p.s1;
-  const size_t slots = (size_t)p.heads * p.n_mc * s_part;
+  // The call counters first, at a fixed offset, so that no other layout
+  // ever writes over them.
+  p.off_sync = take(kSyncBytes);
+  const size_t slots = (size_t)p.heads * p.n_mc * p.s1;
   p.off_ml = take(slots * kRows * 2 * sizeof(float));
   p.off_y = take(slots * kRows * D * sizeof(float));
   p.off_cand = take(slots * kRows * kCand * sizeof(int2));
@@ -1145,8 +1140,11 @@ ScorePlan make_score_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Lk, int64_
 }
 
 namespace {
-int g_tail_mode = 1;         // 1: selection in pass 2's tail whenever the call allows it
-int g_tail_spin = 1 << 16;   // polls at the tail's barrier A before a workgroup gives up
+// Process-wide settings of the selection tail, read once per call (relaxed:
+// a call in flight on another thread sees either the old or the new value).
+std::atomic<int> g_tail_mode{1};          // 1: selection in pass 2's tail whenever the call allows it
+std::atomic<int> g_tail_spin{1 << 16};    // polls at the tail's barrier A before a workgroup gives up
+std::atomic<int> g_tail_spin_b{1 << 22};  // polls at barrier B before a workgroup finishes the row alone
 
 // Whether `grid` workgroups of `fn` (threads, dynamic LDS bytes) fit on the
 // current GPU at once: the tail's barriers need every workgroup of a row
@@ -1179,9 +1177,10 @@ bool tail_fits(const void* fn, int threads, size_t lds, int64_t grid) {
 }
 }  // namespace
 
-void set_tail_select(int mode, int spin) {
-  g_tail_mode = mode;
-  if (spin >= 0) g_tail_spin = spin;
+void set_tail_select(int mode, int spin, int spin_b) {
+  g_tail_mode.store(mode, std::memory_order_relaxed);
+  if (spin >= 0) g_tail_spin.store(spin, std::memory_order_relaxed);
+  if (spin_b >= 0) g_tail_spin_b.store(spin_b, std::memory_order_relaxed);
 }
 
 template <typename T, int D>
@@ -1250,13 +1249,15 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   const auto k2 = p_round ? pass2_kernel<T, D, 8, 1, true> : pass2_kernel<T, D, 8, 1, false>;
   // The whole selection in pass 2's tail: needs the scores in LDS, an
   // output to emit into, and every workgroup of the grid running at once.
-  if (fuse && fz.sc_lds && fuse->keep_idx && fuse->cp && g_tail_mode && p.s2 <= kFuseMaxSplits) {
+  if (fuse && fz.sc_lds && fuse->keep_idx && fuse->cp && g_tail_mode.load(std::memory_order_relaxed) &&
+      p.s2 <= kFuseMaxSplits) {
     const size_t lds_t = (size_t)cg * kOpSlots * kMB * (D / 32) * 64 * 16 + (size_t)cg * kMB * kStatWords * 4 +
                          (size_t)p.kps2 * 4 + (size_t)tail_lds_words(512, p.kps2) * 4;
     if (tail_fits(reinterpret_cast<const void*>(k2), 512, lds_t, (int64_t)p.heads * p.s2)) {
       fz.full = 1;
       fz.keep = fuse->keep;
-      fz.spin = g_tail_spin;
+      fz.spin = g_tail_spin.load(std::memory_order_relaxed);
+      fz.spin_b = g_tail_spin_b.load(std::memory_order_relaxed);
       fz.out_idx = fuse->keep_idx;
       fz.ca = compact_args(fuse->cp);
       lds2 = std::max(lds2, lds_t);

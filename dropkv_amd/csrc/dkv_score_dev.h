@@ -1,7 +1,6 @@
-// Device-side pieces of the DropKV scoring kernels shared by the streaming
-// passes (dkv_score.hip) and the resident layer-call (dkv_resident.hip):
-// tile geometry, the online-softmax step, operand loads, the candidate order,
-// one row of the cross-split merge and the pooling-tail parameters.
+// Device-side pieces of the DropKV scoring kernels (dkv_score.hip): tile
+// geometry, the online-softmax step, operand loads, the candidate order, one
+// row of the cross-split merge and the pooling-tail parameters.
 #pragma once
 
 #include "dkv_common.h"
@@ -297,9 +296,7 @@ constexpr float kCorrMinP = 1.0f / 4096.0f;
 constexpr float kCorrMinLog2P = -12.0f;  // log2(kCorrMinP)
 constexpr int kCorrKeys = 8;  // candidates corrected per row (the largest p)
 
-// kCoherent: every result is written with device-coherent stores (st_dev),
-// for readers in the same kernel (the resident layer-call).
-template <typename T, int D, bool kCoherent = false>
+template <typename T, int D>
 __device__ __forceinline__ void merge_row(int rid, const float* __restrict__ part_ml, const float* __restrict__ part_y,
                                           const int2* __restrict__ part_cand, int n_mc, int n_splits, int M,
                                           int n_rows, int p_round, int y_round, const T* __restrict__ q,
@@ -529,21 +526,12 @@ __device__ __forceinline__ void merge_row(int rid, const float* __restrict__ par
     return ob + ((size_t)((which * kMB + mb) * KK + kk) * 64 + li + 16 * lg) * 8 + e8;
   };
   if (col) {
-    if constexpr (kCoherent) {
-      static_assert(DPL == 2, "coherent stores pack two columns per word");
-      typedef T t2 __attribute__((ext_vector_type(2)));
-      st_dev(reinterpret_cast<uint64_t*>(yf32 + rbase * D + d0), __builtin_bit_cast(uint64_t, f32x2{ye[0], ye[1]}));
-      st_dev(reinterpret_cast<uint32_t*>(op_at(0, d0)), __builtin_bit_cast(uint32_t, t2{qe[0], qe[1]}));
-      st_dev(reinterpret_cast<uint32_t*>(op_at(1, d0)), __builtin_bit_cast(uint32_t, t2{he[0], he[1]}));
-      st_dev(reinterpret_cast<uint32_t*>(op_at(2, d0)), __builtin_bit_cast(uint32_t, t2{le[0], le[1]}));
-    } else {
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) {
-        yf32[rbase * D + d0 + e] = ye[e];
-        *op_at(0, d0 + e) = qe[e];
-        *op_at(1, d0 + e) = he[e];
-        *op_at(2, d0 + e) = le[e];
-      }
+    for (int e = 0; e < DPL; ++e) {
+      yf32[rbase * D + d0 + e] = ye[e];
+      *op_at(0, d0 + e) = qe[e];
+      *op_at(1, d0 + e) = he[e];
+      *op_at(2, d0 + e) = le[e];
     }
   }
   const float yn2 = wave_sum_dpp(ysq);
@@ -551,21 +539,12 @@ __device__ __forceinline__ void merge_row(int rid, const float* __restrict__ par
   if (lane == 0) {
     const float lse_row = valid ? lse2 : INFINITY;
     float* sb = stblk + (((int64_t)head * n_mc + mc) * kMB + row / 16) * kStatWords + (row % 16);
-    if constexpr (kCoherent) {
-      st_dev(ystat + rbase * 2 + 0, lse_row);
-      st_dev(ystat + rbase * 2 + 1, yn2);
-      st_dev(sb + 0, lse_row);
-      st_dev(sb + 16, yn2);
-      st_dev(sb + 32, __builtin_bit_cast(float, k_top));
-      st_dev(sb + 48, nd2_top);
-    } else {
-      ystat[rbase * 2 + 0] = lse_row;
-      ystat[rbase * 2 + 1] = yn2;
-      sb[0] = lse_row;
-      sb[16] = yn2;
-      sb[32] = __builtin_bit_cast(float, k_top);
-      sb[48] = nd2_top;
-    }
+    ystat[rbase * 2 + 0] = lse_row;
+    ystat[rbase * 2 + 1] = yn2;
+    sb[0] = lse_row;
+    sb[16] = yn2;
+    sb[32] = __builtin_bit_cast(float, k_top);
+    sb[48] = nd2_top;
   }
 }
 
@@ -589,6 +568,7 @@ struct SelFuse {
   int full;
   int keep;
   int spin;    // polls at the tail's barrier A before a workgroup gives up
+  int spin_b;  // polls at barrier B before a workgroup finishes the row alone
   int64_t* out_idx;
   CompactArgs ca;
 };

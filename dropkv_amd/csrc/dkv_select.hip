@@ -44,6 +44,90 @@ sel_pool_kernel(const float* __restrict__ scores, int Lk, int ks, int window, in
 }
 
 // ---------------------------------------------------------------------------
+// pool (standalone) for any kernel size, also those whose window exceeds the
+// LDS halo of sel_pool_kernel (h > kMaxHalo).  The row is cut into blocks of
+// w = 2h+1 keys (van Herk / Gil-Werman):
+//   pre[j] = max x[block start .. j],  suf[j] = max x[j .. block end]
+// (the last block ends at Lk-1).  A window [a, b] (a = max(j-h, 0),
+// b = min(j+h, Lk-1), at most w keys) meets at most two blocks, so
+//   max x[a..b] = max(suf[a], pre[b])  if a and b lie in different blocks,
+//                 pre[b]               if a starts their common block,
+//                 suf[a]               otherwise (then b = Lk-1 ends it).
+// ---------------------------------------------------------------------------
+constexpr int kWideScanT = 256;  // one wave per block of w keys
+
+__device__ __forceinline__ float wave_incl_max_scan(float x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float t = __shfl_up(x, o);
+    if (lane >= o) x = fmaxf(x, t);
+  }
+  return x;
+}
+
+// pre / suf: [rows][Lk] each (the tail's candidate regions, unused here).
+__global__ void __launch_bounds__(kWideScanT)
+sel_pool_wide_scan_kernel(const float* __restrict__ scores, int rows, int Lk, int w, int nblk,
+                          float* __restrict__ pre, float* __restrict__ suf) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = (int64_t)blockIdx.x * (kWideScanT / 64) + (threadIdx.x >> 6);
+  if (gw >= (int64_t)rows * nblk) return;
+  const int row = (int)(gw / nblk), blk = (int)(gw % nblk);
+  const int start = blk * w, end = min(start + w, Lk);  // keys [start, end)
+  const float* x = scores + (int64_t)row * Lk;
+  float* pr = pre + (int64_t)row * Lk;
+  float* sf = suf + (int64_t)row * Lk;
+  float carry = -INFINITY;
+  for (int c = start; c < end; c += 64) {
+    const int j = c + lane;
+    const float v = fmaxf(wave_incl_max_scan(j < end ? x[j] : -INFINITY), carry);
+    if (j < end) pr[j] = v;
+    carry = __shfl(v, 63);
+  }
+  carry = -INFINITY;
+  for (int c = end - 1; c >= start; c -= 64) {
+    const int j = c - lane;  // lane 0 holds the block's last key of this round
+    const float v = fmaxf(wave_incl_max_scan(j >= start ? x[j] : -INFINITY), carry);
+    if (j >= start) sf[j] = v;
+    carry = __shfl(v, 63);
+  }
+}
+
+// grid = rows * chunks: the pooled values of the chunk's keys from pre / suf,
+// into the pooled row, the row maximum and the top-digit histogram.
+__global__ void __launch_bounds__(kSelT)
+sel_pool_wide_kernel(const float* __restrict__ pre, const float* __restrict__ suf, int Lk, int h, int window,
+                     int chunks, SelWs ws) {
+  __shared__ uint32_t hist[kBins1];
+  __shared__ uint32_t red[16];
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x / chunks;
+  const int c0 = (blockIdx.x % chunks) * kChunk, c1 = min(c0 + kChunk, Lk);
+  const int w = 2 * h + 1, prot = Lk - window;
+  const float* pr = pre + (int64_t)row * Lk;
+  const float* sf = suf + (int64_t)row * Lk;
+  float* prow = ws.pooled + (int64_t)row * Lk;
+  uint32_t* rw = ws.rowws + (int64_t)row * kRowWords;
+  for (int i = tid; i < kBins1; i += kSelT) hist[i] = 0u;
+  __syncthreads();
+  uint32_t kmax = 0u;
+  for (int j = c0 + tid; j < c1; j += kSelT) {
+    const int a = max(j - h, 0), b = (int)min((int64_t)j + h, (int64_t)Lk - 1);
+    const float m = a / w != b / w ? fmaxf(sf[a], pr[b]) : (a % w == 0 ? pr[b] : sf[a]);
+    prow[j] = m;
+    const uint32_t key = float_key(m);
+    kmax = max(kmax, key);
+    if (j < prot) atomicAdd(&hist[key >> kShift1], 1u);
+  }
+  kmax = block_max_u32(kmax, red);
+  if (tid == 0 && c0 < c1) atomicMax(&rw[kRowMax], kmax);
+  __syncthreads();
+  for (int i = tid; i < kBins1; i += kSelT)
+    if (hist[i]) atomicAdd(&rw[kRowHist1 + i], hist[i]);
+}
+
+// ---------------------------------------------------------------------------
 // resolve: grid = rows * parts; part p of a row sweeps its chunks
 // [p*cpp, (p+1)*cpp).
 //   A. (every part) Pools the keys next to the scoring pass's split
@@ -463,8 +547,25 @@ hipError_t launch_select(const float* scores, int rows, int Lk, int ks, int wind
     launch(sel_zero_kernel, dim3((unsigned)std::min<int64_t>((zn + kSelT - 1) / kSelT, 1024)),
                        dim3(kSelT), 0, st, ws.rowws, zn);
   }
-  launch(sel_pool_kernel, dim3((unsigned)(rows * chunks)), dim3(kSelT), 0, st, scores, Lk, ks, window,
-                     chunks, ws);
+  const int h = ks / 2;
+  if (h <= kMaxHalo) {
+    launch(sel_pool_kernel, dim3((unsigned)(rows * chunks)), dim3(kSelT), 0, st, scores, Lk, ks, window, chunks, ws);
+  } else {
+    // Windows past the halo of sel_pool_kernel: block prefix / suffix maxima
+    // first (in the tail's candidate regions, [rows][Lk + kScandPad] entries
+    // of 8 bytes: room for both).  A window wider than the row pools like
+    // one of 2*Lk+1 keys.
+    const int hw = std::min(h, Lk);
+    const int w = 2 * hw + 1;
+    const int nblk = (Lk + w - 1) / w;
+    float* pre = reinterpret_cast<float*>(ws.scand);
+    float* suf = pre + (int64_t)rows * Lk;
+    const int64_t waves = (int64_t)rows * nblk;
+    launch(sel_pool_wide_scan_kernel, dim3((unsigned)((waves + kWideScanT / 64 - 1) / (kWideScanT / 64))),
+           dim3(kWideScanT), 0, st, scores, rows, Lk, w, nblk, pre, suf);
+    launch(sel_pool_wide_kernel, dim3((unsigned)(rows * chunks)), dim3(kSelT), 0, st, pre, suf, Lk, hw, window,
+           chunks, ws);
+  }
   return launch_select_after_pool(scores, rows, Lk, ks, window, keep, 1, Lk, out_idx, pooled_out, ws_base, cp, st);
 }
 

@@ -49,7 +49,6 @@ constexpr int kRowArrive = 4;              // resolve parts of the row that have
 constexpr int kRowNcand = 5;               // candidates the parts have found (may exceed kResCandCap)
 constexpr int kRowBarA = 8;                // selection in the scoring tail: arrivals at barrier A (| poison bit)
 constexpr int kRowBarB = 9;                //   arrivals at barrier B
-constexpr int kRowStatus = 10;             //   nonzero: barrier B's hang guard gave up
 constexpr int kRowHist1 = 16;              // top-digit histogram (unprotected interior keys), 16-byte aligned
 constexpr int kRowWords = kRowHist1 + kBins1;
 constexpr int kResCandCap = 4096;          // candidates (key, index) kept per row, in the workspace and in LDS

@@ -23,8 +23,7 @@
 //      index order and gathers their K/V rows.
 //
 // Publishing uses device-coherent stores (st_dev), a wait for them and then
-// the arrival; the waiting side polls with agent-scope loads and acquires
-// once per workgroup (as the resolve stage and the resident kernel do).
+// the arrival; the waiting side polls with agent-scope loads.
 //
 // Barrier A is the one place where a workgroup could wait for another that
 // is not running: the host takes this path only when the whole grid fits on
@@ -34,8 +33,12 @@
 // leaves, as do the others when they see the flag; the row's last workgroup
 // to arrive then finishes the row alone from the pooled row in memory (the
 // same keys, so the same result).  Barrier B is reached only by workgroups
-// that passed A together, all running; its wait is bounded as a hang guard
-// that sets the row's status word.
+// that passed A together, all running, so its wait ends; it is still bounded
+// (`spin_b` polls).  A workgroup that gives up there writes the pooled
+// values of every boundary key of the row (it has them all) and finishes the
+// whole row alone from the pooled row in memory, as at barrier A: every
+// workgroup that finishes the row, alone or not, writes the same indices and
+// rows, so the outputs are those of a call without the give-up.
 #pragma once
 
 #include "dkv_common.h"
@@ -46,7 +49,6 @@ namespace dkv {
 
 constexpr uint32_t kTailPoison = 0x80000000u;
 constexpr int kTailGo = 0, kTailLeave = 1, kTailAlone = 2;
-constexpr int kTailSpinB = 1 << 22;  // polls at barrier B before the hang guard gives up
 constexpr int kEmitPer = 4;          // consecutive keys per thread in one emit round
 constexpr int kFuseCandCap = 2048;   // candidates resolved from LDS (more: the row is swept instead)
 constexpr int kPre = 8;              // 16-byte units of K and of V per thread loaded ahead of barrier B
@@ -455,6 +457,16 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
     }
   };
 
+  // Every key of the row from the pooled row in memory: digits 2 and 3, then
+  // the ordered emit and gather of the whole row.  The caller made the
+  // pooled row complete and visible to this workgroup's loads.
+  auto finish_alone = [&]() __attribute__((always_inline)) {
+    uint32_t T, take_eq;
+    tail_digits(sweep, b1, k1, hist2, hist3, small + 64, &T, &take_eq);
+    tail_emit<NT>(fz, row, 0, Lk, 0u, 0u, T, take_eq, kbig, prot, [&](int j) { return prow[j]; }, s_src, s_dst,
+                  small);
+  };
+
   if (alone) {
     // The others left: finish the row from the pooled row in memory (every
     // interior came in before barrier A; this workgroup wrote the boundary
@@ -463,10 +475,7 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
     __syncthreads();
     if (tid == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     __syncthreads();
-    uint32_t T, take_eq;
-    tail_digits(sweep, b1, k1, hist2, hist3, small + 64, &T, &take_eq);
-    tail_emit<NT>(fz, row, 0, Lk, 0u, 0u, T, take_eq, kbig, prot, [&](int j) { return prow[j]; }, s_src, s_dst,
-                  small);
+    finish_alone();
     return;
   }
 
@@ -533,15 +542,34 @@ __device__ void fused_tail(const SelFuse& fz, const float* __restrict__ sc, uint
     }
   }
   if (tid == 0) {
-    int n = 0;
-    while (ld_dev(rw + kRowBarB) < (uint32_t)S && ++n < kTailSpinB) __builtin_amdgcn_s_sleep(2);
-    const bool ok = n < kTailSpinB;
-    if (!ok) atomicOr(rw + kRowStatus, 1u);
+    bool ok = true;
+    for (int n = 0; ld_dev(rw + kRowBarB) < (uint32_t)S; ++n) {
+      if (n >= fz.spin_b) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
     small[120] = ok ? 1u : 0u;
     small[122] = 0u;  // set below when a split has more candidates than were peeked
   }
   __syncthreads();
-  if (!small[120]) return;
+  if (!small[120]) {
+    // Gave up at B: the boundary keys of every split (their raw scores are
+    // still in U) into the pooled row, then the whole row alone.
+    for (int t = tid; t < nb * w2; t += NT) {
+      const int bi = t / w2, k = t % w2;
+      const int j = (bi + 1) * kps - h + k;
+      if (j < Lk)
+        st_dev(reinterpret_cast<uint32_t*>(prow + j), __float_as_uint(lds_window_max(ex, bi * w4 + k, bi * w4 + k + w2)));
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __syncthreads();
+    finish_alone();
+    return;
+  }
 
   // 3. One round trip: every split's header and its first `peek`
   // candidates (read blindly; kPeekTotal entries in all, the region is

@@ -26,7 +26,7 @@ from typing import Any, Iterable, Optional
 
 import torch
 
-from . import ops, torch_ops
+from . import _lib, ops, torch_ops
 from .hf_query import take_captured_query
 
 logger = logging.getLogger(__name__)
@@ -98,6 +98,15 @@ def _deployed_path_scores(query_states, key_states, value_states, window_size: i
     return ops.scores(query_states, key_states, value_states, W, eps=1e-6, p_round=True, y_round=True)
 
 
+def _check_head_dim(head_dim: int) -> None:
+    """The HIP scoring kernels take head dimensions up to
+    ``_lib.MAX_HEAD_DIM``; larger ones are refused here, before any device
+    work (the reference's PyTorch path scores any D)."""
+    if head_dim > _lib.MAX_HEAD_DIM:
+        raise ValueError(f"head dimension {head_dim} is above {_lib.MAX_HEAD_DIM}, the largest the DropKV HIP "
+                         "kernels score")
+
+
 class DropKVCache(_LayerCache):
     """KV cache that evicts at prefill by the DropKV score
     (dropkv_cache.py:310-648).
@@ -163,6 +172,7 @@ class DropKVCache(_LayerCache):
         num_query_heads = query_states.shape[1]
         if num_query_heads % num_kv_heads != 0:
             raise ValueError(f"Query heads {num_query_heads} must be divisible by KV heads {num_kv_heads}")
+        _check_head_dim(head_dim)
 
         scores = None
         if self.use_triton:
@@ -208,6 +218,7 @@ class DropKVCache(_LayerCache):
         num_query_heads = query_states.shape[1]
         if num_query_heads % num_kv_heads != 0:
             raise ValueError(f"Query heads {num_query_heads} must be divisible by KV heads {num_kv_heads}")
+        _check_head_dim(head_dim)
         fast = self._fast_path_ok(query_states, key_states, value_states)
         W = self.window_size if fast else min(self.window_size, query_states.shape[2])
         keep = self._keep_length(seq_len, total_tokens, max_keep_len)
@@ -356,6 +367,7 @@ class DropKVCache(_LayerCache):
         raises ``ValueError`` when the kept rows exceed the capacity."""
         if query_states.shape[1] % k_src.shape[1] != 0:
             raise ValueError(f"Query heads {query_states.shape[1]} must be divisible by KV heads {k_src.shape[1]}")
+        _check_head_dim(k_src.shape[3])
         fast = self._fast_path_ok(query_states, k_src[:, :, :Lk], v_src[:, :, :Lk])
         W = self.window_size if fast else min(self.window_size, query_states.shape[2])
         total_tok = self._seen_tokens if self._evict_use_seen_tokens else None

@@ -91,7 +91,7 @@ def dropkv_scores_triton(
     ``match_pytorch_precision=True`` rounds the softmax probabilities to the
     input dtype before ``w = (p/(1-p+eps))^2`` (dropkv_triton.py:584-587).
     Head dimensions 32, 64 and 128 run on the matrix-core kernels, other
-    powers of two (up to 512) on the library's generic fp32 kernels.
+    powers of two (up to 4096) on the library's generic fp32 kernels.
 
     ``allow_tf32`` is accepted for compatibility and has no effect: gfx950 has
     no TF32 matrix path; P.V and Y.V^T run as bf16/fp16 MFMAs with the fp32

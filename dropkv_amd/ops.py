@@ -55,6 +55,17 @@ def _stream_workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
     return ws
 
 
+def release_workspaces() -> None:
+    """Drop the per-(device, stream) workspaces kept for calls that bring
+    none (they only grow, to the largest call seen on that stream, and are
+    otherwise held for the life of the process).  Each goes back to
+    PyTorch's caching allocator, which orders its reuse after the work
+    already enqueued on its stream (``torch.cuda.empty_cache()`` can then
+    return it to the device); the next call allocates a fresh workspace."""
+    with _shared_ws_lock:
+        _shared_ws.clear()
+
+
 def _aligned(t: torch.Tensor) -> bool:
     return t.data_ptr() % 16 == 0
 
@@ -265,22 +276,16 @@ def evict(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, window: int, kernel
     return idx, ko, vo
 
 
-def set_resident(enabled: bool = True, spin_polls: int = -1) -> None:
-    """``dropkv_set_resident``: whether layer-calls that fit on chip score in
-    the one resident kernel (off by default), and the polls a workgroup waits at its
-    first barrier before it leaves its KV head to the last one to arrive
-    (``spin_polls`` < 0: unchanged; 0 forces that path)."""
-    _lib.check(_lib.load().dropkv_set_resident(int(bool(enabled)), int(spin_polls)), "dropkv_set_resident")
-
-
-def set_tail_select(enabled: bool = True, spin_polls: int = -1) -> None:
+def set_tail_select(enabled: bool = True, spin_polls: int = -1, spin_polls_b: int = -1) -> None:
     """``dropkv_set_tail_select``: whether layer-calls finish their selection
     (threshold, ordered emit, K/V gather) in the scoring kernel's tail when
-    the call allows it (on by default) or always in two further kernels, and
-    the polls a workgroup waits at the tail's first barrier before it leaves
-    its row to the last one to arrive (``spin_polls`` < 0: unchanged; 0
-    forces that path).  Same results either way."""
-    _lib.check(_lib.load().dropkv_set_tail_select(int(bool(enabled)), int(spin_polls)), "dropkv_set_tail_select")
+    the call allows it (on by default) or always in two further kernels; the
+    polls a workgroup waits at the tail's first barrier before it leaves its
+    row to the last one to arrive (``spin_polls``), and at the second barrier
+    before it finishes the row alone (``spin_polls_b``); < 0 leaves a limit
+    unchanged, 0 forces that path.  Same results every way."""
+    _lib.check(_lib.load().dropkv_set_tail_select(int(bool(enabled)), int(spin_polls), int(spin_polls_b)),
+               "dropkv_set_tail_select")
 
 
 class EvictPlan:

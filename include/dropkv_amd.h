@@ -42,7 +42,7 @@ const char* dropkv_last_error(void);
 
 /* Head dimensions of the matrix-core scoring kernels (bf16 / fp16 inputs);
  * writes up to `cap` values into `out` and returns how many exist.  Every
- * other head dimension up to 512, fp32 inputs, and GQA groups of more than
+ * other head dimension up to 4096, fp32 inputs, and GQA groups of more than
  * 4096 query rows (g * W) are scored by generic fp32 kernels on the vector
  * ALUs with the same arguments and results. */
 int dropkv_supported_head_dims(int64_t* out, int cap);
@@ -67,7 +67,9 @@ int dropkv_supported_head_dims(int64_t* out, int cap);
  *          (deployed path, dropkv_cache.py:434)
  *   splits 0 = automatic split-K depth over keys, otherwise that many splits
  *          per (b, hkv, row-chunk)
- * Requires Hq % Hkv == 0, 1 <= W <= Lq <= Lk, 1 <= D <= 512.
+ * Requires Hq % Hkv == 0, 1 <= W <= Lq <= Lk, 1 <= D <= 4096, and
+ * B*Hq*W and B*Hkv*Lk at most 2^31-1 (the workspace functions return 0
+ * otherwise).
  * The first DROPKV_SYNC_BYTES of the workspace must be zero when a workspace
  * is first used; every call leaves them zero (see dropkv_evict).
  * ------------------------------------------------------------------------ */
@@ -136,11 +138,10 @@ int dropkv_compact2(const void* k0, const void* v0, int64_t s0_b, int64_t s0_h, 
  * deployed path).  `scores` may be NULL (then it lives in the workspace).
  * Pooling and the top-k threshold run in the tail of the scoring kernel
  * whenever the plan allows it (three kernels per call), otherwise as the
- * standalone selection kernels.  Calls that fit on chip (D = 128, g*W <= 32,
- * bf16/fp16, splits = 0, B*Hkv*ceil(Lk/1024) no more than the device's CUs)
- * can score in one kernel that streams K/V once (dropkv_set_resident).
+ * standalone selection kernels.  kernel_size may be any positive odd number
+ * (windows past 129 keys pool in two extra kernels).
  *
- * The first DROPKV_SYNC_BYTES of the workspace hold that kernel's barrier
+ * The first DROPKV_SYNC_BYTES of the workspace are reserved for call
  * counters: they must be zero when a workspace is first used (fill a new
  * workspace with zeros), and every call leaves them zero.  The rest of the
  * workspace needs no initialisation.  Calls that share a workspace must be
@@ -169,9 +170,10 @@ int dropkv_evict(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_
  * ends.  The first call on a device looks up its address there (make that
  * first call outside graph capture); no call allocates or frees anything.
  * Calls whose dropkv_evict_workspace_bytes exceeds the maximum return
- * DROPKV_E_UNSUPPORTED: 32 MiB covers a Llama-3.1-8B layer (Hq 32, Hkv 8,
- * D 128) up to about 470K keys and a Qwen2-0.5B layer up to about 2.0M
- * keys; the B4 Hq64 Hkv8 128K-key stress shape needs 78 MiB and is refused.
+ * DROPKV_E_UNSUPPORTED: 32 MiB covers a Llama-3.1-8B layer (B 1, Hq 32,
+ * Hkv 8, D 128, W 8) up to 231544 keys and a Qwen2-0.5B layer (B 1, Hq 14,
+ * Hkv 2, D 64, W 8) up to 992160 keys; the B4 Hq64 Hkv8 D128 W32 128K-key
+ * stress shape needs 111.5 MiB and is refused.
  * Every call on one GPU uses the same scratch and leaves its contents
  * behind: calls that overlap on one GPU (two streams, or two threads) race
  * and must be serialised by the caller.  The caller initialises nothing (the
@@ -220,20 +222,6 @@ int dropkv_evict_ld(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int
                     float* scores, int64_t* keep_idx, void* k_out, void* v_out, int64_t out_ld,
                     void* workspace, size_t workspace_bytes, void* stream);
 
-/* ------------------------------------------------------------------------
- * The one-kernel (resident) scoring of dropkv_evict / dropkv_evict_ld /
- * dropkv_evict_noalloc (no counterpart in the reference, whose Triton path
- * always launches its kernels in sequence).  mode 1 takes it for every call
- * that fits; mode 0 (the default) never does.  Its workgroups wait for one
- * another twice per call; a workgroup that has waited spin_polls polls at
- * the first wait (spin_polls < 0: unchanged; default 65536, a few tens of
- * milliseconds) leaves its KV head to the last workgroup of the head to
- * arrive, which finishes that head alone with the same results.  That only
- * happens when other work holds CUs; spin_polls = 0 forces it (tests).
- * Process-wide; not synchronised with calls in flight.
- * ------------------------------------------------------------------------ */
-int dropkv_set_resident(int mode, int64_t spin_polls);
-
 /* Where the layer-calls' selection runs (no counterpart in the reference,
  * whose pooling, top-k and gather are separate torch ops).  mode 1 (the
  * default): dropkv_evict / dropkv_evict_ld / dropkv_evict_noalloc finish the
@@ -244,11 +232,13 @@ int dropkv_set_resident(int mode, int64_t spin_polls);
  * workgroups then wait for one another twice per call.  mode 0: the
  * selection always runs as two further kernels.  Both give the same
  * results.  A workgroup that has waited spin_polls polls at the first wait
- * (spin_polls < 0: unchanged; default 65536, a few tens of milliseconds)
- * leaves its row to the row's last workgroup to arrive, which finishes the
- * row alone; spin_polls = 0 forces that (tests).  Process-wide; not
- * synchronised with calls in flight. */
-int dropkv_set_tail_select(int mode, int64_t spin_polls);
+ * (default 65536, a few tens of milliseconds) leaves its row to the row's
+ * last workgroup to arrive, which finishes the row alone; one that has
+ * waited spin_polls_b polls at the second wait (default 4194304, seconds)
+ * finishes the whole row alone itself.  Either way the outputs are the same
+ * bits.  A limit < 0 leaves it unchanged; 0 forces that path (tests).
+ * Process-wide: a call reads the settings once when it is enqueued. */
+int dropkv_set_tail_select(int mode, int64_t spin_polls, int64_t spin_polls_b);
 
 /* Kernel timing with HIP events (no counterpart in the reference, which has
  * no timers).  dropkv_timing_enable(1) makes every later dropkv_scores /

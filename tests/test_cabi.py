@@ -68,7 +68,9 @@ def test_workspace_queries(lib):
     (dict(Lq=4), 1, "must be >= window_size"),
     (dict(Lq=200), 1, "must be <= Lk"),
     (dict(D=0), 1, "head dim must be positive"),
-    (dict(D=1024), 2, "head dim 1024 above 512"),
+    (dict(D=8192), 2, "head dim 8192 above 4096"),
+    (dict(B=1 << 20, Lk=1 << 12), 2, "B*Hq*W or B*Hkv*Lk above"),     # 2^35 keys
+    (dict(Hq=1 << 22, Hkv=1 << 10, W=1 << 10, Lq=1 << 10, Lk=1 << 10), 2, "B*Hq*W or B*Hkv*Lk above"),  # 2^32 rows
 ])
 def test_score_argument_checks(lib, args, code, msg):
     """Checks happen on the host before anything is enqueued."""
@@ -134,3 +136,40 @@ def test_noalloc_entry_refuses_shapes_beyond_its_scratch(lib):
     args[14] = 0  # window 0: an argument error comes first
     assert lib.dropkv_evict_noalloc(*args) == 1
     assert "window must be positive" in lib.dropkv_last_error().decode()
+
+
+def test_workspace_sizes_refuse_overflowing_shapes(lib):
+    """Shapes whose window rows (B*Hq*W) or keys (B*Hkv*Lk) exceed 2^31-1
+    get no workspace size (0) rather than a wrapped-around one."""
+    assert lib.dropkv_scores_workspace_bytes(1 << 20, 32, 8, 32768, 128, 8, 0) == 0
+    assert lib.dropkv_evict_workspace_bytes(1 << 20, 32, 8, 32768, 128, 8, 0) == 0
+    assert lib.dropkv_scores_workspace_bytes(1, 1 << 22, 1 << 10, 4096, 128, 1 << 10, 0) == 0
+    assert lib.dropkv_select_workspace_bytes(1 << 16, 1 << 16) == 0
+    assert lib.dropkv_scores_workspace_bytes(1, 32, 8, 32768, 128, 8, 0) > 0
+
+
+def _noalloc_max_keys(lib, B, Hq, Hkv, D, W):
+    cap = _lib.NOALLOC_SCRATCH_BYTES
+    lo, hi = 1, 1 << 26
+    while lo < hi:
+        m = (lo + hi + 1) // 2
+        b = lib.dropkv_evict_workspace_bytes(B, Hq, Hkv, m, D, W, 0)
+        lo, hi = (m, hi) if 0 < b <= cap else (lo, m - 1)
+    return lo
+
+
+def test_noalloc_limits_in_the_header_match_the_library(lib):
+    """The key counts the header quotes for dropkv_evict_noalloc are the
+    largest Lk whose dropkv_evict_workspace_bytes fits the static scratch,
+    and the stress shape's figure is its workspace size."""
+    import re
+    text = open(HEADER).read()
+    m = re.search(r"Llama-3\.1-8B layer \(B 1, Hq 32,\s*\*\s*Hkv 8, D 128, W 8\) up to (\d+) keys and a "
+                  r"Qwen2-0\.5B layer \(B 1, Hq 14,\s*\*\s*Hkv 2, D 64, W 8\) up to (\d+) keys;.*?needs "
+                  r"([0-9.]+) MiB", text, re.S)
+    assert m, "no-alloc coverage sentence not found in the header"
+    assert int(m.group(1)) == _noalloc_max_keys(lib, 1, 32, 8, 128, 8)
+    assert int(m.group(2)) == _noalloc_max_keys(lib, 1, 14, 2, 64, 8)
+    c5 = lib.dropkv_evict_workspace_bytes(4, 64, 8, 131072, 128, 32, 0) / 2 ** 20
+    assert abs(float(m.group(3)) - c5) < 0.05
+    assert c5 * 2 ** 20 > _lib.NOALLOC_SCRATCH_BYTES

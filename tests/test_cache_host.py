@@ -172,6 +172,23 @@ def test_eviction_on_cpu_tensors_fails_loudly():
         ops.compact(K, V, torch.zeros(1, 8, 4, dtype=torch.int64))
 
 
+def test_head_dim_above_the_kernel_limit_fails_early():
+    """A head dimension above the kernels' 4096 is refused with ValueError
+    naming the limit, before any device work (CPU tensors would otherwise
+    raise RuntimeError at the device check), in both cache modes."""
+    cfg = dict(B=1, Hq=2, Hkv=1, D=4104)
+    Q, K, V = make_qkv(cfg, 16)
+    for c in (_cache(), DropKVCache(keep_ratio=0.5, window_size=8, capacity=64)):
+        with pytest.raises(ValueError, match="above 4096"):
+            c.update(Q, K, V, layer_idx=0)
+
+
+def test_release_workspaces_empties_the_stream_cache():
+    ops._shared_ws[("probe", 0)] = object()
+    ops.release_workspaces()
+    assert not ops._shared_ws
+
+
 # --- scoring guards reachable without a GPU (dropkv_triton.py:680-693) -------
 
 def test_guard_window_size():

@@ -1,5 +1,5 @@
 """Head dimensions and input dtypes beyond the bf16/fp16 D=64/128 core: D=32
-on the matrix-core kernels, any other D (up to 512) and fp32 inputs on the
+on the matrix-core kernels, any other D (up to 4096) and fp32 inputs on the
 generic vector-ALU kernels, through the same C ABI entry points.
 
 The reference's Triton scorer takes any power-of-two D >= 32 in fp16/bf16
@@ -74,7 +74,7 @@ def test_head_dims_bf16_mode_binding(gpu, D):
     print(f"[D={D}] binding keys {n_sel}, worst rel {worst:.2e}, beyond 1e-3: {n_above}", flush=True)
 
 
-@pytest.mark.parametrize("D", [80, 96, 512])
+@pytest.mark.parametrize("D", [80, 96, 512, 1024, 4096])
 def test_deployed_path_other_head_dims(gpu, D):
     """Head dimensions only the deployed path takes (dropkv_cache.py:401-460):
     p and y rounded to bf16 against the oracle's fallback scores."""

@@ -31,6 +31,19 @@ def test_select_random(gpu, rows, Lk, keep):
     _select_case(gpu, scores, 11, 8, keep)
 
 
+@pytest.mark.parametrize("rows,Lk,ks,keep", [(2, 5000, 131, 500), (3, 3000, 1001, 300), (1, 700, 4095, 70),
+                                             (2, 40000, 257, 4000), (1, 2000, 131, 2000)])
+def test_select_wide_kernels(gpu, rows, Lk, ks, keep):
+    """Pooling windows wider than 129 keys (block prefix / suffix maxima,
+    any odd kernel size as the reference takes, dropkv_cache.py:327-328):
+    pooled values and the lowest-index tie rule bit-exact, including a window
+    wider than the row (every key pools to the row maximum) and wide
+    plateaus tied at the threshold."""
+    g = torch.Generator().manual_seed(ks + Lk)
+    scores = torch.rand(1, rows, Lk, generator=g)
+    _select_case(gpu, scores, ks, 8, keep)
+
+
 def test_select_ties_and_plateaus(gpu):
     """Integer-valued scores: pooling makes long plateaus, so the threshold
     is tied many times over; the lowest indices must win."""
@@ -153,6 +166,9 @@ def test_evict_fused_matches_ops(gpu, shape):
     (32768, 11, 8, 3276, 0, False),   # the headline row length
     (40000, 11, 8, 4000, 0, False),   # 40 chunks: more than one speculative window per region
     (40000, 11, 8, 4000, 0, True),    # ... with every score tied (overflow of the speculative loads)
+    (5000, 131, 8, 500, 0, False),    # windows past 129 keys: block prefix / suffix pooling kernels
+    (3000, 2049, 8, 300, 0, False),   # a window two thirds of the row
+    (700, 4095, 8, 70, 0, False),     # a window wider than the row
 ])
 def test_evict_fused_selection_edges(gpu, Lk, ks, window, keep, splits, vzero):
     """dropkv_evict (selection fused into the scoring tail where the plan

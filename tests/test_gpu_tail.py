@@ -16,9 +16,13 @@ the oracle's selection rule.
 * V = 0 makes every score 0: all unprotected keys tie at the threshold, the
   candidates overflow the tail's LDS list and each workgroup sweeps the
   pooled row instead; the lowest indices must win, as in the oracle.
-* Lone finish: with a spin limit of 0 every workgroup but a row's last one
-  leaves at barrier A, and the last one finishes the row from memory; the
-  bits must not change.
+* Lone finish: with a spin limit of 0 at barrier A every workgroup but a
+  row's last one leaves there, and the last one finishes the row from
+  memory; with a limit of 0 at barrier B every workgroup that does not find
+  the whole row arrived gives up there and finishes the whole row alone
+  (concurrently with the others, writing the same outputs); with both at 0,
+  both happen.  In every case every kernel exits and the bits must not
+  change.
 * Repeated calls, and HIP graph replays with eager calls in between, give
   the same bits (the barrier words are cleared by the merge kernel of every
   call).
@@ -38,6 +42,8 @@ from oracle import dropkv_ref as R
 
 pytestmark = pytest.mark.gpu
 
+SPIN_A, SPIN_B = 1 << 16, 1 << 22  # the library's default poll limits at barriers A and B
+
 CASES = [
     # (cfg, Lq, Lk, W, dtype, keep_ratio)
     (LLAMA_CFG, 8192, 8192, 8, torch.bfloat16, 0.1),                       # 32 splits of 256 keys
@@ -54,9 +60,9 @@ CASES = [
 def tail():
     """The tail on (the library default) for the test and afterwards."""
     from dropkv_amd import ops
-    ops.set_tail_select(True, 1 << 16)
+    ops.set_tail_select(True, SPIN_A, SPIN_B)
     yield ops
-    ops.set_tail_select(True, 1 << 16)
+    ops.set_tail_select(True, SPIN_A, SPIN_B)
 
 
 def _run(ops, Q, K, V, W, ks, keep, plan=None):
@@ -130,15 +136,18 @@ def test_tail_all_ties_sweeps_the_row(gpu, tail):
     assert torch.equal(a[0].cpu(), expect.expand_as(a[0].cpu()))
 
 
+@pytest.mark.parametrize("limits", [(0, SPIN_B), (SPIN_A, 0), (0, 0)], ids=["A", "B", "AB"])
 @pytest.mark.parametrize("case", [0, 4])
-def test_tail_lone_finish_is_bit_identical(gpu, tail, case):
+def test_tail_lone_finish_is_bit_identical(gpu, tail, case, limits):
     (Q, K, V), (Qg, Kg, Vg), W, keep = _inputs(case, gpu, 80 + case)
     ks = 11
-    print(f"[tail lone] case {case}", flush=True)
+    print(f"[tail lone] case {case} poll limits {limits}", flush=True)
     plan, a = _run(tail, Qg, Kg, Vg, W, ks, keep)
-    tail.set_tail_select(True, 0)
-    plan_b, b = _run(tail, Qg, Kg, Vg, W, ks, keep)
-    tail.set_tail_select(True, 1 << 16)
+    tail.set_tail_select(True, *limits)
+    try:
+        plan_b, b = _run(tail, Qg, Kg, Vg, W, ks, keep)
+    finally:
+        tail.set_tail_select(True, SPIN_A, SPIN_B)
     for x, y in zip(a, b):
         assert torch.equal(x, y)
     # the workspace serves a normal call again afterwards
