@@ -96,21 +96,25 @@ def binding_keys(ref, pooled_ref, keep, frac=0.1):
 
 
 def assert_binding_scores(got, ref, pooled_ref, keep, Qt, K, V, W, p_round, max_rel, rel_bar, frac_above,
-                          frac=0.1, excuse_sinks=True, max_arbitrated=4096):
+                          frac=0.1, excuse_sinks=True, max_arbitrated=4096, bracket=None):
     """Relative bars on the binding keys: every one within ``max_rel`` and
     fewer than ``frac_above`` of them beyond ``rel_bar``.
 
     A key beyond ``rel_bar`` against the float32 reference is arbitrated in
-    float64 (the oracle's ``dropkv_scores_fp64``: the same formula with the
-    direct distance, p rounded from a float64 p, and with p off by 2^-20
-    before the rounding, which can flip it to the neighbouring bf16 value):
-    it counts as within a bar if it is within it of either evaluation.  With
-    ``excuse_sinks`` a key beyond ``max_rel`` of both may still pass within
-    four times the rounding bound of a float32 expansion of that score (an
-    attention sink, p ~ 1: no float32 evaluation determines it); such keys
-    must stay under 1e-3 of the row; the same rule excuses a key from the
-    count beyond ``rel_bar``.  Returns (binding keys, worst relative error
-    after arbitration, keys beyond rel_bar, sink-excused keys)."""
+    float64.  With p rounded (``p_round``), by the oracle's
+    ``dropkv_score_bracket``: the interval of values a float32 evaluation of
+    the formula can return (p off by its float32 error before the rounding,
+    which can flip it to the neighbouring bf16 value; y and the expansion
+    off by their float32 rounding); its error is its distance to that
+    interval, relative to the float64 score.  Keys within ``max_rel`` of
+    their bracket but of neither the float32 reference nor the float64
+    score (attention sinks, p ~ 1: no float32 evaluation determines them)
+    are counted as sinks and must stay under 1e-3 of the row, and need
+    ``excuse_sinks``.  Without p
+    rounding the arbiter is the float64 score alone (``dropkv_scores_fp64``).
+    ``bracket`` may hold precomputed (score, lo, hi) [B, Hkv, Lk] float64.
+    Returns (binding keys, worst relative error after arbitration, keys
+    beyond rel_bar, sink-excused keys)."""
     from oracle import dropkv_ref as R
     got, ref = got.double().cpu(), ref.double().cpu()
     sel = binding_keys(ref, pooled_ref.cpu(), keep, frac)
@@ -118,7 +122,6 @@ def assert_binding_scores(got, ref, pooled_ref, keep, Qt, K, V, W, p_round, max_
     B, Hkv, Lk = ref.shape
     g = Qt.shape[1] // Hkv
     worst, n_above, n_excused = 0.0, 0, 0
-    probes = (1.0,) if p_round is None else (1.0, 1 - 2.0 ** -20, 1 + 2.0 ** -20)
     for b in range(B):
         for h in range(Hkv):
             r = rel[b, h]
@@ -129,34 +132,24 @@ def assert_binding_scores(got, ref, pooled_ref, keep, Qt, K, V, W, p_round, max_
                 gk = got[b, h, keys]
                 qh = Qt[b:b + 1, h * g:(h + 1) * g].cpu()
                 kh, vh = K[b:b + 1, h:h + 1].cpu(), V[b:b + 1, h:h + 1].cpu()
-                r64s, bnd = [], None
-                for f in probes:
-                    r64, bb = R.dropkv_scores_fp64(qh, kh, vh, W, p_round=p_round, p_scale=f, keys=keys,
-                                                   return_bound=True)
-                    r64s.append(r64[0, 0])
-                    bnd = bb[0, 0] if bnd is None else torch.maximum(bnd, bb[0, 0])
-                r64s = torch.stack(r64s)
-                rel64 = ((gk[None] - r64s).abs() / r64s.abs().clamp_min(1e-300)).min(0).values
-                best[keys] = torch.minimum(r[keys], rel64)
-                beyond = best[keys] > max_rel
-                if beyond.any():
-                    assert excuse_sinks, ((b, h), keys[beyond][:8].tolist(), best[keys][beyond][:8].tolist())
-                    slack = ((gk[None] - r64s).abs() - max_rel * r64s.abs() - 4 * bnd[None]).min(0).values
-                    assert (slack[beyond] <= 0).all(), ((b, h), keys[beyond][slack[beyond] > 0][:8].tolist())
-                    row_sinks = int(beyond.sum())
-                    best[keys[beyond]] = 0.0
+                if p_round is None:
+                    s64 = R.dropkv_scores_fp64(qh, kh, vh, W, keys=keys)[0, 0]
+                    lo = hi = s64
+                elif bracket is not None:
+                    s64, lo, hi = (x[b, h, keys] for x in bracket)
                 else:
-                    row_sinks = 0
-                # Keys beyond rel_bar whose distance from a float64 evaluation
-                # is within four times the float32 rounding bound of their
-                # score are sinks too (no float32 evaluation determines them
-                # to rel_bar).
-                beyond_bar = best[keys] > rel_bar
-                if excuse_sinks and beyond_bar.any():
-                    slack = ((gk[None] - r64s).abs() - rel_bar * r64s.abs() - 4 * bnd[None]).min(0).values
-                    sink = beyond_bar & (slack <= 0)
-                    row_sinks += int(sink.sum())
-                    best[keys[sink]] = 0.0
+                    s64, lo, hi = (x[0, 0] for x in R.dropkv_score_bracket(qh, kh, vh, W, p_round=p_round,
+                                                                             keys=keys))
+                scale = s64.abs().clamp_min(1e-300)
+                dist = torch.where(gk < lo, lo - gk, torch.where(gk > hi, gk - hi, torch.zeros_like(gk))) / scale
+                e64 = (gk - s64).abs() / scale
+                best[keys] = torch.minimum(r[keys], dist)
+                # within max_rel of its bracket but of neither evaluation: a
+                # score the float32 formula does not determine (a sink)
+                sink = (best[keys] <= max_rel) & (torch.minimum(r[keys], e64) > max_rel)
+                row_sinks = int(sink.sum())
+                if row_sinks:
+                    assert excuse_sinks, ((b, h), keys[sink][:8].tolist())
                 assert row_sinks <= 1e-3 * Lk, ((b, h), row_sinks)
                 n_excused += row_sinks
             worst = max(worst, float(best.max()))

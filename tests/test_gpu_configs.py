@@ -9,15 +9,20 @@ the CPU oracle.
 * C3 -- a 4096-query chunk against Lk = 4096 n (kernel sweep, Q as a strided
   slice of the 65536-row prompt), and the ``every_chunk`` cache flow over 16
   chunks (Lk_n = keep_{n-1} + 4096, keep_n = int(0.1 * 4096 n)), each
-  eviction checked against the oracle on the same stored state (selection
-  arbitrated in float64 where the float32 reference is not decisive).
+  eviction checked against the oracle on the same stored state: selection
+  at 0.999 against the float64 evaluation (ties excused) and against the
+  float32 reference (ties and the indices its rounding leaves undecided
+  excused, oracle.selection_band).
 * C5 -- B4 Hq64 Hkv8 D128 Lq=Lk=131072, K ~ Student-t(3), W32 r0.05: the
   full 8 GiB query tensor is on the device with every row outside the
   32-row tail set to NaN (so any read of it would poison the scores);
-  sampled rows against the oracle's scores wherever the float32 reference
-  is determined (it is not at attention sinks, p ~ 1), their selection
-  against the float64 arbiter, every row's selection against the oracle's
-  pool / protect / rank rule on the GPU scores, every gather bit for bit.
+  every one of the 32 (b, hkv) rows against the oracle: scores on the
+  binding keys and against the float64 brackets (the float32 reference is
+  not determined at attention sinks, p ~ 1), the selection at 0.999
+  against the float64 evaluation (ties excused) and against the float32
+  reference (ties and undecided indices excused); every row's selection
+  against the oracle's pool / protect / rank rule on the GPU scores, every
+  gather bit for bit.
 """
 
 import pytest
@@ -151,21 +156,24 @@ def test_c3_every_chunk_cache_flow(gpu, c3_prompt):
         ref = R.dropkv_scores_reference(qt, fk, fv, W, match_pytorch_precision=True)
         from dropkv_amd import dropkv_scores_triton
         _close(dropkv_scores_triton(q, full_k, full_v, window_size=W), ref, 2e-2, 1e-3)
-        # Selection: against the float64 arbiter at the 0.999 bar; against the
-        # float32 reference at 0.999 or, where the reference is not decisive,
-        # no further from it than the float64 evaluation is.  After a few
-        # compressions the stored keys crowd the keep threshold and the
-        # float32 reference itself ranks about 0.4% of them differently from
-        # the float64 evaluation (the bf16 rounding of p flips with last-bit
-        # logit differences).
-        ref64 = R.dropkv_scores_fp64(qt, fk, fv, W, p_round=torch.bfloat16)
-        idx64, pooled64 = R.compute_keep_indices(qt, fk, fv, 0.1, W, ks, total_tokens=seen, scores=ref64)
+        # Selection, both at 0.999: against the float64 evaluation with only
+        # exact ties excused, and against the float32 reference with ties and
+        # the indices its own rounding leaves undecided excused (the band of
+        # the float64 brackets: after a few compressions the stored keys
+        # crowd the threshold, and the bf16 rounding of p flips with
+        # last-bit logit differences).
+        protect = min(W, fk.shape[2])
+        s64, lo, hi = R.dropkv_score_bracket(qt, fk, fv, W, p_round=torch.bfloat16)
+        idx64, pooled64 = R.compute_keep_indices(qt, fk, fv, 0.1, W, ks, total_tokens=seen, scores=s64)
         worst64, unexcused64 = R.index_overlap(idx.cpu(), idx64, pooled64)
         assert worst64 >= 0.999, (n, worst64, unexcused64)
+        und = R.selection_band(lo, hi, ks, protect, keep)
         ref_idx, pooled = R.compute_keep_indices(qt, fk, fv, 0.1, W, ks, total_tokens=seen, scores=ref)
-        worst, unexcused = R.index_overlap(idx.cpu(), ref_idx, pooled)
-        exact, _ = R.index_overlap(idx64, ref_idx, pooled)
-        assert worst >= min(0.999, exact - 2e-3), (n, worst, unexcused, exact)
+        worst, counted, n_tie, n_band = R.index_overlap(idx.cpu(), ref_idx, pooled, undecided=und,
+                                                        return_counts=True)
+        print(f"[c3 flow] chunk {n}: keep {keep}, vs fp32 reference: overlap {worst:.4f}, counted {counted}, "
+              f"ties {n_tie}, band {n_band} (band size {int(und.sum())}); vs float64: {worst64:.4f}", flush=True)
+        assert worst >= 0.999, (n, worst, counted, n_tie, n_band)
     assert lengths[0] == (409 + 4096, 819) and lengths[-1] == (int(0.1 * 61440) + 4096, 6553)
     del cache
     _free()
@@ -177,10 +185,19 @@ def _student_t3(shape, g, dev):
     return z / torch.sqrt(chi2 / 3)
 
 
-def test_c5_stress_full_size(gpu):
+C5_ROWS = [(b, h) for b in range(4) for h in range(8)]
+C5_GROUPS = 8
+
+
+@pytest.fixture(scope="module")
+def c5_run(gpu):
+    """One C5 layer-call on the device: the full 8 GiB query tensor with every
+    row outside the 32-row tail NaN (any read of it would poison the
+    scores).  Every row's selection against the oracle's pool / protect /
+    rank rule on the GPU scores and every gather bit for bit are checked
+    here; the inputs and results go to the host for the per-row checks."""
     from dropkv_amd import ops
     B, Hq, Hkv, D, L, W, ks, ratio = 4, 64, 8, 128, 131072, 32, 11, 0.05
-    g_heads = Hq // Hkv
     keep = R.keep_length(ratio, L, W)
     assert keep == 6553
     gen = torch.Generator(device=gpu).manual_seed(5)
@@ -190,69 +207,57 @@ def test_c5_stress_full_size(gpu):
     Q = torch.full((B, Hq, L, D), float("nan"), dtype=torch.bfloat16, device=gpu)
     Q[:, :, -W:] = Qt
     assert torch.isfinite(K).all()
+    print("[c5] layer-call", flush=True)
     plan = ops.EvictPlan(Q, K, W, ks, keep, keep_scores=True)
     idx, kc, vc = plan(Q, K, V)
     s = plan.scores
     assert torch.isfinite(s).all() and (s >= 0).all()
-    # every row: selection = the oracle's pool / protect / rank rule on these scores
     s_cpu = s.cpu()
     pooled = R.pool_protect(s_cpu.clone(), ks, W)
     assert torch.equal(idx.cpu(), R.topk_sorted(pooled, keep))
-    # every row: gather bit for bit (torch.gather on the device)
     gk, gv = R.gather_compressed(K, V, idx)
     assert torch.equal(kc, gk) and torch.equal(vc, gv)
-    # Sampled rows against the oracle.  Heavy-tailed keys make attention
-    # sinks: rows where one key takes p ~ 1, whose weight (p/(1-p+eps))^2
-    # reaches 1e12 and multiplies a distance that any float32 evaluation of
-    # |v|^2 - 2<v,y> + |y|^2 (the reference's and this one) resolves only to
-    # ~1e-5.  A key whose score differs from the float32 reference is
-    # therefore checked against float64 evaluations, with p exact or off by
-    # 2^-20 before the bf16 rounding (which can flip to the other neighbour),
-    # to the tolerance plus four times the float32 expansion's rounding
-    # bound; the keys that bound excuses must be rare.  The selection is
-    # arbitrated in float64.
-    Qt_c = Qt.cpu()
-
-    def close(a, b, slack=0.0):
-        return (a.double() - b.double()).abs() <= 1e-3 + 2e-2 * b.double().abs() + slack
-
-    sampled = []
-    for b, h in ((0, 0), (1, 3), (2, 5), (3, 7)):
-        qh = Qt_c[b:b + 1, h * g_heads:(h + 1) * g_heads]
-        kh, vh = K[b:b + 1, h:h + 1].cpu(), V[b:b + 1, h:h + 1].cpu()
-        got = s_cpu[b:b + 1, h:h + 1]
-        r32 = R.dropkv_scores_reference(qh, kh, vh, W, match_pytorch_precision=True)
-        keys = torch.nonzero(~close(got, r32).flatten()).flatten()
-        if keys.numel():
-            g_k = got[..., keys]
-            ok = torch.zeros_like(g_k, dtype=torch.bool)
-            for f in (1.0, 1 - 2.0 ** -20, 1 + 2.0 ** -20):
-                r, bnd = R.dropkv_scores_fp64(qh, kh, vh, W, p_round=torch.bfloat16, p_scale=f, keys=keys,
-                                              return_bound=True)
-                ok |= close(g_k, r, 4 * bnd)
-                if f == 1.0:
-                    excused = ~close(g_k, r) & close(g_k, r, 4 * bnd)
-            assert ok.all(), ((b, h), keys[~ok.flatten()][:8].tolist())
-            assert int(excused.sum()) <= 1e-3 * L, ((b, h), int(excused.sum()))
-        _, rp32 = R.compute_keep_indices(qh, kh, vh, ratio, W, ks, scores=r32)
-        sampled.append((got, r32, rp32, qh, kh, vh))
-        r64 = R.dropkv_scores_fp64(qh, kh, vh, W, p_round=torch.bfloat16)
-        idx64, p64 = R.compute_keep_indices(qh, kh, vh, ratio, W, ks, scores=r64)
-        worst64, unexcused64 = R.index_overlap(idx[b:b + 1, h:h + 1].cpu(), idx64, p64)
-        assert worst64 >= 0.999, ((b, h), worst64, unexcused64)
-        # Against the float32 reference: no further from it than the exact
-        # evaluation is (its sink scores are noise that moves whole pooled
-        # windows across the threshold).
-        ref_idx, rp = R.compute_keep_indices(qh, kh, vh, ratio, W, ks, scores=r32)
-        worst, unexcused = R.index_overlap(idx[b:b + 1, h:h + 1].cpu(), ref_idx, rp)
-        exact, _ = R.index_overlap(idx64, ref_idx, rp)
-        assert worst >= exact - 2e-3, ((b, h), worst, unexcused, exact)
-    # The binding keys of the sampled rows (>= 0.1x the keep threshold):
-    # within 2e-2, fewer than 1e-3 of them beyond 1e-3, sinks by the float64
-    # bound rule (the rows stacked as the KV heads of one batch entry).
-    cat = [torch.cat([row[i] for row in sampled], dim=1) for i in range(6)]
-    stats = assert_binding_scores(cat[0], cat[1], cat[2], keep, cat[3], cat[4], cat[5], W, torch.bfloat16, 2e-2,
-                                  1e-3, 1e-3)
-    print(f"[c5] binding keys {stats[0]}, worst rel {stats[1]:.2e}, beyond 1e-3: {stats[2]}, sinks {stats[3]}")
-    del Q, K, V, plan, kc, vc, gk, gv
+    out = dict(Qt=Qt.cpu(), K=K.cpu(), V=V.cpu(), s=s_cpu, idx=idx.cpu(), W=W, ks=ks, ratio=ratio, keep=keep,
+               g=Hq // Hkv, L=L)
+    del Q, K, V, plan, kc, vc, gk, gv, idx, s
     _free()
+    return out
+
+
+@pytest.mark.parametrize("group", range(C5_GROUPS))
+def test_c5_stress_rows(c5_run, group):
+    """Four (b, hkv) rows of the C5 call per test, all 32 rows over the
+    group: scores on the binding keys (>= 0.1x the keep threshold) within
+    2e-2 of the float32 reference, fewer than 1e-3 of them beyond 1e-3,
+    arbitrated by the float64 brackets (heavy-tailed keys make attention
+    sinks, p ~ 1, whose weight reaches 1e12 and whose score no float32
+    expansion determines); every key within 1e-3 + 2e-2 |score| of its
+    bracket; the selection at 0.999 against the float64 evaluation with only
+    exact ties excused, and at 0.999 against the float32 reference with
+    ties and the indices its own rounding leaves undecided excused."""
+    c = c5_run
+    W, ks, ratio, keep, g = c["W"], c["ks"], c["ratio"], c["keep"], c["g"]
+    per = len(C5_ROWS) // C5_GROUPS
+    for b, h in C5_ROWS[group * per:(group + 1) * per]:
+        qh = c["Qt"][b:b + 1, h * g:(h + 1) * g]
+        kh, vh = c["K"][b:b + 1, h:h + 1], c["V"][b:b + 1, h:h + 1]
+        got = c["s"][b:b + 1, h:h + 1]
+        mine = c["idx"][b:b + 1, h:h + 1]
+        r32 = R.dropkv_scores_reference(qh, kh, vh, W, match_pytorch_precision=True)
+        s64, lo, hi = R.dropkv_score_bracket(qh, kh, vh, W, p_round=torch.bfloat16)
+        gd = got.double()
+        far = torch.where(gd < lo, lo - gd, torch.where(gd > hi, gd - hi, torch.zeros_like(gd)))
+        assert (far <= 1e-3 + 2e-2 * s64.abs()).all(), ((b, h), torch.nonzero(far.flatten() > 0)[:8].flatten().tolist())
+        ref_idx, rp = R.compute_keep_indices(qh, kh, vh, ratio, W, ks, scores=r32)
+        stats = assert_binding_scores(got, r32, rp, keep, qh, kh, vh, W, torch.bfloat16, 2e-2, 1e-3, 1e-3,
+                                      bracket=(s64, lo, hi))
+        idx64, p64 = R.compute_keep_indices(qh, kh, vh, ratio, W, ks, scores=s64)
+        worst64, counted64 = R.index_overlap(mine, idx64, p64)
+        und = R.selection_band(lo, hi, ks, W, keep)
+        worst, counted, n_tie, n_band = R.index_overlap(mine, ref_idx, rp, undecided=und, return_counts=True)
+        print(f"[c5] row (b={b}, h={h}): binding keys {stats[0]}, worst rel {stats[1]:.2e}, beyond 1e-3 {stats[2]}, "
+              f"sinks {stats[3]}; vs fp32 reference: overlap {worst:.4f}, counted {counted}, ties {n_tie}, "
+              f"band {n_band} (band size {int(und.sum())}); vs float64: overlap {worst64:.4f}, counted {counted64}",
+              flush=True)
+        assert worst64 >= 0.999, ((b, h), worst64, counted64)
+        assert worst >= 0.999, ((b, h), worst, counted, n_tie, n_band)
