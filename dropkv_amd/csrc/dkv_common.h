@@ -52,6 +52,14 @@ __device__ __forceinline__ void round_through2<__bf16>(float& a, float& b) {
   b = __builtin_bit_cast(float, u & 0xffff0000u);
 }
 
+// Whether any lane of the wave has `pred`, as a scalar (SGPR) value, so that
+// a branch on it is compiled as a uniform branch: the not-taken side then
+// issues nothing.  (__any's result is not known to be uniform, and a branch
+// on it is compiled as an exec-masked if/else whose both sides issue.)
+__device__ __forceinline__ bool wave_any(bool pred) {
+  return __builtin_amdgcn_readfirstlane((int)(__builtin_amdgcn_ballot_w64(pred) != 0)) != 0;
+}
+
 // min(p, 1) for p >= 0 or NaN (as unsigned integers: NaN gives 1, like fminf)
 // and min(x, 0) for the sign of x (as signed integers): one integer op each,
 // where fminf also canonicalises its operand.

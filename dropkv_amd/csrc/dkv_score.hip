@@ -560,6 +560,7 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
 
   // The per-key sums hold sum_m w * (-dist2/2): scale by -2/g at the end.
   const float out_scale = -2.0f * (1.0f / static_cast<float>(g));
+  const float one_m2eps = 1.0f - 2.0f * eps;
   const int k_begin = split * kps;
   const int k_end = min(k_begin + kps, Lk);
   const int64_t roff = ((int64_t)head * kv_ld + k_begin) * D;
@@ -691,8 +692,9 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb)
           sink_here |= (uint32_t)(__builtin_bit_cast(int, cst[mb * kStatWords + 32]) - t0) < (uint32_t)kTile;
-        auto epilogue = [&](auto masked_c) __attribute__((always_inline)) {
+        auto epilogue = [&](auto masked_c, auto small_c) __attribute__((always_inline)) {
           constexpr bool kMasked = decltype(masked_c)::value;
+          constexpr bool kSmall = decltype(small_c)::value;
 #pragma unroll
           for (int mb = 0; mb < kMB; ++mb) {
             const int m = (c0 + c) * kRows + mb * 16 + li;
@@ -709,23 +711,30 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
                 for (int e = 0; e < 2; ++e) {
                   p[e] = __builtin_amdgcn_exp2f(sacc[kb][mb][r + e] * scale_log2 - lse2);
                   if (kMasked) p[e] = (t0 + 16 * kb + 4 * lg + r + e) <= bound ? p[e] : 0.f;
-                  p[e] = min_one_nonneg(p[e]);
+                  if (!kSmall) p[e] = min_one_nonneg(p[e]);  // (small p: p <= 2^-13 already)
                 }
                 if (PR) round_through2<T>(p[0], p[1]);
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
-                  const float ratio = p[e] * __builtin_amdgcn_rcpf(1.0f - p[e] + eps);
                   float nd2 = min_zero(gacc[kb][mb][r + e]);  // -dist2/2, dist2 clamped at 0
                   if (kMasked) nd2 = (t0 + 16 * kb + 4 * lg + r + e) == skey ? snd2 : nd2;
-                  sc[kb][r + e] = fmaf(ratio * ratio, nd2, sc[kb][r + e]);
+                  sc[kb][r + e] = fmaf(small_p_weight<kSmall>(p[e], eps, one_m2eps), nd2, sc[kb][r + e]);
                 }
               }
           }
         };
-        if (masked || __any(sink_here))
-          epilogue(std::true_type{});
-        else
-          epilogue(std::false_type{});
+        if (masked || wave_any(sink_here)) {
+          epilogue(std::true_type{}, std::false_type{});
+        } else {
+          bool big = false;
+#pragma unroll
+          for (int mb = 0; mb < kMB; ++mb)
+            big |= tile_max4x2(sacc, mb) * scale_log2 - cst[mb * kStatWords] > kSmallLog2P;
+          if (wave_any(big))
+            epilogue(std::false_type{}, std::false_type{});
+          else
+            epilogue(std::false_type{}, std::true_type{});
+        }
       }
 
       // Sum over the 16 query rows held by lanes li = 0..15 as a
@@ -843,6 +852,7 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
     for (int i = tid; i < kBins1; i += NT) hist_l[i] = 0u;
 
   const float out_scale = -2.0f * (1.0f / static_cast<float>(g));
+  const float one_m2eps = 1.0f - 2.0f * eps;
   const int k_begin = split * kps;
   const int k_end = min(k_begin + kps, Lk);
   const int64_t roff = ((int64_t)head * kv_ld + k_begin) * D;
@@ -910,11 +920,12 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
     }
   };
 
-  // One tile: this wave's per-key sums over its rows into red[par][wv][gt * kTile ..].
-  auto tile = [&](const uint32_t* kl, int t0, int par, int gt) __attribute__((always_inline)) {
+  // One tile in two parts.  mma: S^T and G^T of this wave's rows for the
+  // tile whose K/V rows are at kl; epi: the per-element work on them and this
+  // wave's per-key sums over its rows into red[buf][wv][gt * kTile ..].
+  auto mma = [&](const uint32_t* kl, f32x4 (&sacc)[2][kMB], f32x4 (&gacc)[2][kMB]) __attribute__((always_inline)) {
     const uint32_t* vl = kl + kTensorWords;
     const float* vn = reinterpret_cast<const float*>(vl + kTensorWords);
-    f32x4 sacc[2][kMB], gacc[2][kMB];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const f32x4 vn2 = *reinterpret_cast<const f32x4*>(vn + 16 * kb + 4 * lg);
@@ -942,6 +953,9 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
         gacc[kb][mb] = ga;
       }
     }
+  };
+  auto epi = [&](const f32x4 (&sacc)[2][kMB], const f32x4 (&gacc)[2][kMB], int t0, int buf, int gt)
+                 __attribute__((always_inline)) {
     float sc[2][4];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -950,8 +964,9 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
     bool sink_here = false;
 #pragma unroll
     for (int mb = 0; mb < kMB; ++mb) sink_here |= (uint32_t)(skey[mb] - t0) < (uint32_t)kTile;
-    auto epilogue = [&](auto masked_c) __attribute__((always_inline)) {
+    auto epilogue = [&](auto masked_c, auto small_c) __attribute__((always_inline)) {
       constexpr bool kMasked = decltype(masked_c)::value;
+      constexpr bool kSmall = decltype(small_c)::value;
 #pragma unroll
       for (int mb = 0; mb < kMB; ++mb) {
         const int m = mc * kRows + mb * 16 + li;
@@ -965,23 +980,29 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
             for (int e = 0; e < 2; ++e) {
               p[e] = __builtin_amdgcn_exp2f(sacc[kb][mb][r + e] * scale_log2 - lse2[mb]);
               if (kMasked) p[e] = (t0 + 16 * kb + 4 * lg + r + e) <= bound ? p[e] : 0.f;
-              p[e] = min_one_nonneg(p[e]);
+              if (!kSmall) p[e] = min_one_nonneg(p[e]);  // (small p: p <= 2^-13 already)
             }
             if (PR) round_through2<T>(p[0], p[1]);
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-              const float ratio = p[e] * __builtin_amdgcn_rcpf(1.0f - p[e] + eps);
               float nd2 = min_zero(gacc[kb][mb][r + e]);  // -dist2/2, dist2 clamped at 0
               if (kMasked) nd2 = (t0 + 16 * kb + 4 * lg + r + e) == skey[mb] ? snd2[mb] : nd2;
-              sc[kb][r + e] = fmaf(ratio * ratio, nd2, sc[kb][r + e]);
+              sc[kb][r + e] = fmaf(small_p_weight<kSmall>(p[e], eps, one_m2eps), nd2, sc[kb][r + e]);
             }
           }
       }
     };
-    if (pad_chunk || t0 + kTile > unmasked_end || __any(sink_here))
-      epilogue(std::true_type{});
-    else
-      epilogue(std::false_type{});
+    if (pad_chunk || t0 + kTile > unmasked_end || wave_any(sink_here)) {
+      epilogue(std::true_type{}, std::false_type{});
+    } else {
+      bool big = false;
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb) big |= tile_max4x2(sacc, mb) * scale_log2 - lse2[mb] > kSmallLog2P;
+      if (wave_any(big))
+        epilogue(std::false_type{}, std::false_type{});
+      else
+        epilogue(std::false_type{}, std::true_type{});
+    }
     // Sum over the 16 rows of lanes li = 0..15, a reduce-scatter on DPP
     // (partners 15 - li, then 7 - li within each half, then li ^ 2 and
     // li ^ 1: each step pairs lanes that keep complementary keys): lane li
@@ -997,17 +1018,18 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
       v += dpp_f<kDppHalfMirror>(h4 ? k0 : k1);
       v += dpp_f<kDppQuadSwap2>(v);
       v += dpp_f<kDppQuadSwap1>(v);
-      if ((li & 3) == 0) red[par][wv][gt * kTile + 16 * kb + 4 * lg + (li >> 2)] = v;
+      if ((li & 3) == 0) red[buf][wv][gt * kTile + 16 * kb + 4 * lg + (li >> 2)] = v;
     }
   };
 
   // The keys' totals of a stage over the active waves, in wave order, after
   // the barrier that follows the stage's red writes.
-  auto finish = [&](int grp, int par) __attribute__((always_inline)) {
+  auto finish = [&](int grp) __attribute__((always_inline)) {
     if (tid < kG * kTile) {
+      const int buf = grp & 1;
       const int it = grp * kG + tid / kTile;
-      float v = red[par][0][tid];
-      for (int w = 1; w < n_mc; ++w) v += red[par][w][tid];
+      float v = red[buf][0][tid];
+      for (int w = 1; w < n_mc; ++w) v += red[buf][w][tid];
       const int n = k_begin + it * kTile + tid % kTile;
       if (it < ntiles && n < k_end) {
         scores[(int64_t)head * Lk + n] = v * out_scale;
@@ -1023,12 +1045,16 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
 #pragma unroll
       for (int gt = 0; gt < kG; ++gt) {
         const int it = grp * kG + gt;
-        if (it < ntiles) tile(lds + st * kStage + gt * kTileWords, k_begin + it * kTile, grp & 1, gt);
+        if (it < ntiles) {
+          f32x4 sacc[2][kMB], gacc[2][kMB];
+          mma(lds + st * kStage + gt * kTileWords, sacc, gacc);
+          epi(sacc, gacc, k_begin + it * kTile, grp & 1, gt);
+        }
       }
     }
     if (grp + 1 < ngroups) stage(1 - st);
     __syncthreads();
-    finish(grp, grp & 1);
+    finish(grp);
   };
   issue(0);
   stage(0);

@@ -111,7 +111,7 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
     lsum[mb] = lsum[mb] * alpha + psum;
     m2[mb] = mnew;
     // Rescale only when some row's maximum moved (rare after a few tiles).
-    if (__any(alpha != 1.f)) {
+    if (wave_any(alpha != 1.f)) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) yacc[dt][mb] *= alpha;
     }
@@ -546,6 +546,31 @@ __device__ __forceinline__ void merge_row(int rid, const float* __restrict__ par
     sb[32] = __builtin_bit_cast(float, k_top);
     sb[48] = nd2_top;
   }
+}
+
+// The weight w = (p/(1-p+eps))^2 of pass 2 (dropkv_triton.py:589-591).
+// With kSmall the caller has shown p <= 2^kSmallLog2P for every p of the
+// wave's tile; then, with x = p - eps, 1/(1-x)^2 = 1 + 2x + 3x^2 + ... and
+// the terms from 3x^2 on stay below 3 * 2^-26 relative (under one fp32
+// ulp), so w = p^2 (1 + 2p - 2eps) to fp32 rounding, without the
+// reciprocal (a quarter-rate instruction).  one_m2eps = 1 - 2eps.
+constexpr float kSmallLog2P = -13.0f;
+template <bool kSmall>
+__device__ __forceinline__ float small_p_weight(float p, float eps, float one_m2eps) {
+  if constexpr (kSmall) {
+    return (p * p) * fmaf(2.0f, p, one_m2eps);
+  } else {
+    const float ratio = p * __builtin_amdgcn_rcpf(1.0f - p + eps);
+    return ratio * ratio;
+  }
+}
+
+// The largest of a lane's logits of row block mb in a 32-key tile
+// (acc[kb][mb][r], two key blocks of four).
+__device__ __forceinline__ float tile_max4x2(const f32x4 (&acc)[2][kMB], int mb) {
+  const float a = fmaxf(fmaxf(acc[0][mb][0], acc[0][mb][1]), fmaxf(acc[0][mb][2], acc[0][mb][3]));
+  const float b = fmaxf(fmaxf(acc[1][mb][0], acc[1][mb][1]), fmaxf(acc[1][mb][2], acc[1][mb][3]));
+  return fmaxf(a, b);
 }
 
 // ---------------------------------------------------------------------------
