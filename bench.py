@@ -129,9 +129,9 @@ def cpu_baseline(Qt, K, V, cfg, min_seconds=10.0, max_reps=400):
 def parity(Qt, K, V, cfg, gpu_idx, fp64=False):
     """Tie-aware overlap of the GPU selection with the oracle's (scores from
     dropkv_scores_reference(match_pytorch_precision=True), pool, protect,
-    top-k); with ``fp64``, with the float64 arbiter's (the same formula in
-    float64 with the direct distance), which decides where the float32
-    reference is rounding noise (attention sinks)."""
+    top-k); with ``fp64``, with the float64 evaluation's (the same formula in
+    float64), which decides where the float32 reference is rounding noise
+    (attention sinks)."""
     from oracle import dropkv_ref as R
     if fp64:
         ref_scores = R.dropkv_scores_fp64(Qt, K, V, cfg["window"], p_round=torch_bf16())
@@ -140,6 +140,29 @@ def parity(Qt, K, V, cfg, gpu_idx, fp64=False):
     ref_idx, pooled = R.compute_keep_indices(Qt, K, V, cfg["ratio"], cfg["window"], cfg["kernel"],
                                              scores=ref_scores)
     return R.index_overlap(gpu_idx, ref_idx, pooled)
+
+
+def band_parity(Qt, K, V, cfg, gpu_idx):
+    """Overlap of the GPU selection with the float32 reference's where every
+    difference must be an exact tie at the reference's threshold or an index
+    the reference's own float32 rounding leaves undecided (oracle
+    ``selection_band`` over the float64 score brackets), and with the float64
+    evaluation's with ties only.  Returns a dict of the figures."""
+    from oracle import dropkv_ref as R
+    W, ks, ratio = cfg["window"], cfg["kernel"], cfg["ratio"]
+    r32 = R.dropkv_scores_reference(Qt, K, V, W, match_pytorch_precision=True)
+    s64, lo, hi = R.dropkv_score_bracket(Qt, K, V, W, p_round=torch_bf16())
+    Lk = K.shape[2]
+    keep = min(Lk, max(int(ratio * Lk), W, 1))
+    und = R.selection_band(lo, hi, ks, min(W, Lk), keep)
+    ref_idx, pooled = R.compute_keep_indices(Qt, K, V, ratio, W, ks, scores=r32)
+    worst, counted, n_tie, n_band = R.index_overlap(gpu_idx, ref_idx, pooled, undecided=und, return_counts=True)
+    idx64, p64 = R.compute_keep_indices(Qt, K, V, ratio, W, ks, scores=s64)
+    w64, c64 = R.index_overlap(gpu_idx, idx64, p64)
+    return {"vs_fp32_reference": {"min_row_overlap": round(worst, 6), "counted_diffs": counted,
+                                  "excused_ties": n_tie, "excused_undecided": n_band,
+                                  "undecided_indices": int(und.sum())},
+            "vs_fp64": {"min_row_overlap_tie_aware": round(w64, 6), "unexcused_index_diffs": c64}}
 
 
 def torch_bf16():
@@ -611,6 +634,27 @@ def extras(lib, dev):
             flops = 4 * B * Hkv * M * D * Lk
             e["mfma_frac"] = {k: round(flops / (kus[k] * 1e-6) / 1e12 / MFMA_PEAK_TFLOPS, 4)
                               for k in STREAM_STAGES if k in kus}
+        if cfg.get("gen") == "device":
+            # Selection parity on two sampled (b, hkv) rows (the test suite
+            # checks all 32).
+            rows = (SAMPLE_ROWS[0], SAMPLE_ROWS[-1])
+            g_h = Hq // Hkv
+            acc = None
+            for b, h in rows:
+                print(f"[bench] extra: {name} parity row {(b, h)}", file=sys.stderr, flush=True)
+                r = band_parity(Qg[b:b + 1, h * g_h:(h + 1) * g_h, -W:].cpu().contiguous(), Kg[b:b + 1, h:h + 1].cpu(),
+                                Vg[b:b + 1, h:h + 1].cpu(), cfg, plan.keep_idx[b:b + 1, h:h + 1].cpu())
+                if acc is None:
+                    acc = r
+                else:
+                    for k in ("vs_fp32_reference", "vs_fp64"):
+                        for f, v in r[k].items():
+                            acc[k][f] = min(acc[k][f], v) if f.startswith("min") else acc[k][f] + v
+            acc["rows"] = [list(x) for x in rows]
+            acc["rule"] = ("a difference counts unless it is an exact tie at the reference's threshold or an index "
+                           "whose float64 score bracket (the values any float32 evaluation of the formula can "
+                           "return) meets the threshold band (oracle.selection_band)")
+            e["parity"] = acc
         ex[name] = e
         del plan, Qg, Kg, Vg
         torch.cuda.synchronize()
