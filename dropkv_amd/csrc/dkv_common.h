@@ -36,20 +36,14 @@ template <typename T>
 __device__ __forceinline__ float round_through(float x) {
   return static_cast<float>(static_cast<T>(x));
 }
-
-// The same for two values at once (bf16: one packed conversion).
-template <typename T>
-__device__ __forceinline__ void round_through2(float& a, float& b) {
-  a = round_through<T>(a);
-  b = round_through<T>(b);
-}
+// bf16: one packed conversion with x in the high half and +0 in the low half,
+// whose 32 bits are then exactly the rounded value as a float (the plain
+// conversion adds a shift).
 template <>
-__device__ __forceinline__ void round_through2<__bf16>(float& a, float& b) {
+__device__ __forceinline__ float round_through<__bf16>(float x) {
   typedef float f2 __attribute__((ext_vector_type(2)));
   typedef __bf16 h2 __attribute__((ext_vector_type(2)));
-  const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), h2));
-  a = __builtin_bit_cast(float, u << 16);
-  b = __builtin_bit_cast(float, u & 0xffff0000u);
+  return __builtin_bit_cast(float, __builtin_convertvector((f2{0.f, x}), h2));
 }
 
 // Whether any lane of the wave has `pred`, as a scalar (SGPR) value, so that

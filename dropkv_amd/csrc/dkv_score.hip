@@ -526,7 +526,7 @@ template <typename T, int D, int WAVES, int MINW, bool PR>
 __global__ void __launch_bounds__(64 * WAVES, MINW)
 pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
              int Hkv, int Lq, int Lk, int W, int g, int M, int n_mc, int cg, int n_splits, int kps,
-             float scale_log2, float eps,
+             float scale_log2, float eps, float small_c2,
              const u32x4* __restrict__ opblk, const float* __restrict__ stblk, float* __restrict__ scores,
              SelFuse fz) {
   typedef typename Elem<T>::v8 v8;
@@ -560,7 +560,6 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
 
   // The per-key sums hold sum_m w * (-dist2/2): scale by -2/g at the end.
   const float out_scale = -2.0f * (1.0f / static_cast<float>(g));
-  const float one_m2eps = 1.0f - 2.0f * eps;
   const int k_begin = split * kps;
   const int k_end = min(k_begin + kps, Lk);
   const int64_t roff = ((int64_t)head * kv_ld + k_begin) * D;
@@ -569,7 +568,6 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
   const uint32_t k_lane = (li * D + 8 * lg) * sizeof(T);
   const int ntiles = (k_end - k_begin + kTile - 1) / kTile;
   __shared__ uint32_t s_next;
-  const bool pad_rows = mpad > M;
   const int unmasked_end = Lk - W + 1;
 
   v8 kop[2][KK], vop[2][KK];
@@ -618,25 +616,24 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
     auto run = [&](auto nc_const, int npairs) __attribute__((always_inline)) {
     constexpr int NC = decltype(nc_const)::value;
     auto tile = [&](v8 (&kop)[2][KK], v8 (&vop)[2][KK], int t0, int tn) __attribute__((always_inline)) {
-      // |v|^2 of key t0+16kb+li (fp32 dot of the exact operand values), then
-      // redistributed to the result layout (keys 16kb+4lg+r).
-      float vn2[2][4];
+      // The MFMAs put rows on the result registers and keys on the lanes:
+      // lane (lg, li) holds rows 16mb + 4lg + r (r = 0..3) of key t0 + 16kb +
+      // li, so a key's sum over the rows is in-lane but for the four lane
+      // groups.  |v|^2 of key t0+16kb+li: fp32 dot of the exact operand
+      // values.
+      float vn2[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         float part = 0.f;
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) part = sumsq8<T>(vop[kb][kk], part);
-        part = add_xor32(add_xor16(part));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) vn2[kb][r] = __shfl(part, 4 * lg + r);
+        vn2[kb] = add_xor32(add_xor16(part));
       }
-      const bool masked = pad_rows || t0 + kTile > unmasked_end;
+      // (Padding rows need no mask: merge gives them lse = +inf and zero Q,
+      // so their p is 0.)
+      const bool masked = t0 + kTile > unmasked_end;
 
-      float sc[2][4];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sc[kb][r] = 0.f;
+      float sc[2] = {0.f, 0.f};
 
 #pragma unroll 1
       for (int cp = 0; cp < npairs; ++cp)
@@ -645,21 +642,22 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
         const int c = cp * NC + c1;
         f32x4 sacc[2][kMB], gacc[2][kMB];
         const u32x4* ob = opnd + (size_t)(c * OPS) * 64 + lane;
+        const float* cst = stat + (size_t)c * kMB * kStatWords;
         // G starts at -(|v|^2 + |y|^2)/2, so that after the MFMAs it holds
         // <v,y> - (|v|^2 + |y|^2)/2 = -dist2/2 of every (key, row) pair.
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb) {
-          const float nyh = -0.5f * stat[(c * kMB + mb) * kStatWords + 16 + li];
+          const f32x4 y4 = *reinterpret_cast<const f32x4*>(cst + mb * kStatWords + 16 + 4 * lg);
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb) {
             sacc[kb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) gacc[kb][mb][r] = fmaf(vn2[kb][r], -0.5f, nyh);
+            for (int r = 0; r < 4; ++r) gacc[kb][mb][r] = fmaf(vn2[kb], -0.5f, -0.5f * y4[r]);
           }
         }
-        // S^T first: after the last row-chunk's S MFMAs the K registers are
+        // S first: after the last row-chunk's S MFMAs the K registers are
         // free, and the K loads of tile tn (relative; zeros past the range)
-        // start while G^T is computed; then the same for V.
+        // start while G is computed; then the same for V.
         const bool refill = c1 == NC - 1 && cp == npairs - 1;
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb)
@@ -667,7 +665,7 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
           for (int kk = 0; kk < KK; ++kk) {
             const v8 qo = __builtin_bit_cast(v8, ob[(size_t)((0 * kMB + mb) * KK + kk) * 64]);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) sacc[kb][mb] = Elem<T>::mfma(kop[kb][kk], qo, sacc[kb][mb]);
+            for (int kb = 0; kb < 2; ++kb) sacc[kb][mb] = Elem<T>::mfma(qo, kop[kb][kk], sacc[kb][mb]);
           }
         if (refill) load_rows_op<T, D>(kop, krs, k_lane, tn);
 #pragma unroll
@@ -678,8 +676,8 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
             const v8 yl = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-              gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], yh, gacc[kb][mb]);
-              gacc[kb][mb] = Elem<T>::mfma(vop[kb][kk], yl, gacc[kb][mb]);
+              gacc[kb][mb] = Elem<T>::mfma(yh, vop[kb][kk], gacc[kb][mb]);
+              gacc[kb][mb] = Elem<T>::mfma(yl, vop[kb][kk], gacc[kb][mb]);
             }
           }
         if (refill) load_rows_op<T, D>(vop, vrs, k_lane, tn);
@@ -687,74 +685,72 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
         // distance at a row's dominant key (merge), are applied only in
         // tiles that reach the bound or hold such a key (and with padding
         // rows), so that the other tiles carry no per-element selects.
-        const float* cst = stat + (size_t)c * kMB * kStatWords + li;
         bool sink_here = false;
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb)
-          sink_here |= (uint32_t)(__builtin_bit_cast(int, cst[mb * kStatWords + 32]) - t0) < (uint32_t)kTile;
-        auto epilogue = [&](auto masked_c, auto small_c) __attribute__((always_inline)) {
+          sink_here |= (uint32_t)(__builtin_bit_cast(int, cst[mb * kStatWords + 32 + li]) - t0) < (uint32_t)kTile;
+        // log2 p of every element, in place of its logit.
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb) {
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(cst + mb * kStatWords + 4 * lg);
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sacc[kb][mb][r] = sacc[kb][mb][r] * scale_log2 - l4[r];
+        }
+        auto epilogue = [&](auto masked_c, auto small_c, float (&acc)[2]) __attribute__((always_inline)) {
           constexpr bool kMasked = decltype(masked_c)::value;
           constexpr bool kSmall = decltype(small_c)::value;
 #pragma unroll
           for (int mb = 0; mb < kMB; ++mb) {
-            const int m = (c0 + c) * kRows + mb * 16 + li;
-            const int bound = kMasked ? row_bound(m, M, W, Lk) : 0;
-            const int skey = kMasked ? __builtin_bit_cast(int, cst[mb * kStatWords + 32]) : -1;
-            const float snd2 = kMasked ? cst[mb * kStatWords + 48] : 0.f;
-            const float lse2 = cst[mb * kStatWords];
+            int bound[4] = {0, 0, 0, 0}, sk[4] = {-1, -1, -1, -1};
+            float sn[4] = {0.f, 0.f, 0.f, 0.f};
+            if (kMasked) {
+              const u32x4 k4 = *reinterpret_cast<const u32x4*>(cst + mb * kStatWords + 32 + 4 * lg);
+              const f32x4 n4 = *reinterpret_cast<const f32x4*>(cst + mb * kStatWords + 48 + 4 * lg);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-              for (int r = 0; r < 4; r += 2) {
-                float p[2];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                  p[e] = __builtin_amdgcn_exp2f(sacc[kb][mb][r + e] * scale_log2 - lse2);
-                  if (kMasked) p[e] = (t0 + 16 * kb + 4 * lg + r + e) <= bound ? p[e] : 0.f;
-                  if (!kSmall) p[e] = min_one_nonneg(p[e]);  // (small p: p <= 2^-13 already)
-                }
-                if (PR) round_through2<T>(p[0], p[1]);
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                  float nd2 = min_zero(gacc[kb][mb][r + e]);  // -dist2/2, dist2 clamped at 0
-                  if (kMasked) nd2 = (t0 + 16 * kb + 4 * lg + r + e) == skey ? snd2 : nd2;
-                  sc[kb][r + e] = fmaf(small_p_weight<kSmall>(p[e], eps, one_m2eps), nd2, sc[kb][r + e]);
-                }
+              for (int r = 0; r < 4; ++r) {
+                bound[r] = row_bound((c0 + c) * kRows + mb * 16 + 4 * lg + r, M, W, Lk);
+                sk[r] = (int)k4[r];
+                sn[r] = n4[r];
               }
+            }
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+              const int key = t0 + 16 * kb + li;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                float p = __builtin_amdgcn_exp2f(sacc[kb][mb][r]);
+                if (kMasked) p = key <= bound[r] ? p : 0.f;
+                if (!kSmall) p = min_one_nonneg(p);  // (small p: p <= 2^-13 already)
+                if (PR) p = round_through<T>(p);
+                float nd2 = min_zero(gacc[kb][mb][r]);  // -dist2/2, dist2 clamped at 0
+                if (kMasked) nd2 = key == sk[r] ? sn[r] : nd2;
+                acc[kb] = fmaf(kSmall ? small_weight_over_c2(p) : exact_weight(p, eps), nd2, acc[kb]);
+              }
+            }
           }
         };
         if (masked || wave_any(sink_here)) {
-          epilogue(std::true_type{}, std::false_type{});
-        } else {
-          bool big = false;
+          epilogue(std::true_type{}, std::false_type{}, sc);
+        } else if (small_c2 > 0.f && !wave_any(!(tile_max(sacc) <= kSmallLog2P))) {
+          // This chunk's sums carry w / c^2: scaled back as they join sc.
+          float st[2] = {0.f, 0.f};
+          epilogue(std::false_type{}, std::true_type{}, st);
 #pragma unroll
-          for (int mb = 0; mb < kMB; ++mb)
-            big |= tile_max4x2(sacc, mb) * scale_log2 - cst[mb * kStatWords] > kSmallLog2P;
-          if (wave_any(big))
-            epilogue(std::false_type{}, std::false_type{});
-          else
-            epilogue(std::false_type{}, std::true_type{});
+          for (int kb = 0; kb < 2; ++kb) sc[kb] = fmaf(st[kb], small_c2, sc[kb]);
+        } else {
+          epilogue(std::false_type{}, std::false_type{}, sc);
         }
       }
 
-      // Sum over the 16 query rows held by lanes li = 0..15 as a
-      // reduce-scatter: afterwards lane li holds the total of key r = li/4
-      // (for li % 4 == 0), so each key is stored by one lane.  (Lane
-      // shuffles here: the DPP form pass2w_kernel uses measured ~0.2 us
-      // slower at C2, where the shuffles' latency overlaps other waves.)
-      const bool h8 = li & 8, h4 = li & 4;
+      // The four lane groups lg hold the same keys for different rows: their
+      // sum, stored by the lanes of group 0.
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        float k0 = h8 ? sc[kb][2] : sc[kb][0];
-        float k1 = h8 ? sc[kb][3] : sc[kb][1];
-        k0 += __shfl_xor(h8 ? sc[kb][0] : sc[kb][2], 8);
-        k1 += __shfl_xor(h8 ? sc[kb][1] : sc[kb][3], 8);
-        float v = h4 ? k1 : k0;
-        v += __shfl_xor(h4 ? k0 : k1, 4);
-        v += __shfl_xor(v, 2);
-        v += __shfl_xor(v, 1);
-        const int n = t0 + 16 * kb + 4 * lg + (li >> 2);
-        if ((li & 3) == 0 && n < k_end) {
+        float v = add_xor16(add_xor32(sc[kb]));
+        const int n = t0 + 16 * kb + li;
+        if (lg == 0 && n < k_end) {
           float* dst = scores + (int64_t)head * Lk + n;
           if (!first) v += *dst;
           *dst = last ? v * out_scale : v;
@@ -819,8 +815,8 @@ __device__ __forceinline__ float sum_over_row_lanes(float x) {
 template <typename T, int D, int kG, bool PR>
 __global__ void __launch_bounds__(64 * kWideWaves, 1)
 pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int Hkv, int Lq, int Lk, int W, int g,
-              int M, int n_mc, int n_splits, int kps, float scale_log2, float eps, const u32x4* __restrict__ opblk,
-              const float* __restrict__ stblk, float* __restrict__ scores, SelFuse fz) {
+              int M, int n_mc, int n_splits, int kps, float scale_log2, float eps, float small_c2,
+              const u32x4* __restrict__ opblk, const float* __restrict__ stblk, float* __restrict__ scores, SelFuse fz) {
   typedef typename Elem<T>::v8 v8;
   constexpr int KK = D / 32;
   constexpr int OPS = kOpSlots * kMB * KK;
@@ -852,7 +848,6 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
     for (int i = tid; i < kBins1; i += NT) hist_l[i] = 0u;
 
   const float out_scale = -2.0f * (1.0f / static_cast<float>(g));
-  const float one_m2eps = 1.0f - 2.0f * eps;
   const int k_begin = split * kps;
   const int k_end = min(k_begin + kps, Lk);
   const int64_t roff = ((int64_t)head * kv_ld + k_begin) * D;
@@ -863,15 +858,19 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
   const int ngroups = (ntiles + kG - 1) / kG;
 
   // This wave's operands (merge wrote them in pass 2's LDS order) and row
-  // statistics: lse (log2 units), |y|^2, the row's dominant key and
-  // -dist2/2 there.
+  // statistics.  The MFMAs put rows on the result registers and keys on the
+  // lanes: lane (lg, li) holds rows 16mb + 4lg + r (r = 0..3) of key 16kb + li,
+  // so a key's sum over the wave's rows is mostly in-lane.  Per lane: lse
+  // (log2 units) and -|y|^2/2 of its rows; the dominant key of row 16mb + li
+  // and -dist2/2 there (read by the other lanes through shuffles where a
+  // tile needs them).
   const int c = active ? mc : 0;
   v8 qo[kMB][KK], yh[kMB][KK], yl[kMB][KK];
-  float lse2[kMB], nyh[kMB], snd2[kMB];
+  float lse2[kMB][4], nyh[kMB][4], snd2[kMB];
   int skey[kMB];
   {
     const u32x4* ob = opblk + ((size_t)head * n_mc + c) * OPS * 64 + lane;
-    const float* st = stblk + ((size_t)head * n_mc + c) * kMB * kStatWords + li;
+    const float* st = stblk + ((size_t)head * n_mc + c) * kMB * kStatWords;
 #pragma unroll
     for (int mb = 0; mb < kMB; ++mb) {
 #pragma unroll
@@ -880,13 +879,17 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
         yh[mb][kk] = __builtin_bit_cast(v8, ob[(size_t)((1 * kMB + mb) * KK + kk) * 64]);
         yl[mb][kk] = __builtin_bit_cast(v8, ob[(size_t)((2 * kMB + mb) * KK + kk) * 64]);
       }
-      lse2[mb] = st[mb * kStatWords];
-      nyh[mb] = -0.5f * st[mb * kStatWords + 16];
-      skey[mb] = __builtin_bit_cast(int, st[mb * kStatWords + 32]);
-      snd2[mb] = st[mb * kStatWords + 48];
+      const f32x4 l4 = *reinterpret_cast<const f32x4*>(st + mb * kStatWords + 4 * lg);
+      const f32x4 y4 = *reinterpret_cast<const f32x4*>(st + mb * kStatWords + 16 + 4 * lg);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        lse2[mb][r] = l4[r];
+        nyh[mb][r] = -0.5f * y4[r];
+      }
+      skey[mb] = __builtin_bit_cast(int, st[mb * kStatWords + 32 + li]);
+      snd2[mb] = st[mb * kStatWords + 48 + li];
     }
   }
-  const bool pad_chunk = mc * kRows + kRows > M;
   const int unmasked_end = Lk - W + 1;
 
   // Staging: thread tid < KCH owns chunk tid % CPR of row tid / CPR of each
@@ -920,15 +923,17 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
     }
   };
 
-  // One tile in two parts.  mma: S^T and G^T of this wave's rows for the
-  // tile whose K/V rows are at kl; epi: the per-element work on them and this
-  // wave's per-key sums over its rows into red[buf][wv][gt * kTile ..].
+  // One tile in two parts.  mma: S and G of this wave's rows for the tile
+  // whose K/V rows are at kl (G starts at -(|v|^2 + |y|^2)/2, so that after
+  // the MFMAs it holds <v,y> - (|v|^2 + |y|^2)/2 = -dist2/2); epi: the
+  // per-element work on them and this wave's per-key sums over its rows into
+  // red[buf][wv][gt * kTile ..].
   auto mma = [&](const uint32_t* kl, f32x4 (&sacc)[2][kMB], f32x4 (&gacc)[2][kMB]) __attribute__((always_inline)) {
     const uint32_t* vl = kl + kTensorWords;
     const float* vn = reinterpret_cast<const float*>(vl + kTensorWords);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const f32x4 vn2 = *reinterpret_cast<const f32x4*>(vn + 16 * kb + 4 * lg);
+      const float vn2 = vn[16 * kb + li];
       v8 kop[KK], vop[KK];
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
@@ -941,26 +946,29 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
         f32x4 sa = {0.f, 0.f, 0.f, 0.f};
         f32x4 ga;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ga[r] = fmaf(vn2[r], -0.5f, nyh[mb]);
+        for (int r = 0; r < 4; ++r) ga[r] = fmaf(vn2, -0.5f, nyh[mb][r]);
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) sa = Elem<T>::mfma(kop[kk], qo[mb][kk], sa);
+        for (int kk = 0; kk < KK; ++kk) sa = Elem<T>::mfma(qo[mb][kk], kop[kk], sa);
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-          ga = Elem<T>::mfma(vop[kk], yh[mb][kk], ga);
-          ga = Elem<T>::mfma(vop[kk], yl[mb][kk], ga);
+          ga = Elem<T>::mfma(yh[mb][kk], vop[kk], ga);
+          ga = Elem<T>::mfma(yl[mb][kk], vop[kk], ga);
         }
         sacc[kb][mb] = sa;
         gacc[kb][mb] = ga;
       }
     }
   };
-  auto epi = [&](const f32x4 (&sacc)[2][kMB], const f32x4 (&gacc)[2][kMB], int t0, int buf, int gt)
+  auto epi = [&](f32x4 (&sacc)[2][kMB], const f32x4 (&gacc)[2][kMB], int t0, int buf, int gt)
                  __attribute__((always_inline)) {
-    float sc[2][4];
+    float sc[2] = {0.f, 0.f};
+    // log2 p of every element, in place of its logit.
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[kb][r] = 0.f;
+      for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sacc[kb][mb][r] = sacc[kb][mb][r] * scale_log2 - lse2[mb][r];
     bool sink_here = false;
 #pragma unroll
     for (int mb = 0; mb < kMB; ++mb) sink_here |= (uint32_t)(skey[mb] - t0) < (uint32_t)kTile;
@@ -969,56 +977,48 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
       constexpr bool kSmall = decltype(small_c)::value;
 #pragma unroll
       for (int mb = 0; mb < kMB; ++mb) {
-        const int m = mc * kRows + mb * 16 + li;
-        const int bound = kMasked ? row_bound(m, M, W, Lk) : 0;
+        int bound[4] = {0, 0, 0, 0}, sk[4] = {-1, -1, -1, -1};
+        float sn[4] = {0.f, 0.f, 0.f, 0.f};
+        if (kMasked)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; r += 2) {
-            float p[2];
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              p[e] = __builtin_amdgcn_exp2f(sacc[kb][mb][r + e] * scale_log2 - lse2[mb]);
-              if (kMasked) p[e] = (t0 + 16 * kb + 4 * lg + r + e) <= bound ? p[e] : 0.f;
-              if (!kSmall) p[e] = min_one_nonneg(p[e]);  // (small p: p <= 2^-13 already)
-            }
-            if (PR) round_through2<T>(p[0], p[1]);
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              float nd2 = min_zero(gacc[kb][mb][r + e]);  // -dist2/2, dist2 clamped at 0
-              if (kMasked) nd2 = (t0 + 16 * kb + 4 * lg + r + e) == skey[mb] ? snd2[mb] : nd2;
-              sc[kb][r + e] = fmaf(small_p_weight<kSmall>(p[e], eps, one_m2eps), nd2, sc[kb][r + e]);
-            }
+          for (int r = 0; r < 4; ++r) {
+            bound[r] = row_bound(mc * kRows + mb * 16 + 4 * lg + r, M, W, Lk);
+            sk[r] = __shfl(skey[mb], 4 * lg + r);
+            sn[r] = __shfl(snd2[mb], 4 * lg + r);
           }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const int key = t0 + 16 * kb + li;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float p = __builtin_amdgcn_exp2f(sacc[kb][mb][r]);
+            if (kMasked) p = key <= bound[r] ? p : 0.f;
+            if (!kSmall) p = min_one_nonneg(p);  // (small p: p <= 2^-13 already)
+            if (PR) p = round_through<T>(p);
+            float nd2 = min_zero(gacc[kb][mb][r]);  // -dist2/2, dist2 clamped at 0
+            if (kMasked) nd2 = key == sk[r] ? sn[r] : nd2;
+            sc[kb] = fmaf(kSmall ? small_weight_over_c2(p) : exact_weight(p, eps), nd2, sc[kb]);
+          }
+        }
       }
     };
-    if (pad_chunk || t0 + kTile > unmasked_end || wave_any(sink_here)) {
+    // The small-p tiles' sums carry w / c^2: scaled back below.
+    float tile_scale = 1.0f;
+    // (Padding rows need no mask: merge gives them lse = +inf and zero Q, so
+    // their p is 0.)
+    if (t0 + kTile > unmasked_end || wave_any(sink_here)) {
       epilogue(std::true_type{}, std::false_type{});
+    } else if (small_c2 > 0.f && !wave_any(!(tile_max(sacc) <= kSmallLog2P))) {
+      epilogue(std::false_type{}, std::true_type{});
+      tile_scale = small_c2;
     } else {
-      bool big = false;
-#pragma unroll
-      for (int mb = 0; mb < kMB; ++mb) big |= tile_max4x2(sacc, mb) * scale_log2 - lse2[mb] > kSmallLog2P;
-      if (wave_any(big))
-        epilogue(std::false_type{}, std::false_type{});
-      else
-        epilogue(std::false_type{}, std::true_type{});
+      epilogue(std::false_type{}, std::false_type{});
     }
-    // Sum over the 16 rows of lanes li = 0..15, a reduce-scatter on DPP
-    // (partners 15 - li, then 7 - li within each half, then li ^ 2 and
-    // li ^ 1: each step pairs lanes that keep complementary keys): lane li
-    // with li % 4 == 0 then holds key 16kb + 4lg + li/4.
-    const bool h8 = li & 8, h4 = li & 4;
+    // The four lane groups lg hold the same keys for different rows.
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      float k0 = h8 ? sc[kb][2] : sc[kb][0];
-      float k1 = h8 ? sc[kb][3] : sc[kb][1];
-      k0 += dpp_f<kDppMirror>(h8 ? sc[kb][0] : sc[kb][2]);
-      k1 += dpp_f<kDppMirror>(h8 ? sc[kb][1] : sc[kb][3]);
-      float v = h4 ? k1 : k0;
-      v += dpp_f<kDppHalfMirror>(h4 ? k0 : k1);
-      v += dpp_f<kDppQuadSwap2>(v);
-      v += dpp_f<kDppQuadSwap1>(v);
-      if ((li & 3) == 0) red[buf][wv][gt * kTile + 16 * kb + 4 * lg + (li >> 2)] = v;
+      const float v = add_xor16(add_xor32(sc[kb]));
+      if (lg == 0) red[buf][wv][gt * kTile + 16 * kb + li] = v * tile_scale;
     }
   };
 
@@ -1215,6 +1215,10 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
                                   int W, float eps, int p_round, int y_round, float* scores, char* ws,
                                   uint32_t* zero_ptr, int64_t zero_words, const FuseSelect* fuse, hipStream_t st) {
   const float scale_log2 = 1.4426950408889634f / sqrtf((float)D);
+  // c^2 = 1/(1+eps)^2 for pass 2's small-p weight, or 0 where eps is outside
+  // the range that form is exact for (then every tile takes the exact one).
+  const float small_c2 =
+      (eps >= 0.f && eps <= kSmallMaxEps) ? (float)(1.0 / ((1.0 + (double)eps) * (1.0 + (double)eps))) : 0.f;
   float* part_ml = reinterpret_cast<float*>(ws + p.off_ml);
   float* part_y = reinterpret_cast<float*>(ws + p.off_y);
   u32x4* opblk = reinterpret_cast<u32x4*>(ws + p.off_op);
@@ -1244,6 +1248,10 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
   launch((merge_kernel<T, D>), dim3((n_rows + kMergeRows - 1) / kMergeRows), dim3(64 * kMergeRows), 0, st,
                      part_ml, part_y, part_cand, p.n_mc, p.s1, p.M, n_rows, p_round, y_round, qq, q_sb, q_sh, q_ss,
                      q_sd, vv, kv_ld, Lk, Hkv, p.g, W, Lq, opblk, stblk, ystat, yf, zero_ptr, zero_words);
+  // Named here, right after merge, so that the compiler lays pass 2's code
+  // out next to pass 1's and merge's: the three run back to back, and their
+  // code shares each CU pair's instruction cache.
+  const auto k2 = p_round ? pass2_kernel<T, D, 8, 1, true> : pass2_kernel<T, D, 8, 1, false>;
   SelFuse fz{};
   // Row-chunks whose operands share LDS in one sweep over the keys (every
   // further group streams the workgroup's K/V range again): four when they
@@ -1266,13 +1274,12 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
     // One sweep over K/V for all row-chunks (pass2w); its LDS is static.
     if (p_round)
       launch((pass2w_kernel<T, D, DKV_P2_WIDE_GROUP, true>), g2, dim3(64 * kWideWaves), 0, st, kk, vv, kv_ld, Hkv, Lq,
-             Lk, W, p.g, p.M, p.n_mc, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
+             Lk, W, p.g, p.M, p.n_mc, p.s2, p.kps2, scale_log2, eps, small_c2, opblk, stblk, scores, fz);
     else
       launch((pass2w_kernel<T, D, DKV_P2_WIDE_GROUP, false>), g2, dim3(64 * kWideWaves), 0, st, kk, vv, kv_ld, Hkv,
-             Lq, Lk, W, p.g, p.M, p.n_mc, p.s2, p.kps2, scale_log2, eps, opblk, stblk, scores, fz);
+             Lq, Lk, W, p.g, p.M, p.n_mc, p.s2, p.kps2, scale_log2, eps, small_c2, opblk, stblk, scores, fz);
     return hipGetLastError();
   }
-  const auto k2 = p_round ? pass2_kernel<T, D, 8, 1, true> : pass2_kernel<T, D, 8, 1, false>;
   // The whole selection in pass 2's tail: needs the scores in LDS, an
   // output to emit into, and every workgroup of the grid running at once.
   if (fuse && fz.sc_lds && fuse->keep_idx && fuse->cp && g_tail_mode.load(std::memory_order_relaxed) &&
@@ -1291,7 +1298,7 @@ static hipError_t launch_scores_t(const ScorePlan& p, const void* q, int64_t q_s
     }
   }
   launch(k2, g2, dim3(512), lds2, st, kk, vv, kv_ld, Hkv, Lq, Lk, W, p.g, p.M, p.n_mc, cg, p.s2, p.kps2, scale_log2,
-         eps, opblk, stblk, scores, fz);
+         eps, small_c2, opblk, stblk, scores, fz);
   return hipGetLastError();
 }
 

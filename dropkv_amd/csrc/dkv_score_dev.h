@@ -35,9 +35,9 @@ __device__ __forceinline__ int row_bound(int m, int M, int W, int Lk) {
 }
 
 // Online-softmax step (base 2) of one 32-key tile starting at key t0, for
-// the lane's kMB row blocks: scales the logits s in place, applies the causal
-// bound (kMasked: tiles that reach it, or padding rows), updates the running
-// maximum m2 and sum lsum, rescales the y accumulators when a maximum moved,
+// the lane's kMB row blocks: applies the causal bound to the raw logits s in
+// place (kMasked: tiles that reach it, or padding rows), updates the running
+// maximum m2 and sum lsum (log2 units: logits times scale_log2), rescales the y accumulators when a maximum moved,
 // keeps the largest logit among the lane's own keys and the lowest key
 // holding it (lmax, larg: the candidates of merge's correction of y), and
 // returns the tile's P as two parts in the element type, hi and the rounded
@@ -50,15 +50,19 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
   constexpr int DT = D / 16;
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
+    // The largest raw logit of the lane (IEEE maximum: no canonicalising
+    // copies of the MFMA results); scaled once below.  Scaling by a
+    // positive factor keeps the order, so the scaled maximum is the maximum
+    // of the scaled logits.
     float tmax = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float x = s[kb][mb][r] * scale_log2;
+        float x = s[kb][mb][r];
         if (kMasked) x = (t0 + 16 * kb + 4 * lg + r) <= bound[mb] ? x : -INFINITY;
         s[kb][mb][r] = x;
-        tmax = fmaxf(tmax, x);
+        tmax = __builtin_elementwise_maximum(tmax, x);
       }
     {
       // The lane's own maximum so far and the lowest of its keys holding it
@@ -68,6 +72,7 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
       for (int kb = 1; kb >= 0; --kb)
 #pragma unroll
         for (int r = 3; r >= 0; --r) off = s[kb][mb][r] == tmax ? 16 * kb + r : off;
+      tmax *= scale_log2;
       const bool up = tmax > lmax[mb];
       lmax[mb] = up ? tmax : lmax[mb];
       larg[mb] = up ? t0 + 4 * lg + off : larg[mb];
@@ -77,14 +82,15 @@ __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB
     const bool empty = mnew == -INFINITY;
     const float alpha = empty ? 1.f : __builtin_amdgcn_exp2f(m2[mb] - mnew);
     // An empty row (every logit -inf so far) subtracts 0, so that its p are
-    // exp2(-inf) = 0 without a select per element.
+    // exp2(-inf) = 0 without a select per element.  p = 2^(s scale - max)
+    // with one rounding of the exponent.
     const float msub = empty ? 0.f : mnew;
     float psum = 0.f, pv[8];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pv[4 * kb + r] = __builtin_amdgcn_exp2f(s[kb][mb][r] - msub);
+        pv[4 * kb + r] = __builtin_amdgcn_exp2f(fmaf(s[kb][mb][r], scale_log2, -msub));
         psum += pv[4 * kb + r];
       }
     // P in the element type, two values per packed conversion.
@@ -548,29 +554,46 @@ __device__ __forceinline__ void merge_row(int rid, const float* __restrict__ par
   }
 }
 
-// The weight w = (p/(1-p+eps))^2 of pass 2 (dropkv_triton.py:589-591).
-// With kSmall the caller has shown p <= 2^kSmallLog2P for every p of the
-// wave's tile; then, with x = p - eps, 1/(1-x)^2 = 1 + 2x + 3x^2 + ... and
-// the terms from 3x^2 on stay below 3 * 2^-26 relative (under one fp32
-// ulp), so w = p^2 (1 + 2p - 2eps) to fp32 rounding, without the
-// reciprocal (a quarter-rate instruction).  one_m2eps = 1 - 2eps.
-constexpr float kSmallLog2P = -13.0f;
-template <bool kSmall>
-__device__ __forceinline__ float small_p_weight(float p, float eps, float one_m2eps) {
-  if constexpr (kSmall) {
-    return (p * p) * fmaf(2.0f, p, one_m2eps);
-  } else {
-    const float ratio = p * __builtin_amdgcn_rcpf(1.0f - p + eps);
-    return ratio * ratio;
-  }
+// The weight w = (p/(1-p+eps))^2 of pass 2 (dropkv_triton.py:589-591), in
+// the reference's order of operations.
+__device__ __forceinline__ float exact_weight(float p, float eps) {
+  const float ratio = p * __builtin_amdgcn_rcpf(1.0f - p + eps);
+  return ratio * ratio;
 }
 
-// The largest of a lane's logits of row block mb in a 32-key tile
-// (acc[kb][mb][r], two key blocks of four).
-__device__ __forceinline__ float tile_max4x2(const f32x4 (&acc)[2][kMB], int mb) {
-  const float a = fmaxf(fmaxf(acc[0][mb][0], acc[0][mb][1]), fmaxf(acc[0][mb][2], acc[0][mb][3]));
-  const float b = fmaxf(fmaxf(acc[1][mb][0], acc[1][mb][1]), fmaxf(acc[1][mb][2], acc[1][mb][3]));
-  return fmaxf(a, b);
+// Its small-p form.  With c = 1/(1+eps), w = c^2 p^2 / (1-cp)^2.  Where the
+// caller has shown p <= 2^kSmallLog2P for every p of the wave's tile and the
+// host has checked 0 <= eps <= kSmallMaxEps, (p + p^2)^2 = p^2 (1+p)^2
+// stands for p^2 / (1-cp)^2: their ratio is ((1+p)(1-cp))^2 =
+// (1 + p(1-c) - cp^2)^2 with 0 <= p(1-c) <= p eps <= 2^-25 and
+// cp^2 <= 2^-26, so within 2^-24 of 1 (under one fp32 ulp).  The caller
+// multiplies the tile's sums by c^2 (small_c2, computed on the host).  Two
+// operations, where the exact form takes four and a quarter-rate
+// reciprocal.
+constexpr float kSmallLog2P = -13.0f;
+constexpr float kSmallMaxEps = 0x1p-12f;
+__device__ __forceinline__ float small_weight_over_c2(float p) {
+  const float q = fmaf(p, p, p);
+  return q * q;
+}
+
+// The largest of a lane's values of a 32-key tile, x[kb][mb][r] over every
+// key block, row block and element; NaN if any is NaN.  (IEEE maximum: gfx950
+// has a three-operand form of it, where fmaxf first canonicalises each
+// operand with a copy.)
+__device__ __forceinline__ float fmax_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float tile_max(const f32x4 (&x)[2][kMB]) {
+  float t[2 * kMB];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb)
+      t[kb * kMB + mb] = fmax_nan(fmax_nan(x[kb][mb][0], x[kb][mb][1]), fmax_nan(x[kb][mb][2], x[kb][mb][3]));
+#pragma unroll
+  for (int n = 2 * kMB; n > 1; n >>= 1)
+#pragma unroll
+    for (int i = 0; i < n / 2; ++i) t[i] = fmax_nan(t[i], t[i + n / 2]);
+  return t[0];
 }
 
 // ---------------------------------------------------------------------------
