@@ -9,6 +9,7 @@ namespace dkv {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 // Element traits: the bf16 / fp16 operand vector (8 elements = 16 bytes =
 // one lane's share of a 16x16x32 MFMA operand) and the matching MFMA.
@@ -117,6 +118,12 @@ __device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
 }
 __device__ __forceinline__ void st_dev(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The same write-through policy (sc1) for a 16-byte buffer store.
+constexpr int kAuxSc1 = 16;
+__device__ __forceinline__ void st_dev16(rsrc_t r, uint32_t voff, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voff, 0, kAuxSc1);
 }
 
 // Order-preserving map float -> uint32 (larger float => larger key).

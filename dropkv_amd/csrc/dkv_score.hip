@@ -255,13 +255,25 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
              ((uint64_t)(uint32_t)__float_as_int(cs[j]) << 32) | (uint32_t)ck[j]);
   }
   __syncthreads();
-  float* py = part_y + slot * kRows * D;
-  for (int i = threadIdx.x; i < kRows * D; i += NT) {
-    const int row = i / D, d = i % D;
-    float y = 0.f;
+  // y of the workgroup, 16 bytes a thread and step, every LDS read of a
+  // thread issued before its first sum.
+  constexpr int NV = kRows * D / 4;
+  const rsrc_t yrs = make_rsrc(part_y + slot * kRows * D, (uint32_t)(kRows * D * sizeof(float)));
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) y += wbuf[((size_t)w * kRows + row) * kYPitch + d] * sm_f[w * kRows + row];
-    st_dev(py + i, y);
+  for (int j = 0; j < (NV + NT - 1) / NT; ++j) {
+    const int i = (int)threadIdx.x + j * NT;
+    if (NV % NT == 0 || i < NV) {
+      const int row = i / (D / 4), c4 = i % (D / 4);
+      f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        const f32x4 wb = *reinterpret_cast<const f32x4*>(wbuf + ((size_t)w * kRows + row) * kYPitch + 4 * c4);
+        const float f = sm_f[w * kRows + row];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = fmaf(wb[e], f, y[e]);
+      }
+      st_dev16(yrs, (uint32_t)i * 16u, y);
+    }
   }
 }
 

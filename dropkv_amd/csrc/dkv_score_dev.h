@@ -194,17 +194,26 @@ __device__ __forceinline__ void sort_lane_groups(float& v, int& k, int lg) {
 // Merges the WAVES waves' candidate lists of one row (4 per wave, each in
 // candidate order, at sm_cs / sm_ck[(w * kRows + row) * 4 ..]) into the
 // row's kCand first: each step takes the best head and advances that list.
+// All lists are read up front (one 16-byte LDS read each), so the merge
+// itself waits on no LDS round trip.
 template <int WAVES>
 __device__ __forceinline__ void merge_wave_cands(const float* sm_cs, const int* sm_ck, int row,
                                                  float (&cs)[kCand], int (&ck)[kCand]) {
   static_assert(kCand <= 4, "at most one list's length");
+  f32x4 lv[WAVES];
+  i32x4 lk[WAVES];
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    lv[w] = *reinterpret_cast<const f32x4*>(sm_cs + (w * kRows + row) * 4);
+    lk[w] = *reinterpret_cast<const i32x4*>(sm_ck + (w * kRows + row) * 4);
+  }
   float hv[WAVES];
   int hk[WAVES], hp[WAVES];
 #pragma unroll
   for (int w = 0; w < WAVES; ++w) {
     hp[w] = 0;
-    hv[w] = sm_cs[(w * kRows + row) * 4];
-    hk[w] = sm_ck[(w * kRows + row) * 4];
+    hv[w] = lv[w][0];
+    hk[w] = lk[w][0];
   }
 #pragma unroll
   for (int j = 0; j < kCand; ++j) {
@@ -220,13 +229,15 @@ __device__ __forceinline__ void merge_wave_cands(const float* sm_cs, const int* 
     }
     cs[j] = bv;
     ck[j] = bk;
+    if (j + 1 < kCand) {
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) {
-      if (bw == w) {
-        ++hp[w];
-        const bool more = hp[w] < 4;
-        hv[w] = more ? sm_cs[(w * kRows + row) * 4 + min(hp[w], 3)] : -INFINITY;
-        hk[w] = more ? sm_ck[(w * kRows + row) * 4 + min(hp[w], 3)] : -1;
+      for (int w = 0; w < WAVES; ++w) {
+        if (bw == w) {
+          ++hp[w];
+          // (hp <= j + 1 <= 3 here: the list has an entry at hp.)
+          hv[w] = hp[w] == 1 ? lv[w][1] : hp[w] == 2 ? lv[w][2] : lv[w][3];
+          hk[w] = hp[w] == 1 ? lk[w][1] : hp[w] == 2 ? lk[w][2] : lk[w][3];
+        }
       }
     }
   }

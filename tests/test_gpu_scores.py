@@ -95,6 +95,28 @@ def test_lq_lt_lk(gpu, cfg, Lq, Lk):
     _close_rel(got, ref, rtol=1e-4)
 
 
+@pytest.mark.parametrize("eps", [0.0, 1e-6, 2.0 ** -12, 1e-2, 0.5])
+@pytest.mark.parametrize("p_round", [False, True])
+def test_eps_vs_oracle(gpu, eps, p_round):
+    """The weight (p/(1-p+eps))^2 at several eps (reference dropkv_triton.py:589-591).
+    16384 keys of near-uniform attention put every tile's p under 2^-13, where
+    pass 2 takes its reciprocal-free form for 0 <= eps <= 2^-12 (so 0, 1e-6
+    and 2^-12 run it, and 1e-2 and 0.5 run the exact form everywhere).  fp32 mode: rtol 1e-4;
+    bf16 mode: rtol 2e-2 / atol 1e-3 with at most 0.1% of keys beyond 1e-3."""
+    from dropkv_amd import dropkv_scores_triton
+    cfg = dict(B=1, Hq=8, Hkv=2, D=128)
+    Q, K, V = make_qkv(cfg, 64, 16384, seed=19)
+    Q = (Q.float() * 0.1).to(Q.dtype)  # logits of spread ~0.1: p ~ 2^-14 everywhere
+    ref = R.dropkv_scores_reference(Q, K, V, eps=eps, match_pytorch_precision=p_round)
+    got = dropkv_scores_triton(Q.to(gpu), K.to(gpu), V.to(gpu), eps=eps, match_pytorch_precision=p_round).cpu()
+    if not p_round:
+        _close_rel(got, ref, rtol=1e-4)
+    else:
+        torch.testing.assert_close(got, ref, rtol=2e-2, atol=1e-3)
+        rel = (got - ref).abs() / ref.abs().clamp_min(1e-30)
+        assert (rel > 1e-3).float().mean().item() < 1e-3
+
+
 def test_large_window(gpu):
     """W=65 > a 64-key block: splits entirely past some rows' causal bound
     (reference tests:1654-1743)."""
