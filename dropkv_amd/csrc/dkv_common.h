@@ -216,6 +216,17 @@ __device__ __forceinline__ float add_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// The value of lane i ^ 16 (resp. i ^ 32): the swap's two results are the
+// values of the lane with that bit clear and of the lane with it set.
+__device__ __forceinline__ uint32_t from_xor16(uint32_t x, int lane) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  return (lane & 16) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t from_xor32(uint32_t x, int lane) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return (lane & 32) ? r[0] : r[1];
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);

@@ -193,10 +193,13 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   load_v_pairs<T, D>(va, vb, vrs, v_lane, t);
   for (; t < nrel; t += stride) tile(kop, va, vb, k_begin + t, t + stride);
 
-  // Row sums are per lane-group partials; fold the four groups.
+  // Row sums are per lane-group partials; fold the four groups.  The lanes'
+  // candidates of a row go into candidate order along the lane groups (lane
+  // swaps, no LDS: done before the barrier).
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
     lsum[mb] = add_xor32(add_xor16(lsum[mb]));
+    sort_lane_groups(lmax[mb], larg[mb], lg);
   }
 
   // Cross-wave merge in LDS (the V tiles are dead now): every wave stores
@@ -214,7 +217,6 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
     const int ci = (wv * kRows + 16 * mb + li) * 4 + lg;
-    sort_lane_groups(lmax[mb], larg[mb], lg);
     sm_cs[ci] = lmax[mb];
     sm_ck[ci] = larg[mb];
     if (lg == 0) {

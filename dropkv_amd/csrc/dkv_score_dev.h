@@ -175,11 +175,13 @@ __device__ __forceinline__ bool cand_before(float va, int ka, float vb, int kb) 
 
 // Sorts the four (logit, key) candidates of a row held by the lanes of its
 // four lane groups (lg = lane / 16) into candidate order along lg (a bitonic
-// network over lane shuffles).
+// network over lane swaps).
 __device__ __forceinline__ void sort_lane_groups(float& v, int& k, int lg) {
+  const int lane = lg << 4;  // (only bits 4 and 5 are read)
   auto step = [&](int mask, bool keep_first) {
-    const float ov = __shfl_xor(v, mask);
-    const int ok = __shfl_xor(k, mask);
+    const float ov = __uint_as_float(mask == 16 ? from_xor16(__float_as_uint(v), lane)
+                                                : from_xor32(__float_as_uint(v), lane));
+    const int ok = (int)(mask == 16 ? from_xor16((uint32_t)k, lane) : from_xor32((uint32_t)k, lane));
     const bool mine_first = cand_before(v, k, ov, ok);
     if (mine_first != keep_first) {
       v = ov;
