@@ -58,12 +58,16 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   constexpr int KK = D / 32;
   constexpr int DT = D / 16;
   constexpr int CPR = D / 8;           // 16-byte chunks per key row
-  constexpr int GRP = 64 / CPR;        // key pairs covered per load round
-  constexpr int NIT = (kTile / 2) / GRP;
+  constexpr int GRP = 64 / CPR;        // key rows covered per load round
+  constexpr int NVC = kTile / GRP;     // V chunks per lane and tile
   constexpr int NT = 64 * WAVES;
+  // A wave's V tile in LDS: its rows as loaded, padded so that the
+  // transposing reads (16 lanes: 4 rows x 32 bytes) hit no bank twice.
+  constexpr int kVPitch = D + 16;
+  constexpr int kVTileWords = kTile * kVPitch / 2;
 
   constexpr int kYPitch = D + 4;  // fp32 row pitch of the merge buffer
-  constexpr int kLdsTiles = WAVES * D * kPitch;
+  constexpr int kLdsTiles = WAVES * kVTileWords;
   constexpr int kLdsMerge = 3 * WAVES * kRows + 8 * WAVES * kRows + WAVES * kRows * kYPitch;
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsTiles > kLdsMerge ? kLdsTiles : kLdsMerge];
 
@@ -95,8 +99,16 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   const uint32_t range = (uint32_t)(k_end - k_begin) * (D * sizeof(T));
   const rsrc_t krs = make_rsrc(kp + roff, range), vrs = make_rsrc(vp + roff, range);
   const uint32_t k_lane = (li * D + 8 * lg) * sizeof(T);
-  const uint32_t v_lane = (2 * (lane / CPR) * D + 8 * (lane % CPR)) * sizeof(T);
-  uint32_t* vt = lds + wv * D * kPitch;
+  // V chunk i of a lane: row lane / CPR + i * GRP of the tile, columns
+  // 8 (lane % CPR) .. +7.
+  const uint32_t v_lane = ((lane / CPR) * D + 8 * (lane % CPR)) * sizeof(T);
+  const int v_row = lane / CPR, v_col = 8 * (lane % CPR);
+  uint32_t* vt = lds + wv * kVTileWords;
+  auto load_v = [&](u32x4 (&vc)[NVC], int t) __attribute__((always_inline)) {
+    const uint32_t base = v_lane + (uint32_t)t * (D * sizeof(T));
+#pragma unroll
+    for (int i = 0; i < NVC; ++i) vc[i] = buf_load16(vrs, base + (uint32_t)(i * GRP * D * sizeof(T)));
+  };
 
   float m2[kMB], lsum[kMB];
   // Per lane: the largest logit among its own keys and the lowest key
@@ -115,13 +127,13 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   }
 
   v8 kop[2][KK];
-  u32x4 va[NIT], vb[NIT];
+  u32x4 vch[NVC];
   const int stride = WAVES * kTile;
 
   // One tile (t0 absolute, tn relative to k_begin): consume the K/V
   // registers, refill them with tile tn (zeros past the range), then the
   // softmax and P.V work, which overlaps both tiles' loads.
-  auto tile = [&](v8 (&kop)[2][KK], u32x4 (&va)[NIT], u32x4 (&vb)[NIT], int t0, int tn)
+  auto tile = [&](v8 (&kop)[2][KK], u32x4 (&vch)[NVC], int t0, int tn)
       __attribute__((always_inline)) {
     // S^T = K Q^T.
     f32x4 s[2][kMB];
@@ -139,25 +151,13 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     // exact) before waiting for this tile's V.
     load_rows_op<T, D>(kop, krs, k_lane, tn);
 
-    // Transposed V tile -> LDS: dword (d, pair p) = {V[2p][d], V[2p+1][d]}.
-    // The pair column is XOR-swizzled with bits 4-5 of d to spread banks.
+    // The V rows -> LDS, as loaded.
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int p = it * GRP + lane / CPR;
-      const int c = lane % CPR;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t a = va[it][j], bb = vb[it][j];
-        const uint32_t lo = __builtin_amdgcn_perm(bb, a, 0x05040100u);
-        const uint32_t hi = __builtin_amdgcn_perm(bb, a, 0x07060302u);
-        const int d0 = 8 * c + 2 * j, d1 = d0 + 1;
-        vt[d0 * kPitch + (p ^ (4 * ((d0 >> 4) & 3)))] = lo;
-        vt[d1 * kPitch + (p ^ (4 * ((d1 >> 4) & 3)))] = hi;
-      }
-    }
+    for (int i = 0; i < NVC; ++i)
+      *reinterpret_cast<u32x4*>(vt + ((v_row + i * GRP) * kVPitch + v_col) / 2) = vch[i];
 
     // The V registers are free again: start the V loads of tile tn.
-    load_v_pairs<T, D>(va, vb, vrs, v_lane, tn);
+    load_v(vch, tn);
 
     // Online softmax.  P enters the MFMA as hi + lo: the p of a tile is
     // relative to the running maximum, so rounding it to the input dtype
@@ -169,14 +169,22 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
     else
       softmax_tile<T, D, false>(s, m2, lsum, lmax, larg, yacc, phi, plo, bound, t0, lg, scale_log2);
 
-    // Y^T += V^T P^T.  Lane (li, lg) reads V^T[16dt+li][keys 4lg..4lg+3, 16+4lg..+3].
+    // Y^T += V^T P^T, V^T read transposed from the V rows in LDS: lane
+    // (li, lg) needs V[key][16dt + li] for keys 4lg + e and 16 + 4lg + e
+    // (e = 0..3, the keys of its P^T operand).  A transposing read gives
+    // output lane i of each 16-lane group element e of input lane 4e + i/4's
+    // 8 bytes, element i % 4; so input lane li reads key base + li/4,
+    // columns 16dt + 4(li % 4) .. +3.
+    const int tr_row = 4 * lg + li / 4, tr_col = 4 * (li % 4);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const int d = 16 * dt + li;
-      const int sw = 4 * (dt & 3);
-      const u32x2 x0 = *reinterpret_cast<const u32x2*>(vt + d * kPitch + ((2 * lg) ^ sw));
-      const u32x2 x1 = *reinterpret_cast<const u32x2*>(vt + d * kPitch + ((8 + 2 * lg) ^ sw));
-      const v8 aop = bitcast_u4<v8>(u32x4{x0[0], x0[1], x1[0], x1[1]});
+      typedef short s4 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) s4 lds_s4;
+      const T* vrow = reinterpret_cast<const T*>(vt);
+      const s4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(vrow + tr_row * kVPitch + 16 * dt + tr_col));
+      const s4 x1 =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(vrow + (16 + tr_row) * kVPitch + 16 * dt + tr_col));
+      const v8 aop = __builtin_bit_cast(v8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
       for (int mb = 0; mb < kMB; ++mb) {
         yacc[dt][mb] = Elem<T>::mfma(aop, phi[mb], yacc[dt][mb]);
@@ -190,8 +198,8 @@ pass1_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, 
   const int nrel = k_end - k_begin;
   int t = wv * kTile;  // relative to k_begin
   load_rows_op<T, D>(kop, krs, k_lane, t);  // zeros if t >= nrel
-  load_v_pairs<T, D>(va, vb, vrs, v_lane, t);
-  for (; t < nrel; t += stride) tile(kop, va, vb, k_begin + t, t + stride);
+  load_v(vch, t);
+  for (; t < nrel; t += stride) tile(kop, vch, k_begin + t, t + stride);
 
   // Row sums are per lane-group partials; fold the four groups.  The lanes'
   // candidates of a row go into candidate order along the lane groups (lane
@@ -306,12 +314,14 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
   constexpr int DT = D / 16;
   constexpr int NT = 64 * kWideWaves;
   constexpr int CPR = D / 8;                 // 16-byte chunks per key row
-  constexpr int KCH = kTile * CPR;           // K chunks per tile
-  constexpr int VPR = (kTile / 2) * CPR;     // (key pair, chunk) items of V per tile
-  static_assert(KCH <= NT && VPR <= NT, "one K chunk and one V pair per thread");
+  constexpr int KCH = kTile * CPR;           // K (and V) chunks per tile
+  static_assert(KCH <= NT, "one K chunk and one V chunk per thread");
   constexpr int kKPitch = D + 8;             // elements per padded K row in LDS
   constexpr int kKWords = kTile * kKPitch / 2;
-  constexpr int kVWords = D * kPitch;
+  // V rows as loaded, padded so that the transposing reads below (16 lanes:
+  // 4 rows x 32 bytes) cover the banks without conflicts.
+  constexpr int kVPitch = D + 16;
+  constexpr int kVWords = kTile * kVPitch / 2;
   constexpr int kTileWords = kKWords + kVWords;
   constexpr int kStage = kWideG * kTileWords;  // dwords per buffer stage
   __shared__ __attribute__((aligned(16))) uint32_t lds[2 * kStage];
@@ -342,22 +352,19 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
   const int64_t roff = ((int64_t)head * kv_ld + k_begin) * D;
   const uint32_t range = (uint32_t)(k_end - k_begin) * (D * sizeof(T));
   const rsrc_t krs = make_rsrc(kp + roff, range), vrs = make_rsrc(vp + roff, range);
-  // This thread's share of a tile: K chunk tid (row tid / CPR, chunk tid % CPR)
-  // and V pair item tid (keys 2p, 2p+1, chunk c).
+  // This thread's share of a tile: chunk tid of K and of V (row tid / CPR,
+  // chunk tid % CPR).
   const int kr = tid / CPR, kc = tid % CPR;
-  const int vpi = tid / CPR, vc = tid % CPR;
   const uint32_t k_off = (uint32_t)(kr * D + 8 * kc) * sizeof(T);
-  const uint32_t v_off = (uint32_t)(2 * vpi * D + 8 * vc) * sizeof(T);
-  u32x4 kreg[kWideG], va[kWideG], vb[kWideG];
+  u32x4 kreg[kWideG], vreg[kWideG];
   // Loads of tile group grp (rows past the range read as zeros).
   auto issue = [&](int grp) __attribute__((always_inline)) {
 #pragma unroll
     for (int gt = 0; gt < kWideG; ++gt) {
       const uint32_t base = (uint32_t)((grp * kWideG + gt) * kTile) * (D * sizeof(T));
-      if (tid < KCH) kreg[gt] = buf_load16(krs, base + k_off);
-      if (tid < VPR) {
-        va[gt] = buf_load16(vrs, base + v_off);
-        vb[gt] = buf_load16(vrs, base + v_off + D * sizeof(T));
+      if (tid < KCH) {
+        kreg[gt] = buf_load16(krs, base + k_off);
+        vreg[gt] = buf_load16(vrs, base + k_off);
       }
     }
   };
@@ -366,16 +373,9 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
     for (int gt = 0; gt < kWideG; ++gt) {
       uint32_t* kl = lds + buf * kStage + gt * kTileWords;
       uint32_t* vt = kl + kKWords;
-      if (tid < KCH) *reinterpret_cast<u32x4*>(kl + (kr * kKPitch + 8 * kc) / 2) = kreg[gt];
-      if (tid < VPR) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t lo = __builtin_amdgcn_perm(vb[gt][j], va[gt][j], 0x05040100u);
-          const uint32_t hi = __builtin_amdgcn_perm(vb[gt][j], va[gt][j], 0x07060302u);
-          const int d0 = 8 * vc + 2 * j, d1 = d0 + 1;
-          vt[d0 * kPitch + (vpi ^ (4 * ((d0 >> 4) & 3)))] = lo;
-          vt[d1 * kPitch + (vpi ^ (4 * ((d1 >> 4) & 3)))] = hi;
-        }
+      if (tid < KCH) {
+        *reinterpret_cast<u32x4*>(kl + (kr * kKPitch + 8 * kc) / 2) = kreg[gt];
+        *reinterpret_cast<u32x4*>(vt + (kr * kVPitch + 8 * kc) / 2) = vreg[gt];
       }
     }
   };
@@ -430,14 +430,23 @@ pass1w_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
         softmax_tile<T, D, true>(s, m2, lsum, lmax, larg, yacc, phi, plo, bound, t0, lg, scale_log2);
       else
         softmax_tile<T, D, false>(s, m2, lsum, lmax, larg, yacc, phi, plo, bound, t0, lg, scale_log2);
-      // Y^T += V^T P^T with V^T from LDS.
+      // Y^T += V^T P^T with V^T read transposed from the V rows in LDS: lane
+      // (li, lg) needs V[key][16dt + li] for keys 4lg + e and 16 + 4lg + e
+      // (e = 0..3, the keys of its P^T operand).  A transposing read gives
+      // output lane i of each 16-lane group element e of input lane 4e + i/4's
+      // 8 bytes, element i % 4; so input lane li reads key base + li/4,
+      // columns 16dt + 4(li % 4) .. +3.
+      const int tr_row = 4 * lg + li / 4, tr_col = 4 * (li % 4);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const int d = 16 * dt + li;
-        const int sw = 4 * (dt & 3);
-        const u32x2 x0 = *reinterpret_cast<const u32x2*>(vt + d * kPitch + ((2 * lg) ^ sw));
-        const u32x2 x1 = *reinterpret_cast<const u32x2*>(vt + d * kPitch + ((8 + 2 * lg) ^ sw));
-        const v8 aop = bitcast_u4<v8>(u32x4{x0[0], x0[1], x1[0], x1[1]});
+        typedef short s4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) s4 lds_s4;
+        const T* vrow = reinterpret_cast<const T*>(vt);
+        const s4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s4*)(vrow + tr_row * kVPitch + 16 * dt + tr_col));
+        const s4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s4*)(vrow + (16 + tr_row) * kVPitch + 16 * dt + tr_col));
+        const v8 aop = __builtin_bit_cast(v8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb) {
           yacc[dt][mb] = Elem<T>::mfma(aop, phi[mb], yacc[dt][mb]);
@@ -570,7 +579,6 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
   const int head = lid / n_splits;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int mpad = n_mc * kRows;
 
   // The per-key sums hold sum_m w * (-dist2/2): scale by -2/g at the end.
   const float out_scale = -2.0f * (1.0f / static_cast<float>(g));

@@ -24,7 +24,6 @@ constexpr int kMB = kRows / 16;
 constexpr int kYParts = 2;
 constexpr int kOpSlots = 1 + kYParts;  // Q and the parts of Y, per row block and k-step
 constexpr int kStatWords = 64;         // per 16-row block: lse, |y|^2, sink key, -dist2/2 at it
-constexpr int kPitch = 18;          // dwords per row of the transposed V tile
 // Candidate keys per (row, split) for merge's rounding correction of y: the
 // keys holding the largest logits among those of individual lanes.
 constexpr int kCand = 4;
@@ -265,22 +264,6 @@ __device__ __forceinline__ void load_rows_op(typename Elem<T>::v8 (&op)[2][D / 3
 #pragma unroll
     for (int kk = 0; kk < D / 32; ++kk)
       op[kb][kk] = bitcast_u4<v8>(buf_load16(rs, base + (16 * kb * D + 32 * kk) * sizeof(T)));
-}
-
-// 32 value rows in coalesced 16-byte chunks, two adjacent keys per lane
-// (pairs p, chunk c) for the transposed LDS tile.  `lane_off` =
-// (2*(lane/CPR)*D + 8*(lane%CPR)) * sizeof(T).
-template <typename T, int D>
-__device__ __forceinline__ void load_v_pairs(u32x4 (&va)[(kTile / 2) / (64 / (D / 8))],
-                                             u32x4 (&vb)[(kTile / 2) / (64 / (D / 8))], rsrc_t rs,
-                                             uint32_t lane_off, int t) {
-  constexpr int CPR = D / 8, GRP = 64 / CPR, NIT = (kTile / 2) / GRP;
-  const uint32_t base = lane_off + (uint32_t)t * (D * sizeof(T));
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    va[it] = buf_load16(rs, base + (2 * it * GRP) * D * sizeof(T));
-    vb[it] = buf_load16(rs, base + (2 * it * GRP + 1) * D * sizeof(T));
-  }
 }
 
 template <typename T>
