@@ -1126,7 +1126,7 @@ static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b)
 #define DKV_P1_WIDE_MIN 3      // row-chunks from which pass 1 shares tiles across chunks (0: never)
 #endif
 #ifndef DKV_P1_WIDE_GROUP
-#define DKV_P1_WIDE_GROUP 1    // tiles per LDS stage of the wide pass 1 (1, 2 or 4)
+#define DKV_P1_WIDE_GROUP 2    // tiles per LDS stage of the wide pass 1 (1, 2 or 4)
 #endif
 #ifndef DKV_P2_WIDE_GROUP
 #define DKV_P2_WIDE_GROUP 3    // tiles per LDS stage of the wide pass 2 (1 to 3)
