@@ -117,6 +117,28 @@ def test_eps_vs_oracle(gpu, eps, p_round):
         assert (rel > 1e-3).float().mean().item() < 1e-3
 
 
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("g,W", [(4, 25), (8, 18), (8, 32)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_wide_row_chunks_vs_oracle(gpu, D, g, W, dtype):
+    """g*W = 100, 144 (four and five 32-row chunks, the last one padded) and
+    256 query rows per KV head: the kernels that share each K/V tile across
+    3-8 row-chunks (one chunk per wave; V staged in LDS and read transposed), at every
+    matrix-core head dimension, against the oracle in fp32 mode (rtol 1e-4)
+    and the p-rounding mode (rtol 2e-2 / atol 1e-3, at most 0.1% beyond 1e-3)."""
+    from dropkv_amd import dropkv_scores_triton
+    cfg = dict(B=1, Hq=2 * g, Hkv=2, D=D)
+    Q, K, V = make_qkv(cfg, 2048, 3000, dtype=dtype, seed=D + g + W)
+    ref = R.dropkv_scores_reference(Q, K, V, window_size=W, match_pytorch_precision=False)
+    got = dropkv_scores_triton(Q.to(gpu), K.to(gpu), V.to(gpu), window_size=W, match_pytorch_precision=False)
+    _close_rel(got, ref, rtol=1e-4)
+    ref = R.dropkv_scores_reference(Q, K, V, window_size=W, match_pytorch_precision=True)
+    got = dropkv_scores_triton(Q.to(gpu), K.to(gpu), V.to(gpu), window_size=W, match_pytorch_precision=True).cpu()
+    torch.testing.assert_close(got, ref, rtol=2e-2, atol=1e-3)
+    rel = (got - ref).abs() / ref.abs().clamp_min(1e-30)
+    assert (rel > 1e-3).float().mean().item() < 1e-3
+
+
 def test_large_window(gpu):
     """W=65 > a 64-key block: splits entirely past some rows' causal bound
     (reference tests:1654-1743)."""
