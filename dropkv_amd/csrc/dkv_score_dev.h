@@ -36,11 +36,12 @@ __device__ __forceinline__ int row_bound(int m, int M, int W, int Lk) {
 // Online-softmax step (base 2) of one 32-key tile starting at key t0, for
 // the lane's kMB row blocks: applies the causal bound to the raw logits s in
 // place (kMasked: tiles that reach it, or padding rows), updates the running
-// maximum m2 and sum lsum (log2 units: logits times scale_log2), rescales the y accumulators when a maximum moved,
-// keeps the largest logit among the lane's own keys and the lowest key
-// holding it (lmax, larg: the candidates of merge's correction of y), and
-// returns the tile's P as two parts in the element type, hi and the rounded
-// remainder lo (~16 significant bits together).
+// maximum m2 and sum lsum (log2 units: logits times scale_log2), rescales
+// the y accumulators when a maximum moved, keeps the largest logit among the
+// lane's own keys and the lowest key holding it (lmax, larg: the candidates
+// of merge's correction of y), and returns the tile's P as two parts in the
+// element type, hi and the rounded remainder lo (~16 significant bits
+// together).
 template <typename T, int D, bool kMasked>
 __device__ __forceinline__ void softmax_tile(f32x4 (&s)[2][kMB], float (&m2)[kMB], float (&lsum)[kMB],
                                              float (&lmax)[kMB], int (&larg)[kMB], f32x4 (&yacc)[D / 16][kMB],
