@@ -79,6 +79,47 @@ def test_decode_attention_strided_inputs(gpu):
     torch.testing.assert_close(out.float(), _ref_attention(q, k_rows, v_rows, D ** -0.5), rtol=2e-2, atol=2e-2)
 
 
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 14, 2), (128, 16, 1)])
+@pytest.mark.parametrize("C,n", [
+    (4160, 4159),   # 64 splits of 65 rows (two steps each, the second of one row); last row of the buffer
+    (4160, 4100),
+    (4160, 64),     # the new row alone in split 0's second step
+    (4160, 65),     # the new row first in split 1; splits 2.. empty
+    (4160, 0),      # only the new row
+    (200, 130),     # 4 splits of 50 rows: one partial step each
+])
+def test_decode_attention_split_edges_nan_rows(gpu, D, Hq, Hkv, C, n):
+    """Split rows are fixed by the capacity, so splits can run two steps,
+    end in a partial step, or hold no row at all. Every buffer row from the
+    new row's position on holds NaN: the rows past it are masked out of the
+    logits and out of P.V (0 * NaN is NaN), and the buffer keeps them as
+    they were; row n ends up holding the new row."""
+    from dropkv_amd import ops
+    B = 1
+    g = torch.Generator().manual_seed(7 * C + n + D)
+    kb = torch.randn(B, Hkv, C, D, generator=g).bfloat16()
+    vb = torch.randn(B, Hkv, C, D, generator=g).bfloat16()
+    kb[:, :, n:] = float("nan")
+    vb[:, :, n:] = float("nan")
+    kb, vb = kb.to(gpu), vb.to(gpu)
+    q = torch.randn(B, Hq, 1, D, generator=g).bfloat16().to(gpu)
+    kn = torch.randn(B, Hkv, 1, D, generator=g).bfloat16().to(gpu)
+    vn = torch.randn(B, Hkv, 1, D, generator=g).bfloat16().to(gpu)
+    k_before, v_before = kb.clone(), vb.clone()
+    n_rows = torch.tensor([n], dtype=torch.int32, device=gpu)
+    out = torch.empty(B, 1, Hq, D, dtype=torch.bfloat16, device=gpu)
+    ops.decode_attention(q, kn, vn, kb, vb, n_rows, D ** -0.5, out, ops.decode_workspace(B, Hq, Hkv, D, C, gpu))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    ref = _ref_attention(q, torch.cat([k_before[:, :, :n], kn], dim=2), torch.cat([v_before[:, :, :n], vn], dim=2),
+                         D ** -0.5)
+    torch.testing.assert_close(out.float(), ref, rtol=2e-2, atol=2e-2)
+    assert torch.equal(kb[:, :, n], kn[:, :, 0]) and torch.equal(vb[:, :, n], vn[:, :, 0])
+    for buf, before in ((kb, k_before), (vb, v_before)):
+        assert torch.equal(buf[:, :, :n], before[:, :, :n])
+        assert torch.equal(buf[:, :, n + 1:].view(torch.int16), before[:, :, n + 1:].view(torch.int16))
+
+
 TINY = dict(vocab_size=1000, hidden_size=512, intermediate_size=1024, num_hidden_layers=3,
             num_attention_heads=8, num_key_value_heads=2, max_position_embeddings=8192)
 
