@@ -5,7 +5,8 @@ the CPU oracle.
 * C2 -- B1 Hq32 Hkv8 D128 Lq=Lk=32768 bf16, K with a LogNormal per-channel
   scale, W8 ks11 r0.1: every row's scores (bf16 bar) and kept set (tie-aware
   overlap), gather bit-exact, the one-call layer path equal to the separate
-  scoring op bit for bit.
+  scoring op bit for bit; the same shape with fp16 inputs (p rounded to
+  fp16), and in fp32 mode.
 * C3 -- a 4096-query chunk against Lk = 4096 n (kernel sweep, Q as a strided
   slice of the 65536-row prompt), and the ``every_chunk`` cache flow over 16
   chunks (Lk_n = keep_{n-1} + 4096, keep_n = int(0.1 * 4096 n)), each
@@ -64,6 +65,35 @@ def test_c2_full_size(gpu):
     # within 2e-2 relative, fewer than 1e-3 of them beyond 1e-3.
     stats = assert_binding_scores(s, ref, pooled, keep, Qt, K, V, W, torch.bfloat16, 2e-2, 1e-3, 1e-3)
     print(f"[c2] binding keys {stats[0]}, worst rel {stats[1]:.2e}, beyond 1e-3: {stats[2]}, sinks {stats[3]}")
+    worst, unexcused = R.index_overlap(idx.cpu(), ref_idx, pooled)
+    assert worst >= 0.999, (worst, unexcused)
+    rk, rv = R.gather_compressed(K, V, idx.cpu())
+    assert torch.equal(kc.cpu(), rk) and torch.equal(vc.cpu(), rv)
+    del Qg, Kg, Vg, plan
+    _free()
+
+
+def test_c2_full_size_fp16(gpu):
+    """The C2 shape with fp16 inputs: p rounded to fp16 before the weight,
+    as the reference's F.softmax(...).to(float16) (dropkv_triton.py:88-93),
+    through the one-call layer path; the binding keys at the bf16 bars
+    (arbitrated by the float64 bracket with fp16 rounding), the kept set
+    against the float32 reference (tie-aware overlap) and the gather bit for
+    bit."""
+    from dropkv_amd import ops
+    L, W, ks, ratio = 32768, 8, 11, 0.1
+    Q, K, V = make_qkv(LLAMA_CFG, L, dtype=torch.float16, seed=1, k_scale="lognormal")
+    keep = R.keep_length(ratio, L, W)
+    Qg, Kg, Vg = Q.to(gpu), K.to(gpu), V.to(gpu)
+    plan = ops.EvictPlan(Qg, Kg, W, ks, keep, keep_scores=True)
+    idx, kc, vc = plan(Qg, Kg, Vg)
+    s = plan.scores
+    Qt = Q[:, :, -W:].contiguous()
+    ref = R.dropkv_scores_reference(Qt, K, V, W, match_pytorch_precision=True)
+    _close(s, ref, 2e-2, 1e-3)
+    ref_idx, pooled = R.compute_keep_indices(Qt, K, V, ratio, W, ks, scores=ref)
+    stats = assert_binding_scores(s, ref, pooled, keep, Qt, K, V, W, torch.float16, 2e-2, 1e-3, 1e-3)
+    print(f"[c2 fp16] binding keys {stats[0]}, worst rel {stats[1]:.2e}, beyond 1e-3: {stats[2]}, sinks {stats[3]}")
     worst, unexcused = R.index_overlap(idx.cpu(), ref_idx, pooled)
     assert worst >= 0.999, (worst, unexcused)
     rk, rv = R.gather_compressed(K, V, idx.cpu())
