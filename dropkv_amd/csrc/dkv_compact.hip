@@ -59,8 +59,8 @@ compact_kernel(Seg s0, Seg s1, int H, int units_per_row, const int64_t* __restri
       const int t = t0 + q * kCopyThreads;
       if (t < total) {
         const int64_t o = ((int64_t)bh * keep + r0 + t / units_per_row) * out_row_bytes;
-        reinterpret_cast<U*>(ko + o)[t % units_per_row] = kval[q];
-        reinterpret_cast<U*>(vo + o)[t % units_per_row] = vval[q];
+        __builtin_nontemporal_store(kval[q], reinterpret_cast<U*>(ko + o) + t % units_per_row);
+        __builtin_nontemporal_store(vval[q], reinterpret_cast<U*>(vo + o) + t % units_per_row);
       }
     }
   }
@@ -96,8 +96,8 @@ append_kernel(Seg s, int H, int units_per_row, int L, int blocks_per_head, uint8
       const int t = t0 + q * kCopyThreads;
       if (t < total) {
         const int64_t o = ((int64_t)bh * dst_ld + row0 + r0 + t / units_per_row) * row_bytes;
-        reinterpret_cast<U*>(dk + o)[t % units_per_row] = kval[q];
-        reinterpret_cast<U*>(dv + o)[t % units_per_row] = vval[q];
+        __builtin_nontemporal_store(kval[q], reinterpret_cast<U*>(dk + o) + t % units_per_row);
+        __builtin_nontemporal_store(vval[q], reinterpret_cast<U*>(dv + o) + t % units_per_row);
       }
     }
   }
@@ -116,7 +116,7 @@ hipError_t launch_append(const void* k, const void* v, int64_t s_b, int64_t s_h,
   uint8_t* k8 = static_cast<uint8_t*>(dk);
   uint8_t* v8 = static_cast<uint8_t*>(dv);
   if (vec)
-    launch(append_kernel<uint4>, grid, dim3(kCopyThreads), 0, st, a, (int)H, (int)(row_bytes / 16), (int)L, bph, k8,
+    launch(append_kernel<u32x4>, grid, dim3(kCopyThreads), 0, st, a, (int)H, (int)(row_bytes / 16), (int)L, bph, k8,
            v8, dst_ld, row0);
   else if (eb == 2)
     launch(append_kernel<uint16_t>, grid, dim3(kCopyThreads), 0, st, a, (int)H, (int)D, (int)L, bph, k8, v8, dst_ld,
@@ -147,7 +147,7 @@ hipError_t launch_compact(const void* k0, const void* v0, int64_t s0b, int64_t s
   const int bph = (int)((keep + kRowsPerBlock - 1) / kRowsPerBlock);
   const dim3 grid((unsigned)(B * H * bph));
   if (vec) {
-    launch(compact_kernel<uint4>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)(row_bytes / 16),
+    launch(compact_kernel<u32x4>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)(row_bytes / 16),
                        idx, (int)keep, bph, static_cast<uint8_t*>(ko), static_cast<uint8_t*>(vo));
   } else if (eb == 2) {
     launch(compact_kernel<uint16_t>, grid, dim3(kCopyThreads), 0, st, a, c, (int)H, (int)D, idx,
