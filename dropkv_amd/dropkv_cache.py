@@ -32,6 +32,28 @@ from .hf_query import take_captured_query
 logger = logging.getLogger(__name__)
 
 
+def cat_rows(k0: torch.Tensor, v0: torch.Tensor, k1: torch.Tensor, v1: torch.Tensor):
+    """``torch.cat([k0, k1], dim=-2)`` and the same for v, the reference's
+    cache append (dropkv_cache.py:573-578, :583-588, :611-616): a new
+    contiguous [B, H, L0 + L1, D] tensor each, filled by two launches of the
+    library's append kernel, whose non-temporal stores do not leave the copy
+    waiting at its end for dirty cache lines.  The same values as torch.cat;
+    torch.cat itself where the kernel does not apply (tensors off the GPU,
+    mismatched shapes or dtypes, while torch.compile traces)."""
+    ok = (not torch_ops.compiling() and k0.is_cuda and k0.dim() == 4 and k1.dim() == 4
+          and k0.dtype == v0.dtype == k1.dtype == v1.dtype and k0.shape == v0.shape and k1.shape == v1.shape
+          and k0.shape[:2] == k1.shape[:2] and k0.shape[3] == k1.shape[3]
+          and len({k0.device, v0.device, k1.device, v1.device}) == 1)
+    if not ok:
+        return torch.cat([k0, k1], dim=-2), torch.cat([v0, v1], dim=-2)
+    B, H, L0, D = k0.shape
+    k = torch.empty(B, H, L0 + k1.shape[2], D, dtype=k0.dtype, device=k0.device)
+    v = torch.empty_like(k)
+    ops.append(k0, v0, k, v, 0)
+    ops.append(k1, v1, k, v, L0)
+    return k, v
+
+
 class _LayerCache:
     """Per-layer K/V lists with the legacy HF container protocol that the
     reference's ``DropKVCache`` inherits (dropkv_cache.py:104-307): only the
@@ -302,12 +324,12 @@ class DropKVCache(_LayerCache):
 
         # --- decode / chunked-prefill continuation ---
         if self._prefill_mode == "accumulate":
-            self.key_cache[layer_idx] = torch.cat([self.key_cache[layer_idx], key_states], dim=-2)
-            self.value_cache[layer_idx] = torch.cat([self.value_cache[layer_idx], value_states], dim=-2)
+            self.key_cache[layer_idx], self.value_cache[layer_idx] = cat_rows(
+                self.key_cache[layer_idx], self.value_cache[layer_idx], key_states, value_states)
             return self.key_cache[layer_idx], self.value_cache[layer_idx]
         if self._prefill_mode == "evict_accumulated":
-            full_key = torch.cat([self.key_cache[layer_idx], key_states], dim=-2)
-            full_value = torch.cat([self.value_cache[layer_idx], value_states], dim=-2)
+            full_key, full_value = cat_rows(self.key_cache[layer_idx], self.value_cache[layer_idx], key_states,
+                                            value_states)
             if query_states is not None and full_key.shape[2] >= self.window_size:
                 total_tok = self._seen_tokens if self._evict_use_seen_tokens else None
                 key_c, value_c = self._evict_layer(query_states, full_key, full_value, total_tokens=total_tok,
@@ -319,8 +341,8 @@ class DropKVCache(_LayerCache):
                 self.value_cache[layer_idx] = full_value
             return full_key, full_value
         if self._prefill_mode == "single_pass":
-            self.key_cache[layer_idx] = torch.cat([self.key_cache[layer_idx], key_states], dim=-2)
-            self.value_cache[layer_idx] = torch.cat([self.value_cache[layer_idx], value_states], dim=-2)
+            self.key_cache[layer_idx], self.value_cache[layer_idx] = cat_rows(
+                self.key_cache[layer_idx], self.value_cache[layer_idx], key_states, value_states)
             return self.key_cache[layer_idx], self.value_cache[layer_idx]
         raise ValueError(f"Invalid _prefill_mode {self._prefill_mode!r} in decode path")
 

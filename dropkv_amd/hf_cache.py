@@ -29,6 +29,7 @@ import torch
 from transformers.cache_utils import Cache, DynamicLayer
 
 from . import ops, torch_ops
+from .dropkv_cache import cat_rows
 from .dropkv_triton import check_scoring_inputs
 from .hf_query import query_capture, take_captured_query
 
@@ -155,8 +156,7 @@ class DropKVLayer(DynamicLayer):
             return key_states, value_states
 
         self._prefilled = True
-        self.keys = torch.cat([self.keys, key_states], dim=-2)
-        self.values = torch.cat([self.values, value_states], dim=-2)
+        self.keys, self.values = cat_rows(self.keys, self.values, key_states, value_states)
         return self.keys, self.values
 
     def get_seq_length(self) -> int:

@@ -207,3 +207,28 @@ def test_guards_on_device(gpu):
         dropkv_scores_triton(Q[:, :, :32], K[:, :, :32].contiguous(), V)
     Qn = Q.transpose(2, 3).contiguous().transpose(2, 3)
     assert dropkv_scores_triton(Qn, K, V).shape == (1, 8, 64)
+
+
+@pytest.mark.parametrize("dtype,L0,L1,D,strided", [
+    (torch.bfloat16, 6553, 4096, 128, False),   # the C3 continuation: stored rows || chunk
+    (torch.float16, 0, 300, 64, False),          # nothing stored yet
+    (torch.bfloat16, 1638, 1, 64, True),         # one decode row, inputs as transposed projections
+    (torch.float32, 77, 5, 80, False),           # fp32 rows, D not a multiple of 16 bytes' elements
+])
+def test_cat_rows_equals_torch_cat(gpu, dtype, L0, L1, D, strided):
+    """The continuation's append (dropkv_cache.py:573-588, :611-616) through
+    the library's append kernel gives torch.cat's tensors bit for bit."""
+    from dropkv_amd.dropkv_cache import cat_rows
+    g = torch.Generator(device=gpu).manual_seed(L0 + L1 + D)
+    B, H = 2, 3
+
+    def draw(L):
+        if strided:   # [B, L, H, D] viewed as [B, H, L, D]
+            return torch.randn(B, L, H, D, device=gpu, generator=g).to(dtype).transpose(1, 2)
+        return torch.randn(B, H, L, D, device=gpu, generator=g).to(dtype)
+
+    k0, v0, k1, v1 = draw(L0), draw(L0), draw(L1), draw(L1)
+    k, v = cat_rows(k0, v0, k1, v1)
+    rk, rv = torch.cat([k0, k1], dim=-2), torch.cat([v0, v1], dim=-2)
+    assert k.is_contiguous() and v.is_contiguous() and k.shape == rk.shape
+    assert torch.equal(k, rk) and torch.equal(v, rv)
