@@ -432,3 +432,15 @@ def test_capacity_prefill_keep_above_capacity_raises():
     c = DropKVCache(keep_ratio=0.9, capacity=200)
     with pytest.raises(ValueError, match="capacity of 200 rows exceeded at layer 0: 230 rows needed"):
         c.update(Q, K, V, layer_idx=0)
+
+
+def test_cat_rows_falls_back_to_torch_cat_off_the_gpu():
+    """Off the GPU (and for shapes the append kernel does not take) the
+    continuation's append is torch.cat itself, so host flows keep the
+    reference's tensors."""
+    from dropkv_amd.dropkv_cache import cat_rows
+    g = torch.Generator().manual_seed(0)
+    k0, v0 = torch.randn(1, 2, 5, 8, generator=g), torch.randn(1, 2, 5, 8, generator=g)
+    k1, v1 = torch.randn(1, 2, 3, 8, generator=g), torch.randn(1, 2, 3, 8, generator=g)
+    k, v = cat_rows(k0, v0, k1, v1)
+    assert torch.equal(k, torch.cat([k0, k1], dim=-2)) and torch.equal(v, torch.cat([v0, v1], dim=-2))
