@@ -775,10 +775,7 @@ pass2_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld,
         if (lg == 0 && n < k_end) {
           float* dst = scores + (int64_t)head * Lk + n;
           if (!first) v += *dst;
-          if (last)
-            __builtin_nontemporal_store(v * out_scale, dst);
-          else
-            *dst = v;
+          *dst = last ? v * out_scale : v;
           if (last && fz.sc_lds) sc_row[n - k_begin] = v * out_scale;
         }
       }
@@ -1057,7 +1054,7 @@ pass2w_kernel(const T* __restrict__ kp, const T* __restrict__ vp, int kv_ld, int
       for (int w = 1; w < n_mc; ++w) v += red[buf][w][tid];
       const int n = k_begin + it * kTile + tid % kTile;
       if (it < ntiles && n < k_end) {
-        __builtin_nontemporal_store(v * out_scale, &scores[(int64_t)head * Lk + n]);
+        scores[(int64_t)head * Lk + n] = v * out_scale;
         if (sc_lds) sc_row[n - k_begin] = v * out_scale;
       }
     }
