@@ -23,7 +23,8 @@ the CPU oracle.
   against the float64 evaluation (ties excused) and against the float32
   reference (ties and undecided indices excused); every row's selection
   against the oracle's pool / protect / rank rule on the GPU scores, every
-  gather bit for bit.
+  gather bit for bit; the same call with fp16 inputs, two of its rows
+  against the oracle.
 """
 
 import pytest
@@ -266,28 +267,71 @@ def test_c5_stress_rows(c5_run, group):
     exact ties excused, and at 0.999 against the float32 reference with
     ties and the indices its own rounding leaves undecided excused."""
     c = c5_run
-    W, ks, ratio, keep, g = c["W"], c["ks"], c["ratio"], c["keep"], c["g"]
+    g = c["g"]
     per = len(C5_ROWS) // C5_GROUPS
     for b, h in C5_ROWS[group * per:(group + 1) * per]:
-        qh = c["Qt"][b:b + 1, h * g:(h + 1) * g]
-        kh, vh = c["K"][b:b + 1, h:h + 1], c["V"][b:b + 1, h:h + 1]
-        got = c["s"][b:b + 1, h:h + 1]
-        mine = c["idx"][b:b + 1, h:h + 1]
-        r32 = R.dropkv_scores_reference(qh, kh, vh, W, match_pytorch_precision=True)
-        s64, lo, hi = R.dropkv_score_bracket(qh, kh, vh, W, p_round=torch.bfloat16)
-        gd = got.double()
-        far = torch.where(gd < lo, lo - gd, torch.where(gd > hi, gd - hi, torch.zeros_like(gd)))
-        assert (far <= 1e-3 + 2e-2 * s64.abs()).all(), ((b, h), torch.nonzero(far.flatten() > 0)[:8].flatten().tolist())
-        ref_idx, rp = R.compute_keep_indices(qh, kh, vh, ratio, W, ks, scores=r32)
-        stats = assert_binding_scores(got, r32, rp, keep, qh, kh, vh, W, torch.bfloat16, 2e-2, 1e-3, 1e-3,
-                                      bracket=(s64, lo, hi))
-        idx64, p64 = R.compute_keep_indices(qh, kh, vh, ratio, W, ks, scores=s64)
-        worst64, counted64 = R.index_overlap(mine, idx64, p64)
-        und = R.selection_band(lo, hi, ks, W, keep)
-        worst, counted, n_tie, n_band = R.index_overlap(mine, ref_idx, rp, undecided=und, return_counts=True)
-        print(f"[c5] row (b={b}, h={h}): binding keys {stats[0]}, worst rel {stats[1]:.2e}, beyond 1e-3 {stats[2]}, "
-              f"sinks {stats[3]}; vs fp32 reference: overlap {worst:.4f}, counted {counted}, ties {n_tie}, "
-              f"band {n_band} (band size {int(und.sum())}); vs float64: overlap {worst64:.4f}, counted {counted64}",
-              flush=True)
-        assert worst64 >= 0.999, ((b, h), worst64, counted64)
-        assert worst >= 0.999, ((b, h), worst, counted, n_tie, n_band)
+        _c5_check_row((b, h), c["Qt"][b:b + 1, h * g:(h + 1) * g], c["K"][b:b + 1, h:h + 1],
+                      c["V"][b:b + 1, h:h + 1], c["s"][b:b + 1, h:h + 1], c["idx"][b:b + 1, h:h + 1],
+                      c["W"], c["ks"], c["ratio"], c["keep"], torch.bfloat16)
+
+
+def _c5_check_row(bh, qh, kh, vh, got, mine, W, ks, ratio, keep, p_round):
+    """The per-row checks of a C5 call against the oracle, on one (b, hkv)
+    row's host tensors (p rounded to ``p_round``): the scores against the
+    float64 brackets and on the binding keys, the selection against the
+    float64 evaluation and the float32 reference."""
+    b, h = bh
+    r32 = R.dropkv_scores_reference(qh, kh, vh, W, match_pytorch_precision=True)
+    s64, lo, hi = R.dropkv_score_bracket(qh, kh, vh, W, p_round=p_round)
+    gd = got.double()
+    far = torch.where(gd < lo, lo - gd, torch.where(gd > hi, gd - hi, torch.zeros_like(gd)))
+    assert (far <= 1e-3 + 2e-2 * s64.abs()).all(), ((b, h), torch.nonzero(far.flatten() > 0)[:8].flatten().tolist())
+    ref_idx, rp = R.compute_keep_indices(qh, kh, vh, ratio, W, ks, scores=r32)
+    stats = assert_binding_scores(got, r32, rp, keep, qh, kh, vh, W, p_round, 2e-2, 1e-3, 1e-3,
+                                  bracket=(s64, lo, hi))
+    idx64, p64 = R.compute_keep_indices(qh, kh, vh, ratio, W, ks, scores=s64)
+    worst64, counted64 = R.index_overlap(mine, idx64, p64)
+    und = R.selection_band(lo, hi, ks, W, keep)
+    worst, counted, n_tie, n_band = R.index_overlap(mine, ref_idx, rp, undecided=und, return_counts=True)
+    print(f"[c5 {str(p_round)[6:]}] row (b={b}, h={h}): binding keys {stats[0]}, worst rel {stats[1]:.2e}, "
+          f"beyond 1e-3 {stats[2]}, sinks {stats[3]}; vs fp32 reference: overlap {worst:.4f}, counted {counted}, "
+          f"ties {n_tie}, band {n_band} (band size {int(und.sum())}); vs float64: overlap {worst64:.4f}, "
+          f"counted {counted64}", flush=True)
+    assert worst64 >= 0.999, ((b, h), worst64, counted64)
+    assert worst >= 0.999, ((b, h), worst, counted, n_tie, n_band)
+
+
+def test_c5_fp16_call_and_two_rows(gpu):
+    """The C5 layer-call with fp16 inputs (p rounded to fp16 before the
+    weight, dropkv_triton.py:88-93): the full query tensor with every row
+    outside the tail NaN; every row's selection against the oracle's rule on
+    the GPU scores and every gather bit for bit; two (b, hkv) rows against
+    the oracle as in the bf16 tests."""
+    from dropkv_amd import ops
+    B, Hq, Hkv, D, L, W, ks, ratio = 4, 64, 8, 128, 131072, 32, 11, 0.05
+    keep = R.keep_length(ratio, L, W)
+    gen = torch.Generator(device=gpu).manual_seed(7)
+    Qt = torch.randn(B, Hq, W, D, generator=gen, device=gpu).half()
+    K = _student_t3((B, Hkv, L, D), gen, gpu).half()
+    V = torch.randn(B, Hkv, L, D, generator=gen, device=gpu).half()
+    assert torch.isfinite(K).all()
+    Q = torch.full((B, Hq, L, D), float("nan"), dtype=torch.float16, device=gpu)
+    Q[:, :, -W:] = Qt
+    print("[c5 fp16] layer-call", flush=True)
+    plan = ops.EvictPlan(Q, K, W, ks, keep, keep_scores=True)
+    idx, kc, vc = plan(Q, K, V)
+    s = plan.scores.cpu()
+    assert torch.isfinite(s).all() and (s >= 0).all()
+    pooled = R.pool_protect(s.clone(), ks, W)
+    assert torch.equal(idx.cpu(), R.topk_sorted(pooled, keep))
+    gk, gv = R.gather_compressed(K, V, idx)
+    assert torch.equal(kc, gk) and torch.equal(vc, gv)
+    del Q, plan, kc, vc, gk, gv
+    g = Hq // Hkv
+    idx = idx.cpu()
+    for b, h in [(1, 2), (3, 6)]:
+        _c5_check_row((b, h), Qt[b:b + 1, h * g:(h + 1) * g].cpu(), K[b:b + 1, h:h + 1].cpu(),
+                      V[b:b + 1, h:h + 1].cpu(), s[b:b + 1, h:h + 1], idx[b:b + 1, h:h + 1], W, ks, ratio, keep,
+                      torch.float16)
+    del K, V
+    _free()
