@@ -39,8 +39,10 @@ def cat_rows(k0: torch.Tensor, v0: torch.Tensor, k1: torch.Tensor, v1: torch.Ten
     library's append kernel, whose non-temporal stores do not leave the copy
     waiting at its end for dirty cache lines.  The same values as torch.cat;
     torch.cat itself where the kernel does not apply (tensors off the GPU,
-    mismatched shapes or dtypes, while torch.compile traces)."""
-    ok = (not torch_ops.compiling() and k0.is_cuda and k0.dim() == 4 and k1.dim() == 4
+    mismatched shapes or dtypes, while torch.compile traces, or where autograd
+    would record the op)."""
+    grad = torch.is_grad_enabled() and any(t.requires_grad for t in (k0, v0, k1, v1))
+    ok = (not grad and not torch_ops.compiling() and k0.is_cuda and k0.dim() == 4 and k1.dim() == 4
           and k0.dtype == v0.dtype == k1.dtype == v1.dtype and k0.shape == v0.shape and k1.shape == v1.shape
           and k0.shape[:2] == k1.shape[:2] and k0.shape[3] == k1.shape[3]
           and len({k0.device, v0.device, k1.device, v1.device}) == 1)

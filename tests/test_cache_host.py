@@ -444,3 +444,6 @@ def test_cat_rows_falls_back_to_torch_cat_off_the_gpu():
     k1, v1 = torch.randn(1, 2, 3, 8, generator=g), torch.randn(1, 2, 3, 8, generator=g)
     k, v = cat_rows(k0, v0, k1, v1)
     assert torch.equal(k, torch.cat([k0, k1], dim=-2)) and torch.equal(v, torch.cat([v0, v1], dim=-2))
+    # inputs autograd tracks keep torch.cat's graph
+    k, v = cat_rows(k0.requires_grad_(), v0, k1, v1)
+    assert k.grad_fn is not None
