@@ -2,7 +2,10 @@
 // dropkv_cache.py:479-491) and its two-segment form for the chunked-prefill
 // continuation (dropkv_cache.py:581-607).  Bit copies in 16-byte pieces when
 // the row allows it, element copies otherwise.  Indices outside [0, L) are
-// not dereferenced; their output rows are zero-filled.
+// not dereferenced; their output rows are zero-filled.  Outputs are written
+// with non-temporal stores: a short copy kernel that leaves its output dirty
+// in the L2 waits at its end for the write-back (a 16 MB append took 20 us
+// with plain stores against 5 us).
 #include "dkv_common.h"
 #include "dkv_internal.h"
 
